@@ -1,0 +1,179 @@
+#!/usr/bin/env python3
+"""Headline benchmark: Qwen3-30B-A3B-shaped bf16 decode at batch 1 on one MI355X.
+
+    python bench.py [--gpus 1] [--steps 32] [--warmup 4] [--ctx 1024] [--no-cpu] [--unfused]
+
+Setup (untimed): seeded random-init weights N(0, 0.02) in HBM, a prompt of `ctx` seeded random token ids fed
+token by token through the decode step (as examples/llm/host.hip:203-213 does), then `warmup` greedy steps.
+Timed: `steps` greedy decode steps (one persistent megakernel launch each), bracketed by synchronisation and
+HIP events on the launch stream.  One JSON line on stdout; progress on stderr.
+
+Bytes per token follow the reference's ledger rules (etx/models/vllm_llm/byte_ledger.py:121-178): every
+non-expert weight once, the TOPK active experts, the KV cache read over the context plus one position written.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (str(ROOT), str(ROOT / "etx-megakernel_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "decode ms/token at batch 1, Qwen3-30B-A3B shape; achieved HBM GB/s vs peak"
+HBM_PEAK_GBPS = 8000.0
+REFERENCE_MI300X_MS = 4.087415          # docs/qwen/QWEN-BATCH-BASELINE-2026-10-18.md:17 (MI300X, not comparable hardware)
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def bytes_per_token(cfg, context: int) -> dict:
+    """Algorithmic HBM bytes of one decode step at `context` cached positions."""
+    H, HD, NH, NKV, V = cfg.H, cfg.HD, cfg.NH, cfg.NKV, cfg.V
+    bf = 2
+    glob = (H + H + V * H) * bf                     # embedding row, final norm, lm_head
+    layer = (2 * H + 2 * HD) * bf                   # ln1, ln2, q/k norm
+    layer += ((NH + 2 * NKV) * HD * H + H * NH * HD) * bf
+    if cfg.moe:
+        layer += (cfg.E * H + cfg.TOPK * 3 * cfg.MI * H) * bf
+    else:
+        layer += 3 * cfg.I * H * bf
+    kv_pos = 2 * NKV * HD * bf
+    kv = cfg.L * (context * kv_pos + kv_pos)
+    weights = glob + cfg.L * layer
+    return {"weights": weights, "kv": kv, "total": weights + kv}
+
+
+def cpu_baseline(cfg, ctx: int, seed: int) -> dict:
+    """The CPU oracle on a bounded sample of the same workload: two real-shape layers plus the full head at
+    context `ctx`, scaled to the model's layer count."""
+    import numpy as np
+    from oracle import oracle as O
+    from etx.models.configs import with_layers
+    sample = with_layers(cfg, 2)
+    t0 = time.time()
+    m = O.OracleModel(sample.as_dict(), seed, 0.02)
+    m.materialize_experts()
+    m.fill_kv_random(ctx)
+    log(f"[cpu] oracle sample built in {time.time() - t0:.1f}s ({O.num_threads()} threads)")
+    x = O.bf16_bits_to_f32(O.gen_normal_bf16(seed, O.stream_id(O.S_XIN, -1), cfg.H, scale=1.0))
+    reps = 3
+    t1 = time.time()
+    for r in range(reps):
+        for l in range(2):
+            x, _, _, _ = m.layer_step(l, x, ctx + r)
+    t_layers = (time.time() - t1) / reps                     # two layers
+    t2 = time.time()
+    for r in range(reps):
+        m.step(int(r), ctx + reps + r)
+    t_step = (time.time() - t2) / reps                       # embed + two layers + head
+    t_head = max(t_step - t_layers, 0.0)
+    ms = (t_head + t_layers * cfg.L / 2) * 1e3
+    m.close()
+    import platform
+    return {"value": round(ms, 3), "unit": "ms/token", "cores": O.num_threads(), "kind": "port",
+            "sample": f"CPU oracle (C, OpenMP), {reps} decode steps of 2 real-shape layers + lm_head at context {ctx}; "
+                      f"ms/token = head + {cfg.L}/2 x two-layer time ({platform.processor() or platform.machine()})",
+            "tokens_per_s": round(1e3 / ms, 3), "effective_GBps": round(bytes_per_token(cfg, ctx)["total"] / ms / 1e6, 2)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=32)
+    ap.add_argument("--warmup", type=int, default=4)
+    ap.add_argument("--ctx", type=int, default=1024)
+    ap.add_argument("--seed", type=int, default=20261201)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--unfused", action="store_true")
+    ap.add_argument("--workgroups", type=int, default=0)
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py: this build runs on exactly one GPU (asked for {a.gpus}); multi-GPU sharding is a design "
+              f"note only", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+    from etx.runtime import native as N
+    from etx.models import configs
+
+    cfg = configs.QWEN3_30B_A3B
+    if a.ctx + a.warmup + a.steps + 1 > cfg.max_ctx:
+        raise SystemExit(f"ctx {a.ctx} + warmup + steps exceeds max_ctx {cfg.max_ctx}")
+    dev = torch.device("cuda:0")
+    t0 = time.time()
+    dec = N.Decoder(cfg, device="cuda:0", fused=not a.unfused, workgroups=a.workgroups)
+    dec.init_weights(a.seed, 0.02)
+    torch.cuda.synchronize()
+    log(f"[gpu] weights {dec.sizes['weights'] / 1e9:.2f} GB initialised in {time.time() - t0:.1f}s; "
+        f"{dec.barriers_per_step()} grid barriers per step")
+    prompt = np.random.default_rng(a.seed).integers(0, cfg.V, a.ctx).astype(np.int32)
+    dec.set_tokens(prompt)
+    t1 = time.time()
+    for pos in range(a.ctx):
+        dec.step(pos, write_next=pos + 1 >= a.ctx)
+        if pos % 256 == 255:
+            dec.sync()
+            log(f"[gpu] prefill {pos + 1}/{a.ctx} ({(time.time() - t1) / (pos + 1) * 1e3:.3f} ms/token)")
+    dec.sync()
+    pos = a.ctx
+    for _ in range(a.warmup):
+        dec.step(pos, write_next=True)
+        pos += 1
+    dec.sync()
+    stream = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    w0 = time.perf_counter()
+    e0.record(stream)
+    first_timed = pos
+    for _ in range(a.steps):
+        dec.step(pos, write_next=True)
+        pos += 1
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - w0) * 1e3
+    dec.sync()
+    ms = e0.elapsed_time(e1) / a.steps
+    toks = dec.read_tokens(pos)
+    ctx_mean = (first_timed + pos - 1) / 2.0
+    b = bytes_per_token(cfg, int(round(ctx_mean)))
+    gbps = b["total"] / (ms * 1e-3) / 1e9
+    log(f"[gpu] {a.steps} steps: {ms:.4f} ms/token (events), host wall {wall / a.steps:.4f} ms/token, "
+        f"{gbps:.1f} GB/s = {gbps / HBM_PEAK_GBPS:.3f} of 8 TB/s; last tokens {list(toks[-4:])}")
+    out = {
+        "metric": METRIC, "value": round(ms, 4), "unit": "ms/token", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: seeded random-init bf16 weights N(0,0.02); prompt of seeded uniform token ids",
+        "config": {"workload": f"{cfg.name} decode, batch 1, context {a.ctx} (+{a.warmup} warmup), greedy "
+                               f"(BASELINE.json configs[2])",
+                   "batch": 1, "context": a.ctx, "layers": cfg.L, "experts": cfg.E, "top_k": cfg.TOPK,
+                   "vocab": cfg.V, "mode": "unfused" if a.unfused else "fused megakernel",
+                   "workgroups": a.workgroups or "one per CU", "seed": a.seed},
+        "tokens_per_s": round(1e3 / ms, 2), "host_wall_ms_per_token": round(wall / a.steps, 4),
+        "bytes_per_token": b["total"], "achieved_GBps": round(gbps, 1),
+        "reference_mi300x_ms_per_token": REFERENCE_MI300X_MS,
+        "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "kernel": "etxmk_fused" if not a.unfused else "etxmk_phase (all phases)"},
+        "cpu_baseline": None,
+    }
+    if not a.no_cpu:
+        try:
+            out["cpu_baseline"] = cpu_baseline(cfg, a.ctx, a.seed)
+        except Exception as e:  # the baseline is reported, never gating
+            log(f"[cpu] baseline failed: {e!r}")
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,521 @@
+// Host side of the etxmk C ABI (include/etxmk.h): arena layout, seeded initialisation, launches.
+//
+// Reference counterparts: etx_host (etx/runtime/include/etx/host.h:22-692) for setup / run / wait, and the model
+// hosts examples/llm/host.hip:57-244 and examples/vllm_llm/host.hip:126-1159 for buffers and per-step parameters.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <initializer_list>
+#include <vector>
+
+#include "etxmk.h"
+#include "mk_device.h"
+
+using namespace mk;
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+#define HIPCHK(call)                                                                       \
+  do {                                                                                     \
+    hipError_t e_ = (call);                                                                \
+    if (e_ != hipSuccess) return fail(ETXMK_EHIP, "%s: %s", #call, hipGetErrorString(e_)); \
+  } while (0)
+
+constexpr uint64_t ALIGN = 256;
+inline uint64_t align_up(uint64_t v) { return (v + ALIGN - 1) & ~(ALIGN - 1); }
+
+struct TensorSlot {
+  int kind, layer;
+  int count;                 // tensors of this shape back to back (experts)
+  int rows, cols, perm;      // perm: rows stored lane-permuted
+  uint64_t off;              // byte offset of tensor 0
+};
+
+inline uint64_t stream_id(int kind, int layer, int expert) {
+  return ((uint64_t)kind << 48) | ((uint64_t)(layer + 1) << 24) | (uint64_t)expert;
+}
+
+// row lengths each GEMV phase is instantiated for (MK_K_* in mk_device.h)
+bool k_in(int k, std::initializer_list<int> ks) {
+  for (int v : ks)
+    if (k == v) return true;
+  return false;
+}
+
+int check_config(const etxmk_config* c) {
+  if (!c) return fail(ETXMK_EINVAL, "config is NULL");
+  if (c->H <= 0 || c->NH <= 0 || c->NKV <= 0 || c->L <= 0 || c->V <= 0) return fail(ETXMK_EINVAL, "non-positive dimension");
+  if (c->HD != HDIM) return fail(ETXMK_EINVAL, "head_dim %d unsupported (the attention phase is built for %d)", c->HD, HDIM);
+  if (c->NH % c->NKV) return fail(ETXMK_EINVAL, "NH %d not a multiple of NKV %d", c->NH, c->NKV);
+  if (c->H > MAX_H || !k_in(c->H, {MK_K_HIDDEN})) return fail(ETXMK_EINVAL, "hidden size %d unsupported", c->H);
+  if (!k_in(c->NH * c->HD, {MK_K_ATTN})) return fail(ETXMK_EINVAL, "NH*HD %d unsupported", c->NH * c->HD);
+  if (c->batch != 1) return fail(ETXMK_EINVAL, "batch %d unsupported (batch 1 only)", c->batch);
+  if (c->block_size <= 0 || CHUNK % c->block_size) return fail(ETXMK_EINVAL, "block size %d must divide %d", c->block_size, CHUNK);
+  if (c->max_ctx <= 0 || c->max_ctx > MAX_CTX) return fail(ETXMK_EINVAL, "max_ctx %d outside 1..%d", c->max_ctx, MAX_CTX);
+  if (c->moe) {
+    if (c->E <= 0 || c->E > MAX_E || c->TOPK <= 0 || c->TOPK > MAX_TOPK || c->TOPK > c->E)
+      return fail(ETXMK_EINVAL, "experts %d / top-k %d unsupported", c->E, c->TOPK);
+    if (!k_in(c->MI, {MK_K_MOE}) || c->TOPK * c->MI > MAX_K) return fail(ETXMK_EINVAL, "moe intermediate %d unsupported", c->MI);
+  } else {
+    if (!k_in(c->I, {MK_K_INTER}) || c->I > MAX_K) return fail(ETXMK_EINVAL, "intermediate %d unsupported", c->I);
+  }
+  return ETXMK_OK;
+}
+
+// Weight arena: every tensor 256-byte aligned, experts of one layer contiguous.
+std::vector<TensorSlot> weight_layout(const etxmk_config* c, uint64_t* total) {
+  std::vector<TensorSlot> v;
+  uint64_t off = 0;
+  auto add = [&](int kind, int layer, int count, int rows, int cols, int perm) {
+    v.push_back({kind, layer, count, rows, cols, perm, off});
+    off = align_up(off + (uint64_t)count * rows * cols * 2);
+  };
+  const int NQKV = (c->NH + 2 * c->NKV) * c->HD;
+  add(ETXMK_T_EMBED, -1, 1, c->V, c->H, 0);
+  add(ETXMK_T_LMHEAD, -1, 1, c->V, c->H, 1);
+  add(ETXMK_T_FINAL_NORM, -1, 1, 1, c->H, 0);
+  for (int l = 0; l < c->L; ++l) {
+    add(ETXMK_T_LN1, l, 1, 1, c->H, 0);
+    add(ETXMK_T_LN2, l, 1, 1, c->H, 0);
+    add(ETXMK_T_QNORM, l, 1, 1, c->HD, 0);
+    add(ETXMK_T_KNORM, l, 1, 1, c->HD, 0);
+    add(ETXMK_T_WQKV, l, 1, NQKV, c->H, 1);
+    add(ETXMK_T_WO, l, 1, c->H, c->NH * c->HD, 1);
+    if (c->moe) {
+      add(ETXMK_T_ROUTER, l, 1, c->E, c->H, 1);
+      add(ETXMK_T_W13, l, c->E, 2 * c->MI, c->H, 1);
+      add(ETXMK_T_W2, l, c->E, c->H, c->MI, 1);
+    } else {
+      add(ETXMK_T_WGU, l, 1, 2 * c->I, c->H, 1);
+      add(ETXMK_T_WD, l, 1, c->H, c->I, 1);
+    }
+  }
+  *total = off;
+  return v;
+}
+
+int nblocks_of(const etxmk_config* c) { return (c->max_ctx + c->block_size - 1) / c->block_size; }
+
+uint64_t kv_layer_elems(const etxmk_config* c) { return (uint64_t)nblocks_of(c) * c->block_size * c->NKV * c->HD; }
+
+struct WsLayout {
+  uint64_t x, qkv, o, logits, hbuf, amax, bar, abort_w, tokens, out_tokens, btab, rcos, rsin, layers, total;
+};
+
+WsLayout ws_layout(const etxmk_config* c) {
+  WsLayout w{};
+  uint64_t off = 0;
+  auto take = [&](uint64_t bytes) { const uint64_t o = off; off = align_up(off + bytes); return o; };
+  const int NQKV = (c->NH + 2 * c->NKV) * c->HD;
+  w.x = take(4ull * c->H);
+  w.qkv = take(4ull * NQKV);
+  w.o = take(4ull * c->NH * c->HD);
+  w.logits = take(4ull * (c->E > 0 ? c->E : 1));
+  const int hb = c->moe ? c->TOPK * c->MI : c->I;
+  w.hbuf = take(4ull * (hb > 0 ? hb : 1));
+  w.amax = take(8);
+  w.bar = take(4);
+  w.abort_w = take(4);
+  w.tokens = take(4ull * (c->max_ctx + 1));
+  w.out_tokens = take(4ull * (c->max_ctx + 1));
+  w.btab = take(4ull * nblocks_of(c));
+  w.rcos = take(4ull * c->max_ctx * (c->HD / 2));
+  w.rsin = take(4ull * c->max_ctx * (c->HD / 2));
+  w.layers = take(sizeof(LayerW) * (uint64_t)c->L);
+  w.total = off;
+  return w;
+}
+
+}  // namespace
+
+struct etxmk_handle {
+  etxmk_config c;
+  std::vector<TensorSlot> slots;
+  uint64_t wbytes = 0;
+  WsLayout ws{};
+  uint8_t* w = nullptr;
+  uint8_t* kv = nullptr;
+  uint8_t* wsp = nullptr;
+  int fused = 1;
+  int nwg = 0;
+  int ncu = 0;
+  uint32_t bar_epoch = 0;
+  float* dump_x = nullptr;
+  int32_t* dump_ids = nullptr;
+  float* dump_wts = nullptr;
+  float* dump_logits = nullptr;
+  std::vector<int32_t> btab_host;
+
+  const TensorSlot* slot(int kind, int layer) const {
+    for (const auto& s : slots)
+      if (s.kind == kind && s.layer == layer) return &s;
+    return nullptr;
+  }
+  template <class T> T* wsptr(uint64_t off) const { return (T*)(wsp + off); }
+  const uint16_t* wt(int kind, int layer) const {
+    const TensorSlot* s = slot(kind, layer);
+    return s ? (const uint16_t*)(w + s->off) : nullptr;
+  }
+  int barriers(int l0, int l1, int head) const { return (c.moe ? 6 : 5) * (l1 - l0) + (head ? 1 : 0); }
+};
+
+extern "C" {
+
+int etxmk_abi_version(void) { return ETXMK_ABI_VERSION; }
+const char* etxmk_last_error(void) { return g_err; }
+
+int etxmk_weight_bytes(const etxmk_config* cfg, uint64_t* bytes) {
+  if (int r = check_config(cfg)) return r;
+  if (!bytes) return fail(ETXMK_EINVAL, "bytes is NULL");
+  weight_layout(cfg, bytes);
+  return ETXMK_OK;
+}
+
+int etxmk_kv_bytes(const etxmk_config* cfg, uint64_t* bytes) {
+  if (int r = check_config(cfg)) return r;
+  if (!bytes) return fail(ETXMK_EINVAL, "bytes is NULL");
+  *bytes = 2ull * 2ull * kv_layer_elems(cfg) * (uint64_t)cfg->L;
+  return ETXMK_OK;
+}
+
+int etxmk_workspace_bytes(const etxmk_config* cfg, uint64_t* bytes) {
+  if (int r = check_config(cfg)) return r;
+  if (!bytes) return fail(ETXMK_EINVAL, "bytes is NULL");
+  *bytes = ws_layout(cfg).total;
+  return ETXMK_OK;
+}
+
+int etxmk_create(const etxmk_config* cfg, etxmk_handle** out) {
+  if (int r = check_config(cfg)) return r;
+  if (!out) return fail(ETXMK_EINVAL, "out is NULL");
+  etxmk_handle* h = new etxmk_handle();
+  h->c = *cfg;
+  h->slots = weight_layout(cfg, &h->wbytes);
+  h->ws = ws_layout(cfg);
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&h->ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+    delete h;
+    return fail(ETXMK_EHIP, "no HIP device");
+  }
+  h->nwg = h->ncu;
+  *out = h;
+  return ETXMK_OK;
+}
+
+int etxmk_destroy(etxmk_handle* h) {
+  delete h;
+  return ETXMK_OK;
+}
+
+int etxmk_bind(etxmk_handle* h, void* weights, void* kv, void* workspace) {
+  if (!h || !weights || !kv || !workspace) return fail(ETXMK_EINVAL, "NULL handle or buffer");
+  if (((uintptr_t)weights | (uintptr_t)kv | (uintptr_t)workspace) & (ALIGN - 1))
+    return fail(ETXMK_EINVAL, "buffers must be %llu-byte aligned", (unsigned long long)ALIGN);
+  h->w = (uint8_t*)weights;
+  h->kv = (uint8_t*)kv;
+  h->wsp = (uint8_t*)workspace;
+  const etxmk_config& c = h->c;
+  // per-layer pointer table
+  std::vector<LayerW> lw(c.L);
+  const uint64_t kvl = kv_layer_elems(&c);
+  for (int l = 0; l < c.L; ++l) {
+    LayerW& y = lw[l];
+    y.ln1 = h->wt(ETXMK_T_LN1, l);
+    y.ln2 = h->wt(ETXMK_T_LN2, l);
+    y.qn = h->wt(ETXMK_T_QNORM, l);
+    y.kn = h->wt(ETXMK_T_KNORM, l);
+    y.wqkv = h->wt(ETXMK_T_WQKV, l);
+    y.wo = h->wt(ETXMK_T_WO, l);
+    y.wr = h->wt(ETXMK_T_ROUTER, l);
+    y.w13 = h->wt(ETXMK_T_W13, l);
+    y.w2 = h->wt(ETXMK_T_W2, l);
+    y.wgu = h->wt(ETXMK_T_WGU, l);
+    y.wd = h->wt(ETXMK_T_WD, l);
+    y.kc = (uint16_t*)h->kv + (uint64_t)l * 2 * kvl;
+    y.vc = y.kc + kvl;
+  }
+  HIPCHK(hipMemcpy(h->wsp + h->ws.layers, lw.data(), sizeof(LayerW) * c.L, hipMemcpyHostToDevice));
+  // RoPE tables, bf16 values in fp32 (ref_numpy.py:76-81; host.hip:164-178)
+  const int half = c.HD / 2;
+  std::vector<float> cs((size_t)c.max_ctx * half), sn((size_t)c.max_ctx * half);
+  for (int i = 0; i < half; ++i) {
+    const float inv = 1.0f / powf(c.theta, (float)(2 * i) / (float)c.HD);
+    for (int t = 0; t < c.max_ctx; ++t) {
+      const float f = (float)t * inv;
+      auto rb = [](float x) { uint32_t u; memcpy(&u, &x, 4); u = (u + 0x7FFFu + ((u >> 16) & 1u)) & 0xFFFF0000u; float r; memcpy(&r, &u, 4); return r; };
+      cs[(size_t)t * half + i] = rb(cosf(f));
+      sn[(size_t)t * half + i] = rb(sinf(f));
+    }
+  }
+  HIPCHK(hipMemcpy(h->wsp + h->ws.rcos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice));
+  HIPCHK(hipMemcpy(h->wsp + h->ws.rsin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice));
+  // identity block table, counters and token buffers cleared
+  h->btab_host.resize(nblocks_of(&c));
+  for (int i = 0; i < (int)h->btab_host.size(); ++i) h->btab_host[i] = i;
+  HIPCHK(hipMemcpy(h->wsp + h->ws.btab, h->btab_host.data(), h->btab_host.size() * 4, hipMemcpyHostToDevice));
+  HIPCHK(hipMemset(h->wsp + h->ws.bar, 0, 4));
+  HIPCHK(hipMemset(h->wsp + h->ws.abort_w, 0, 4));
+  HIPCHK(hipMemset(h->wsp + h->ws.tokens, 0, 4ull * (c.max_ctx + 1)));
+  HIPCHK(hipMemset(h->wsp + h->ws.out_tokens, 0, 4ull * (c.max_ctx + 1)));
+  HIPCHK(hipMemset(h->wsp + h->ws.x, 0, 4ull * c.H));
+  h->bar_epoch = 0;
+  return ETXMK_OK;
+}
+
+int etxmk_tensor_info(etxmk_handle* h, int kind, int layer, int expert, uint64_t* offset, int32_t* rows, int32_t* cols,
+                      int32_t* permuted) {
+  if (!h) return fail(ETXMK_EINVAL, "NULL handle");
+  const bool global = kind == ETXMK_T_EMBED || kind == ETXMK_T_LMHEAD || kind == ETXMK_T_FINAL_NORM;
+  const TensorSlot* s = h->slot(kind, global ? -1 : layer);
+  if (!s) return fail(ETXMK_EINVAL, "no tensor kind %d layer %d", kind, layer);
+  if (expert < 0 || expert >= s->count) return fail(ETXMK_EINVAL, "expert %d outside 0..%d", expert, s->count - 1);
+  if (offset) *offset = s->off + (uint64_t)expert * s->rows * s->cols * 2;
+  if (rows) *rows = s->rows;
+  if (cols) *cols = s->cols;
+  if (permuted) *permuted = s->perm;
+  return ETXMK_OK;
+}
+
+int etxmk_init_weights_seeded(etxmk_handle* h, uint64_t seed, float scale, void* stream) {
+  if (!h || !h->w) return fail(ETXMK_EUNBOUND, "handle not bound");
+  hipStream_t st = (hipStream_t)stream;
+  for (const TensorSlot& s : h->slots) {
+    uint16_t* dst = (uint16_t*)(h->w + s.off);
+    const size_t n = (size_t)s.count * s.rows * s.cols;
+    const bool norm = s.kind >= ETXMK_T_LN1;
+    if (norm) {
+      hipLaunchKernelGGL(etxmk_fill_u16, dim3(64), dim3(256), 0, st, dst, n, (uint16_t)0x3F80);
+    } else {
+      if (n % 8) return fail(ETXMK_EINVAL, "tensor kind %d has %zu elements (not a multiple of 8)", s.kind, n);
+      const size_t blocks = (n / 8 + 255) / 256;
+      hipLaunchKernelGGL(etxmk_gen_weights, dim3((unsigned)(blocks < 65536 ? blocks : 65536)), dim3(256), 0, st, dst, seed,
+                         stream_id(s.kind, s.layer, 0), s.count, s.rows, s.cols, s.perm, scale);
+    }
+    HIPCHK(hipGetLastError());
+  }
+  return ETXMK_OK;
+}
+
+int etxmk_load_tensor(etxmk_handle* h, int kind, int layer, int expert, const void* src, void* stream) {
+  if (!h || !h->w) return fail(ETXMK_EUNBOUND, "handle not bound");
+  uint64_t off;
+  int32_t rows, cols, perm;
+  if (int r = etxmk_tensor_info(h, kind, layer, expert, &off, &rows, &cols, &perm)) return r;
+  if (!src) return fail(ETXMK_EINVAL, "src is NULL");
+  hipStream_t st = (hipStream_t)stream;
+  if (perm) {
+    const size_t n = (size_t)rows * cols;
+    hipLaunchKernelGGL(etxmk_pack_rows, dim3((unsigned)((n + 255) / 256 < 65536 ? (n + 255) / 256 : 65536)), dim3(256), 0, st,
+                       (uint16_t*)(h->w + off), (const uint16_t*)src, rows, cols);
+    HIPCHK(hipGetLastError());
+  } else {
+    HIPCHK(hipMemcpyAsync(h->w + off, src, (size_t)rows * cols * 2, hipMemcpyDeviceToDevice, st));
+  }
+  return ETXMK_OK;
+}
+
+int etxmk_set_block_table(etxmk_handle* h, const int32_t* table, int32_t n, void* stream) {
+  if (!h || !h->wsp) return fail(ETXMK_EUNBOUND, "handle not bound");
+  const int nb = nblocks_of(&h->c);
+  if (!table || n <= 0 || n > nb) return fail(ETXMK_EINVAL, "block table length %d outside 1..%d", n, nb);
+  std::vector<char> seen(nb, 0);
+  for (int i = 0; i < n; ++i) {
+    if (table[i] < 0 || table[i] >= nb) return fail(ETXMK_EINVAL, "block %d maps to %d outside 0..%d", i, table[i], nb - 1);
+    if (seen[table[i]]) return fail(ETXMK_EINVAL, "physical block %d used twice", table[i]);
+    seen[table[i]] = 1;
+  }
+  for (int i = 0; i < n; ++i) h->btab_host[i] = table[i];
+  HIPCHK(hipMemcpyAsync(h->wsp + h->ws.btab, h->btab_host.data(), 4ull * n, hipMemcpyHostToDevice, (hipStream_t)stream));
+  HIPCHK(hipStreamSynchronize((hipStream_t)stream));
+  return ETXMK_OK;
+}
+
+int etxmk_fill_kv_seeded(etxmk_handle* h, uint64_t seed, int32_t npos, void* stream) {
+  if (!h || !h->kv) return fail(ETXMK_EUNBOUND, "handle not bound");
+  const etxmk_config& c = h->c;
+  if (npos < 0 || npos > c.max_ctx) return fail(ETXMK_EINVAL, "npos %d outside 0..%d", npos, c.max_ctx);
+  if (npos == 0) return ETXMK_OK;
+  const uint64_t kvl = kv_layer_elems(&c);
+  for (int l = 0; l < c.L; ++l) {
+    uint16_t* kc = (uint16_t*)h->kv + (uint64_t)l * 2 * kvl;
+    const size_t n = (size_t)npos * c.NKV * c.HD;
+    hipLaunchKernelGGL(etxmk_gen_kv, dim3((unsigned)((n + 255) / 256 < 65536 ? (n + 255) / 256 : 65536)), dim3(256), 0,
+                       (hipStream_t)stream, kc, kc + kvl, h->wsptr<const int32_t>(h->ws.btab),
+                       stream_key(seed, stream_id(10, l, 0)), stream_key(seed, stream_id(11, l, 0)), npos, c.NKV, c.HD,
+                       c.block_size);
+    HIPCHK(hipGetLastError());
+  }
+  return ETXMK_OK;
+}
+
+int etxmk_set_tokens(etxmk_handle* h, const int32_t* tokens, int32_t n, void* stream) {
+  if (!h || !h->wsp) return fail(ETXMK_EUNBOUND, "handle not bound");
+  if (!tokens || n < 0 || n > h->c.max_ctx + 1) return fail(ETXMK_EINVAL, "token count %d outside 0..%d", n, h->c.max_ctx + 1);
+  for (int i = 0; i < n; ++i)
+    if (tokens[i] < 0 || tokens[i] >= h->c.V) return fail(ETXMK_EINVAL, "token %d = %d outside 0..%d", i, tokens[i], h->c.V - 1);
+  HIPCHK(hipMemcpyAsync(h->wsp + h->ws.tokens, tokens, 4ull * n, hipMemcpyHostToDevice, (hipStream_t)stream));
+  HIPCHK(hipStreamSynchronize((hipStream_t)stream));
+  return ETXMK_OK;
+}
+
+int etxmk_read_tokens(etxmk_handle* h, int32_t* out, int32_t n, void* stream) {
+  if (!h || !h->wsp) return fail(ETXMK_EUNBOUND, "handle not bound");
+  if (!out || n < 0 || n > h->c.max_ctx + 1) return fail(ETXMK_EINVAL, "token count %d outside 0..%d", n, h->c.max_ctx + 1);
+  HIPCHK(hipMemcpyAsync(out, h->wsp + h->ws.out_tokens, 4ull * n, hipMemcpyDeviceToHost, (hipStream_t)stream));
+  HIPCHK(hipStreamSynchronize((hipStream_t)stream));
+  return ETXMK_OK;
+}
+
+int etxmk_set_residual(etxmk_handle* h, const float* x, void* stream) {
+  if (!h || !h->wsp) return fail(ETXMK_EUNBOUND, "handle not bound");
+  if (!x) return fail(ETXMK_EINVAL, "x is NULL");
+  HIPCHK(hipMemcpyAsync(h->wsp + h->ws.x, x, 4ull * h->c.H, hipMemcpyHostToDevice, (hipStream_t)stream));
+  HIPCHK(hipStreamSynchronize((hipStream_t)stream));
+  return ETXMK_OK;
+}
+
+int etxmk_read_residual(etxmk_handle* h, float* x, void* stream) {
+  if (!h || !h->wsp) return fail(ETXMK_EUNBOUND, "handle not bound");
+  if (!x) return fail(ETXMK_EINVAL, "x is NULL");
+  HIPCHK(hipMemcpyAsync(x, h->wsp + h->ws.x, 4ull * h->c.H, hipMemcpyDeviceToHost, (hipStream_t)stream));
+  HIPCHK(hipStreamSynchronize((hipStream_t)stream));
+  return ETXMK_OK;
+}
+
+int etxmk_set_fused(etxmk_handle* h, int32_t fused) {
+  if (!h) return fail(ETXMK_EINVAL, "NULL handle");
+  h->fused = fused ? 1 : 0;
+  return ETXMK_OK;
+}
+
+int etxmk_set_grid(etxmk_handle* h, int32_t workgroups) {
+  if (!h) return fail(ETXMK_EINVAL, "NULL handle");
+  const etxmk_config& c = h->c;
+  const int need = 8 * (c.NH / c.NKV) * ((c.NKV + 7) / 8);
+  const int wg = workgroups > 0 ? workgroups : h->ncu;
+  if (wg < need || wg > h->ncu) return fail(ETXMK_EINVAL, "workgroups %d outside %d..%d", wg, need, h->ncu);
+  h->nwg = wg;
+  return ETXMK_OK;
+}
+
+int etxmk_set_dump(etxmk_handle* h, float* x_layers, int32_t* topk_ids, float* topk_w, float* router_logits) {
+  if (!h) return fail(ETXMK_EINVAL, "NULL handle");
+  h->dump_x = x_layers;
+  h->dump_ids = topk_ids;
+  h->dump_wts = topk_w;
+  h->dump_logits = router_logits;
+  return ETXMK_OK;
+}
+
+int etxmk_barriers_per_step(etxmk_handle* h, int32_t* n) {
+  if (!h || !n) return fail(ETXMK_EINVAL, "NULL argument");
+  *n = h->barriers(0, h->c.L, 1);
+  return ETXMK_OK;
+}
+
+static int launch(etxmk_handle* h, int pos, int write_next, int l0, int l1, int embed, int head, hipStream_t st) {
+  if (!h || !h->wsp) return fail(ETXMK_EUNBOUND, "handle not bound");
+  const etxmk_config& c = h->c;
+  if (pos < 0 || pos >= c.max_ctx) return fail(ETXMK_EINVAL, "position %d outside 0..%d", pos, c.max_ctx - 1);
+  if (l0 < 0 || l1 > c.L || l0 >= l1) return fail(ETXMK_EINVAL, "layer range [%d, %d) outside [0, %d)", l0, l1, c.L);
+  const int need = 8 * (c.NH / c.NKV) * ((c.NKV + 7) / 8);
+  if (h->nwg < need) return fail(ETXMK_EINVAL, "grid of %d workgroups is below the %d the attention phase needs", h->nwg, need);
+  Params p{};
+  p.H = c.H; p.NH = c.NH; p.NKV = c.NKV; p.HD = c.HD; p.I = c.I; p.E = c.E; p.TOPK = c.TOPK; p.MI = c.MI; p.L = c.L; p.V = c.V;
+  p.moe = c.moe; p.qk_norm = c.qk_norm; p.norm_topk = c.norm_topk; p.BS = c.block_size; p.max_ctx = c.max_ctx;
+  p.nblocks = nblocks_of(&c);
+  p.eps = c.eps;
+  p.attn_scale = (float)(1.0 / sqrt((double)c.HD));
+  p.embed = h->wt(ETXMK_T_EMBED, -1);
+  p.lm_head = h->wt(ETXMK_T_LMHEAD, -1);
+  p.final_norm = h->wt(ETXMK_T_FINAL_NORM, -1);
+  p.layers = h->wsptr<const LayerW>(h->ws.layers);
+  p.rope_cos = h->wsptr<const float>(h->ws.rcos);
+  p.rope_sin = h->wsptr<const float>(h->ws.rsin);
+  p.btab = h->wsptr<const int32_t>(h->ws.btab);
+  p.x = h->wsptr<float>(h->ws.x);
+  p.qkv = h->wsptr<float>(h->ws.qkv);
+  p.o = h->wsptr<float>(h->ws.o);
+  p.logits = h->wsptr<float>(h->ws.logits);
+  p.hbuf = h->wsptr<float>(h->ws.hbuf);
+  p.amax = h->wsptr<uint64_t>(h->ws.amax);
+  p.bar = h->wsptr<uint32_t>(h->ws.bar);
+  p.abort_word = h->wsptr<int32_t>(h->ws.abort_w);
+  p.tokens = h->wsptr<int32_t>(h->ws.tokens);
+  p.out_tokens = h->wsptr<int32_t>(h->ws.out_tokens);
+  p.dump_x = h->dump_x; p.dump_ids = h->dump_ids; p.dump_wts = h->dump_wts; p.dump_logits = h->dump_logits;
+  p.pos = pos; p.write_next = write_next; p.l0 = l0; p.l1 = l1; p.do_embed = embed; p.do_head = head;
+  p.nwg = h->nwg;
+  p.spin_ticks = 200000000ull;            // 2 s of the 100 MHz s_memrealtime clock
+  if (h->fused) {
+    p.bar_base = h->bar_epoch;
+    void* args[] = {&p};
+    HIPCHK(hipLaunchCooperativeKernel((const void*)etxmk_fused, dim3(h->nwg), dim3(NT), args, 0, st));
+    h->bar_epoch += (uint32_t)h->barriers(l0, l1, head) * (uint32_t)h->nwg;
+  } else {
+    auto ph = [&](int phase, int layer) -> int {
+      hipLaunchKernelGGL(etxmk_phase, dim3(h->nwg), dim3(NT), 0, st, p, phase, layer);
+      HIPCHK(hipGetLastError());
+      return ETXMK_OK;
+    };
+    for (int l = l0; l < l1; ++l) {
+      int r = ph(PH_QKV, l);
+      r = r ? r : ph(PH_ATTN, l);
+      r = r ? r : ph(PH_OPROJ, l);
+      if (c.moe) {
+        r = r ? r : ph(PH_ROUTER, l);
+        r = r ? r : ph(PH_EXPUP, l);
+        r = r ? r : ph(PH_EXPDN, l);
+      } else {
+        r = r ? r : ph(PH_GATEUP, l);
+        r = r ? r : ph(PH_DOWN, l);
+      }
+      if (r) return r;
+    }
+    if (head) {
+      if (int r = ph(PH_HEAD, 0)) return r;
+      if (int r = ph(PH_TOKEN, 0)) return r;
+    }
+  }
+  return ETXMK_OK;
+}
+
+int etxmk_step(etxmk_handle* h, int32_t pos, int32_t write_next, void* stream) {
+  if (!h) return fail(ETXMK_EINVAL, "NULL handle");
+  return launch(h, pos, write_next, 0, h->c.L, 1, 1, (hipStream_t)stream);
+}
+
+int etxmk_step_layers(etxmk_handle* h, int32_t pos, int32_t l0, int32_t l1, void* stream) {
+  if (!h) return fail(ETXMK_EINVAL, "NULL handle");
+  return launch(h, pos, 0, l0, l1, 0, 0, (hipStream_t)stream);
+}
+
+int etxmk_sync(etxmk_handle* h, void* stream) {
+  if (!h || !h->wsp) return fail(ETXMK_EUNBOUND, "handle not bound");
+  HIPCHK(hipStreamSynchronize((hipStream_t)stream));
+  int32_t ab = 0;
+  HIPCHK(hipMemcpy(&ab, h->wsp + h->ws.abort_w, 4, hipMemcpyDeviceToHost));
+  if (ab) {
+    HIPCHK(hipMemset(h->wsp + h->ws.abort_w, 0, 4));
+    HIPCHK(hipMemset(h->wsp + h->ws.bar, 0, 4));
+    h->bar_epoch = 0;
+    return fail(ETXMK_ABORTED, "device abort word %d (barrier wait exceeded its limit)", ab);
+  }
+  return ETXMK_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,53 @@
+"""Decoder configurations of the decode path.
+
+The real shapes are those of examples/llm/configs/{qwen3-8b,qwen3-30b-a3b}.json in the reference, read
+through the same rules as examples/llm/model.py:95-140 (load_dims); the tiny ones exist so the CPU oracle
+can check every phase in seconds.
+"""
+from __future__ import annotations
+
+import json
+from pathlib import Path
+
+from etx.runtime.native import ModelConfig
+
+QWEN3_8B = ModelConfig(name="qwen3-8b", H=4096, NH=32, NKV=8, HD=128, L=36, V=151936, I=12288,
+                       moe=0, qk_norm=1, eps=1e-6, theta=1e6, max_ctx=1088)
+QWEN3_30B_A3B = ModelConfig(name="qwen3-30b-a3b", H=2048, NH=32, NKV=4, HD=128, L=48, V=151936,
+                            E=128, TOPK=8, MI=768, moe=1, qk_norm=1, norm_topk=1, eps=1e-6, theta=1e6, max_ctx=1088)
+# one Qwen3-8B layer (the single-layer configuration; the vocabulary is irrelevant there)
+QWEN3_8B_LAYER = ModelConfig(name="qwen3-8b-layer", H=4096, NH=32, NKV=8, HD=128, L=1, V=1024, I=12288,
+                             moe=0, qk_norm=1, eps=1e-6, theta=1e6, max_ctx=1088)
+TINY_MOE = ModelConfig(name="tiny-moe", H=512, NH=4, NKV=2, HD=128, L=2, V=4096, E=16, TOPK=4, MI=256,
+                       moe=1, qk_norm=1, norm_topk=1, max_ctx=256)
+TINY_DENSE = ModelConfig(name="tiny-dense", H=512, NH=4, NKV=2, HD=128, L=2, V=4096, I=1024,
+                         moe=0, qk_norm=1, max_ctx=256)
+
+CONFIGS = {c.name: c for c in (QWEN3_8B, QWEN3_30B_A3B, QWEN3_8B_LAYER, TINY_MOE, TINY_DENSE)}
+
+
+def with_layers(cfg: ModelConfig, L: int, **kw) -> ModelConfig:
+    d = cfg.as_dict()
+    d.update(L=L, **kw)
+    return ModelConfig(name=f"{cfg.name}-L{L}", **d)
+
+
+def from_hf_config(path: str | Path, max_ctx: int = 1088, layers: int = 0) -> ModelConfig:
+    """Dimensions from a Hugging Face config.json (the subset examples/llm/model.py:95-140 accepts for
+    Qwen3 dense and Qwen3-MoE); anything else is refused rather than guessed."""
+    c = json.loads(Path(path).read_text())
+    mt = c.get("model_type", "")
+    if not mt.startswith("qwen3"):
+        raise ValueError(f"{path}: model_type {mt!r} is not a Qwen3 dense/MoE decoder")
+    E = int(c.get("num_experts", 0) or 0)
+    if E and (c.get("mlp_only_layers") or c.get("decoder_sparse_step", 1) != 1):
+        raise ValueError("mixed dense / MoE layer layouts are not supported")
+    if c.get("tie_word_embeddings"):
+        raise ValueError("tied embeddings are not supported by this path")
+    H, NH = c["hidden_size"], c["num_attention_heads"]
+    return ModelConfig(name=Path(path).stem, H=H, NH=NH, NKV=c.get("num_key_value_heads", NH), HD=c.get("head_dim", H // NH),
+                       L=min(layers or c["num_hidden_layers"], c["num_hidden_layers"]), V=c["vocab_size"],
+                       I=0 if E else c["intermediate_size"], E=E, TOPK=int(c.get("num_experts_per_tok", 0)) if E else 0,
+                       MI=int(c.get("moe_intermediate_size", 0)) if E else 0, moe=int(E > 0), qk_norm=1,
+                       norm_topk=int(bool(c.get("norm_topk_prob", True))), eps=float(c.get("rms_norm_eps", 1e-6)),
+                       theta=float(c.get("rope_theta", 1e6)), max_ctx=max_ctx)

@@ -1,0 +1,308 @@
+"""ctypes binding of libetxmk.so, the gfx950 decode megakernel (include/etxmk.h).
+
+PyTorch is used only to allocate the device buffers the library borrows and to pick the HIP stream.
+There is no fallback: if the library is missing or a call fails, an exception says so.
+
+Reference counterparts: etx_host (etx/runtime/include/etx/host.h:22-692) and the per-token loop of
+examples/llm/host.hip:57-244 (prompt fed token by token through the decode step, :203-213).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import re
+from dataclasses import dataclass, field, asdict
+from pathlib import Path
+
+import numpy as np
+
+PKG = Path(__file__).resolve().parents[2]
+LIB_PATH = PKG / "lib" / "libetxmk.so"
+HEADER = PKG.parent / "include" / "etxmk.h"
+
+OK, EINVAL, EHIP, ABORTED, EUNBOUND = 0, 1, 2, 3, 4
+T_EMBED, T_LMHEAD, T_WQKV, T_WO, T_ROUTER, T_W13, T_W2, T_WGU, T_WD = 1, 2, 3, 4, 5, 6, 7, 8, 9
+T_LN1, T_LN2, T_QNORM, T_KNORM, T_FINAL_NORM = 20, 21, 22, 23, 24
+
+
+class EtxmkError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"etxmk error {code}: {msg}")
+        self.code = code
+
+
+class DeviceAbort(EtxmkError):
+    pass
+
+
+class EtxmkConfig(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in ("H", "NH", "NKV", "HD", "I", "E", "TOPK", "MI", "L", "V",
+                                          "moe", "qk_norm", "norm_topk", "block_size", "max_ctx", "batch")] + \
+               [("eps", C.c_float), ("theta", C.c_float)]
+
+
+@dataclass(frozen=True)
+class ModelConfig:
+    """Decoder dimensions (the fields of examples/llm/model.py:45-93 Dims that the decode step uses)."""
+    H: int
+    NH: int
+    NKV: int
+    HD: int
+    L: int
+    V: int
+    I: int = 0
+    E: int = 0
+    TOPK: int = 0
+    MI: int = 0
+    moe: int = 0
+    qk_norm: int = 1
+    norm_topk: int = 1
+    block_size: int = 16
+    max_ctx: int = 1088
+    batch: int = 1
+    eps: float = 1e-6
+    theta: float = 1e6
+    name: str = field(default="custom", compare=False)
+
+    def as_struct(self) -> EtxmkConfig:
+        return EtxmkConfig(**{k: getattr(self, k) for k, _ in EtxmkConfig._fields_})
+
+    def as_dict(self) -> dict:
+        d = asdict(self)
+        d.pop("name")
+        return d
+
+    @property
+    def nqkv(self) -> int:
+        return (self.NH + 2 * self.NKV) * self.HD
+
+
+_lib = None
+
+
+def declared_functions() -> list[str]:
+    """Every function include/etxmk.h declares."""
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(etxmk_\w+)\s*\(", text, re.M)))
+
+
+def load(path: Path | None = None):
+    """Load libetxmk.so (torch first, so the process holds the one HIP runtime torch brings)."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    import torch  # noqa: F401  (binds libamdhip64 before the library resolves it)
+    p = Path(path or LIB_PATH)
+    if not p.exists():
+        raise FileNotFoundError(f"{p} is not built; run etx-megakernel_amd/build_lib.py (no fallback path exists)")
+    L = C.CDLL(str(p))
+    vp, i32, u64 = C.c_void_p, C.c_int32, C.c_uint64
+    sig = {
+        "etxmk_abi_version": [],
+        "etxmk_last_error": [],
+        "etxmk_weight_bytes": [C.POINTER(EtxmkConfig), C.POINTER(u64)],
+        "etxmk_kv_bytes": [C.POINTER(EtxmkConfig), C.POINTER(u64)],
+        "etxmk_workspace_bytes": [C.POINTER(EtxmkConfig), C.POINTER(u64)],
+        "etxmk_create": [C.POINTER(EtxmkConfig), C.POINTER(vp)],
+        "etxmk_destroy": [vp],
+        "etxmk_bind": [vp, vp, vp, vp],
+        "etxmk_tensor_info": [vp, i32, i32, i32, C.POINTER(u64), C.POINTER(i32), C.POINTER(i32), C.POINTER(i32)],
+        "etxmk_init_weights_seeded": [vp, u64, C.c_float, vp],
+        "etxmk_load_tensor": [vp, i32, i32, i32, vp, vp],
+        "etxmk_set_block_table": [vp, C.POINTER(i32), i32, vp],
+        "etxmk_fill_kv_seeded": [vp, u64, i32, vp],
+        "etxmk_set_tokens": [vp, C.POINTER(i32), i32, vp],
+        "etxmk_read_tokens": [vp, C.POINTER(i32), i32, vp],
+        "etxmk_step": [vp, i32, i32, vp],
+        "etxmk_step_layers": [vp, i32, i32, i32, vp],
+        "etxmk_set_residual": [vp, C.POINTER(C.c_float), vp],
+        "etxmk_read_residual": [vp, C.POINTER(C.c_float), vp],
+        "etxmk_sync": [vp, vp],
+        "etxmk_set_fused": [vp, i32],
+        "etxmk_set_dump": [vp, vp, vp, vp, vp],
+        "etxmk_set_grid": [vp, i32],
+        "etxmk_barriers_per_step": [vp, C.POINTER(i32)],
+    }
+    for name, args in sig.items():
+        f = getattr(L, name)
+        f.argtypes = args
+        f.restype = C.c_char_p if name == "etxmk_last_error" else C.c_int
+    if L.etxmk_abi_version() != 1:
+        raise EtxmkError(EINVAL, f"ABI version {L.etxmk_abi_version()} != 1")
+    if path is None:
+        _lib = L
+    return L
+
+
+def _check(L, rc: int):
+    if rc != OK:
+        msg = L.etxmk_last_error().decode(errors="replace")
+        if rc == ABORTED:
+            raise DeviceAbort(rc, msg)
+        raise EtxmkError(rc, msg)
+
+
+def sizes(cfg: ModelConfig) -> dict:
+    """Bytes of the weight arena, KV cache and workspace (no GPU needed)."""
+    L = load()
+    c = cfg.as_struct()
+    out = {}
+    for key, fn in (("weights", L.etxmk_weight_bytes), ("kv", L.etxmk_kv_bytes), ("workspace", L.etxmk_workspace_bytes)):
+        v = C.c_uint64()
+        _check(L, fn(C.byref(c), C.byref(v)))
+        out[key] = int(v.value)
+    return out
+
+
+def unpermute_rows(stored: np.ndarray) -> np.ndarray:
+    """Natural row order from the lane-permuted storage (blocks of 512; lane l holds l, l+64, ...)."""
+    rows, K = stored.shape
+    out = np.empty_like(stored)
+    for base in range(0, K, 512):
+        S = min(512, K - base)
+        m = S // 64
+        blk = stored[:, base:base + S].reshape(rows, 64, m)           # [row][lane][e]
+        out[:, base:base + S] = blk.transpose(0, 2, 1).reshape(rows, S)  # element l + 64 e
+    return out
+
+
+class Decoder:
+    """One model on one GPU: owns the torch buffers the library borrows."""
+
+    def __init__(self, cfg: ModelConfig, device: str = "cuda:0", fused: bool = True, workgroups: int = 0):
+        import torch
+        self.torch = torch
+        self.cfg = cfg
+        self.device = torch.device(device)
+        self.L = load()
+        sz = sizes(cfg)
+        self.sizes = sz
+        self.weights = torch.empty(sz["weights"], dtype=torch.uint8, device=self.device)
+        self.kv = torch.zeros(sz["kv"], dtype=torch.uint8, device=self.device)
+        self.workspace = torch.zeros(sz["workspace"], dtype=torch.uint8, device=self.device)
+        h = C.c_void_p()
+        c = cfg.as_struct()
+        with torch.cuda.device(self.device):
+            _check(self.L, self.L.etxmk_create(C.byref(c), C.byref(h)))
+            self.h = h
+            _check(self.L, self.L.etxmk_bind(h, self.weights.data_ptr(), self.kv.data_ptr(), self.workspace.data_ptr()))
+            _check(self.L, self.L.etxmk_set_fused(h, int(fused)))
+            _check(self.L, self.L.etxmk_set_grid(h, int(workgroups)))
+        self._dumps = None
+
+    # ---- plumbing
+    def _stream(self):
+        return C.c_void_p(self.torch.cuda.current_stream(self.device).cuda_stream)
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.L.etxmk_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # ---- weights / cache
+    def init_weights(self, seed: int, scale: float = 0.02):
+        _check(self.L, self.L.etxmk_init_weights_seeded(self.h, seed, scale, self._stream()))
+
+    def tensor_info(self, kind: int, layer: int = -1, expert: int = 0):
+        off, r, c, p = C.c_uint64(), C.c_int32(), C.c_int32(), C.c_int32()
+        _check(self.L, self.L.etxmk_tensor_info(self.h, kind, layer, expert, C.byref(off), C.byref(r), C.byref(c), C.byref(p)))
+        return int(off.value), int(r.value), int(c.value), bool(p.value)
+
+    def tensor(self, kind: int, layer: int = -1, expert: int = 0, natural: bool = True) -> np.ndarray:
+        """Host copy of one tensor as uint16 bf16 bits [rows][cols] (natural row order unless natural=False)."""
+        off, r, c, perm = self.tensor_info(kind, layer, expert)
+        t = self.weights[off:off + r * c * 2].view(self.torch.int16).cpu().numpy().view(np.uint16).reshape(r, c)
+        return unpermute_rows(t) if (perm and natural) else t
+
+    def load_tensor(self, kind: int, layer: int, expert: int, src):
+        """src: torch bf16/int16 tensor on the device in natural [rows][cols] layout."""
+        _check(self.L, self.L.etxmk_load_tensor(self.h, kind, layer, expert, src.data_ptr(), self._stream()))
+
+    def set_block_table(self, table):
+        t = np.ascontiguousarray(table, np.int32)
+        _check(self.L, self.L.etxmk_set_block_table(self.h, t.ctypes.data_as(C.POINTER(C.c_int32)), len(t), self._stream()))
+
+    def fill_kv_seeded(self, seed: int, npos: int):
+        _check(self.L, self.L.etxmk_fill_kv_seeded(self.h, seed, npos, self._stream()))
+
+    def kv_layer(self, layer: int):
+        """(K, V) of one layer as uint16 bf16 bits, paged layout, flat."""
+        n = self.sizes["kv"] // 2 // self.cfg.L // 2
+        base = layer * 2 * n
+        flat = self.kv.view(self.torch.int16)
+        return (flat[base:base + n].cpu().numpy().view(np.uint16), flat[base + n:base + 2 * n].cpu().numpy().view(np.uint16))
+
+    # ---- dumps
+    def enable_dumps(self, on: bool = True):
+        torch = self.torch
+        cfg = self.cfg
+        if not on:
+            _check(self.L, self.L.etxmk_set_dump(self.h, None, None, None, None))
+            self._dumps = None
+            return
+        k = max(cfg.TOPK, 1)
+        self._dumps = dict(
+            x=torch.zeros((cfg.L, cfg.H), dtype=torch.float32, device=self.device),
+            ids=torch.full((cfg.L, k), -1, dtype=torch.int32, device=self.device),
+            w=torch.zeros((cfg.L, k), dtype=torch.float32, device=self.device),
+            logits=torch.zeros((cfg.L, max(cfg.E, 1)), dtype=torch.float32, device=self.device))
+        d = self._dumps
+        moe = bool(cfg.moe)
+        _check(self.L, self.L.etxmk_set_dump(self.h, d["x"].data_ptr(), d["ids"].data_ptr() if moe else None,
+                                             d["w"].data_ptr() if moe else None, d["logits"].data_ptr() if moe else None))
+
+    def dumps(self) -> dict:
+        self.sync()
+        return {k: v.cpu().numpy().copy() for k, v in self._dumps.items()}
+
+    # ---- steps
+    def set_tokens(self, tokens):
+        t = np.ascontiguousarray(tokens, np.int32)
+        _check(self.L, self.L.etxmk_set_tokens(self.h, t.ctypes.data_as(C.POINTER(C.c_int32)), len(t), self._stream()))
+
+    def read_tokens(self, n: int) -> np.ndarray:
+        out = np.zeros(n, np.int32)
+        _check(self.L, self.L.etxmk_read_tokens(self.h, out.ctypes.data_as(C.POINTER(C.c_int32)), n, self._stream()))
+        return out
+
+    def step(self, pos: int, write_next: bool = True):
+        _check(self.L, self.L.etxmk_step(self.h, pos, int(write_next), self._stream()))
+
+    def step_layers(self, pos: int, l0: int, l1: int):
+        _check(self.L, self.L.etxmk_step_layers(self.h, pos, l0, l1, self._stream()))
+
+    def set_residual(self, x):
+        x = np.ascontiguousarray(x, np.float32)
+        _check(self.L, self.L.etxmk_set_residual(self.h, x.ctypes.data_as(C.POINTER(C.c_float)), self._stream()))
+
+    def read_residual(self) -> np.ndarray:
+        x = np.zeros(self.cfg.H, np.float32)
+        _check(self.L, self.L.etxmk_read_residual(self.h, x.ctypes.data_as(C.POINTER(C.c_float)), self._stream()))
+        return x
+
+    def sync(self):
+        _check(self.L, self.L.etxmk_sync(self.h, self._stream()))
+
+    def barriers_per_step(self) -> int:
+        n = C.c_int32()
+        _check(self.L, self.L.etxmk_barriers_per_step(self.h, C.byref(n)))
+        return int(n.value)
+
+    def generate(self, prompt, n_new: int) -> np.ndarray:
+        """Feed the prompt token by token, then n_new greedy steps; returns the generated ids
+        (examples/llm/host.hip:203-213 and ref_numpy.py:181-186 drive the same loop)."""
+        prompt = list(int(t) for t in prompt)
+        P = len(prompt)
+        if P < 1 or P + n_new > self.cfg.max_ctx:
+            raise ValueError(f"prompt {P} + {n_new} new tokens exceed max_ctx {self.cfg.max_ctx}")
+        self.set_tokens(prompt)
+        for pos in range(P + n_new - 1):
+            self.step(pos, write_next=pos + 1 >= P)
+        self.sync()
+        out = self.read_tokens(P + n_new - 1)
+        return out[P - 1:P - 1 + n_new]

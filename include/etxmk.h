@@ -1,0 +1,136 @@
+/*
+ * etxmk — C ABI of the MI355X (gfx950) batch-small decode megakernel.
+ *
+ * One handle drives one decoder model on one GPU.  The caller owns every buffer (weights, KV cache,
+ * workspace) and hands the library device pointers; the library never allocates device memory and
+ * never frees what it is given.  Calls are asynchronous on the HIP stream passed in; one handle is not
+ * thread-safe; errors are integer status codes with a message in etxmk_last_error() (no exit()).
+ *
+ * Each entry point names the reference interface it replaces (paths relative to the reference checkout).
+ */
+#ifndef ETXMK_H
+#define ETXMK_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ETXMK_ABI_VERSION 1
+
+/* status codes */
+#define ETXMK_OK 0
+#define ETXMK_EINVAL 1          /* bad argument or unsupported shape */
+#define ETXMK_EHIP 2            /* a HIP runtime call failed */
+#define ETXMK_ABORTED 3         /* the device spin limit fired or the host set the abort word */
+#define ETXMK_EUNBOUND 4        /* buffers not bound yet */
+
+/* tensor kinds (also the seeded generator's stream kinds: stream = kind << 48 | (layer + 1) << 24 | expert) */
+#define ETXMK_T_EMBED 1
+#define ETXMK_T_LMHEAD 2
+#define ETXMK_T_WQKV 3
+#define ETXMK_T_WO 4
+#define ETXMK_T_ROUTER 5
+#define ETXMK_T_W13 6
+#define ETXMK_T_W2 7
+#define ETXMK_T_WGU 8
+#define ETXMK_T_WD 9
+#define ETXMK_T_LN1 20
+#define ETXMK_T_LN2 21
+#define ETXMK_T_QNORM 22
+#define ETXMK_T_KNORM 23
+#define ETXMK_T_FINAL_NORM 24
+
+/* Model dimensions: the POD copy of examples/llm/model.py:45-93 Dims (load_dims, :95-140) that the
+ * reference's llm_params.h (__constant__ LlmParams, examples/llm/llm_params.h:1-73) carries. */
+typedef struct etxmk_config {
+  int32_t H, NH, NKV, HD, I, E, TOPK, MI, L, V;
+  int32_t moe, qk_norm, norm_topk, block_size, max_ctx, batch;
+  float eps, theta;
+} etxmk_config;
+
+typedef struct etxmk_handle etxmk_handle;
+
+/* Library identity; no reference counterpart (the reference links its runtime statically). */
+int etxmk_abi_version(void);
+/* Message of the last failing call on this thread (reference: ETX_CHECK's stderr text, etx/runtime/include/etx/host.h:18). */
+const char* etxmk_last_error(void);
+
+/* Buffer sizes for a configuration (reference: the allocations of examples/llm/host.hip:122-160 and
+ * examples/vllm_llm/host.hip:274-317; here the caller allocates). */
+int etxmk_weight_bytes(const etxmk_config* cfg, uint64_t* bytes);
+int etxmk_kv_bytes(const etxmk_config* cfg, uint64_t* bytes);
+int etxmk_workspace_bytes(const etxmk_config* cfg, uint64_t* bytes);
+
+/* Create / destroy a handle (reference: etx_host::setup, etx/runtime/include/etx/host.h:79-210). */
+int etxmk_create(const etxmk_config* cfg, etxmk_handle** out);
+int etxmk_destroy(etxmk_handle* h);
+
+/* Bind caller-owned device buffers (reference: the tensor table etx_params.args, etx/runtime/include/etx/abi.h:80-84,
+ * filled by the host from its allocations).  Computes and uploads the bf16 RoPE tables
+ * (examples/llm/host.hip:164-178) into the workspace and the identity block table. */
+int etxmk_bind(etxmk_handle* h, void* weights, void* kv, void* workspace);
+
+/* Where a tensor lives in the weight arena: byte offset, rows, cols, and whether its rows are stored
+ * lane-permuted (1) or natural (0).  Reference: the `t name offset count` manifest lines of
+ * etx/models/llm/prep.py:243-258. */
+int etxmk_tensor_info(etxmk_handle* h, int kind, int layer, int expert, uint64_t* offset, int32_t* rows,
+                      int32_t* cols, int32_t* permuted);
+
+/* Fill every weight from the seeded generator (bf16(scale * N(0,1)); norm weights 1.0).
+ * Reference: random-init weights have no counterpart; the shapes are those of prep.py:88-146. */
+int etxmk_init_weights_seeded(etxmk_handle* h, uint64_t seed, float scale, void* stream);
+
+/* Copy one tensor in natural row-major layout (device pointer) into the arena, permuting its rows.
+ * Reference: the weight load of examples/llm/host.hip:70-121. */
+int etxmk_load_tensor(etxmk_handle* h, int kind, int layer, int expert, const void* src, void* stream);
+
+/* Paged-KV block table: logical block i of the sequence -> physical block table[i].
+ * Reference: block_tables upload, examples/vllm_llm/host.hip:279-282. */
+int etxmk_set_block_table(etxmk_handle* h, const int32_t* table, int32_t n, void* stream);
+
+/* Fill KV positions [0, npos) of every layer with bf16 N(0,1) from the seeded generator (the
+ * single-layer configuration's cache).  No reference counterpart (the reference prefills by decoding). */
+int etxmk_fill_kv_seeded(etxmk_handle* h, uint64_t seed, int32_t npos, void* stream);
+
+/* Token buffer: tokens[0..n) are the prompt; step s reads tokens[s] (reference: P.token_in,
+ * examples/llm/tiles.hip:77-82). */
+int etxmk_set_tokens(etxmk_handle* h, const int32_t* tokens, int32_t n, void* stream);
+int etxmk_read_tokens(etxmk_handle* h, int32_t* out_tokens, int32_t n, void* stream);
+
+/* One decode step at position pos for sequence step `pos` (token tokens[pos]); the greedy token goes to
+ * out_tokens[pos] and, when write_next != 0, to tokens[pos + 1].  Asynchronous on `stream`.
+ * Reference: etx_host::run (etx/runtime/include/etx/host.h:518-544) = reset_step + launch of
+ * etx_megakernel_d0 (etx/codegen/kernel.py:471-605), after llm_set_params (examples/llm/tiles.hip:16-19). */
+int etxmk_step(etxmk_handle* h, int32_t pos, int32_t write_next, void* stream);
+
+/* Layers [l0, l1) only, on the residual already in the workspace (etxmk_set_residual), no embedding and
+ * no head: the single-layer configuration.  Reference: a graph of one layer (examples/llm/model.py:220-273). */
+int etxmk_step_layers(etxmk_handle* h, int32_t pos, int32_t l0, int32_t l1, void* stream);
+int etxmk_set_residual(etxmk_handle* h, const float* x, void* stream);
+int etxmk_read_residual(etxmk_handle* h, float* x, void* stream);
+
+/* Wait for the stream and check the abort word (reference: etx_host::wait + after_wait,
+ * etx/runtime/include/etx/host.h:351-417).  Returns ETXMK_ABORTED if the device gave up. */
+int etxmk_sync(etxmk_handle* h, void* stream);
+
+/* Execution mode: 1 = one persistent cooperative launch per step (the fused megakernel), 0 = one launch per
+ * phase with the same device functions (reference: run_unfused, etx/runtime/include/etx/host.h:418-457). */
+int etxmk_set_fused(etxmk_handle* h, int32_t fused);
+
+/* Per-layer dumps of the next steps (device pointers, may be NULL): residual after each layer [L][H] fp32,
+ * top-k ids [L][TOPK] int32, weights [L][TOPK] fp32, router logits [L][E] fp32.
+ * Reference: ref_numpy.py --dump (examples/llm/ref_numpy.py:199-201) and host --check-dsl
+ * (examples/vllm_llm/host.hip:954-1141). */
+int etxmk_set_dump(etxmk_handle* h, float* x_layers, int32_t* topk_ids, float* topk_w, float* router_logits);
+
+/* Workgroups of the persistent launch (0 = one per CU). */
+int etxmk_set_grid(etxmk_handle* h, int32_t workgroups);
+/* Grid barriers executed by one step (diagnostics). */
+int etxmk_barriers_per_step(etxmk_handle* h, int32_t* n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,573 @@
+/*
+ * CPU oracle for the batch-small decode step (TEST INFRASTRUCTURE ONLY).
+ *
+ * This file is a checker: only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
+ * load it.  The product (the HIP library) never calls it.
+ *
+ * It restates the reference's CPU numerical reference, examples/llm/ref_numpy.py (Ref.step,
+ * :105-158), with bf16 round-to-nearest-even at exactly the points that file rounds (bfr, :26-32).
+ * Where the reference leaves the fp32 evaluation order to numpy/BLAS (matvec `@`, np.mean, .sum()),
+ * this oracle fixes one documented order, the same order the gfx950 kernels use, so that GPU
+ * results can be compared bit for bit:
+ *
+ *   dot64(w, x, K)   64 interleaved fp32 accumulators, acc[k % 64] = fma(w[k], x[k], acc[k % 64]) for
+ *                    k ascending, then an xor butterfly: for off in 32,16,8,4,2,1: a[l] = a[l] + a[l ^ off];
+ *                    the result is a[0].  Every matvec and every sum of squares uses it.
+ *   attention        chunks of 64 positions; per chunk the local max m_c, p_t = expf(s_t - m_c),
+ *                    l_c and a_c[d] as ascending-t fma chains; chunks merged in ascending order with
+ *                    w_c = expf(m_c - M):  L = fma(w_c, l_c, L), A[d] = fma(w_c, a_c[d], A[d]); o = bfr(A / L).
+ *                    This is the split/merge form of the reference's GPU tiles (examples/llm/tiles.hip:175-247),
+ *                    mathematically the softmax of ref_numpy.py:122-129.
+ *   softmax sums     over experts: the dot64 accumulator pattern with plain adds.
+ *   exp              mk_expf below: Cody-Waite reduction by ln2 and a degree-7 Taylor polynomial.
+ *
+ * The seeded weight generator (splitmix64 counter stream + Box-Muller with polynomial log/sin/cos, all
+ * in IEEE basic operations) is specified here independently of the device code that must reproduce it.
+ *
+ * Compile: gcc -O3 -mavx2 -mfma -ffp-contract=off -fopenmp -shared -fPIC (see oracle/Makefile).
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+#include <omp.h>
+
+#define EXPORT __attribute__((visibility("default")))
+
+/* ------------------------------------------------------------------ bf16 */
+/* ref_numpy.py:26-32 bfr(): u + 0x7FFF + lsb, masked to the top 16 bits */
+static inline float bfr(float x) {
+  uint32_t u; memcpy(&u, &x, 4);
+  u = (u + 0x7FFFu + ((u >> 16) & 1u)) & 0xFFFF0000u;
+  float r; memcpy(&r, &u, 4); return r;
+}
+static inline uint16_t f2bf(float x) {
+  uint32_t u; memcpy(&u, &x, 4);
+  return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+static inline float bf2f(uint16_t b) {
+  uint32_t u = (uint32_t)b << 16; float r; memcpy(&r, &u, 4); return r;
+}
+
+/* ------------------------------------------------------------------ exp */
+/* exp(x) in IEEE single operations only: n = floor(x*log2e + 1/2), r = x - n*ln2 (Cody-Waite, two
+ * constants), e^r by a degree-7 Taylor polynomial in Horner form with fma, times 2^n applied in two
+ * exact halves.  Results below 2^-125 are returned as 0 (no subnormal outputs); x > 88.72283 gives inf. */
+static inline float mk_expf(float x) {
+  if (!(x > -87.0f)) return (x != x) ? x : 0.0f;
+  if (x > 88.72283f) return INFINITY;
+  const float n = floorf(fmaf(x, 1.44269504f, 0.5f));
+  float r = fmaf(n, -0.693359375f, x);
+  r = fmaf(n, 2.12194440e-4f, r);
+  float p = 1.98412698e-4f;                 /* 1/5040 */
+  p = fmaf(p, r, 1.38888889e-3f);           /* 1/720  */
+  p = fmaf(p, r, 8.33333333e-3f);           /* 1/120  */
+  p = fmaf(p, r, 4.16666667e-2f);           /* 1/24   */
+  p = fmaf(p, r, 1.66666667e-1f);           /* 1/6    */
+  p = fmaf(p, r, 0.5f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
+  const int ni = (int)n, h = ni / 2, g = ni - h;
+  uint32_t b1 = (uint32_t)(h + 127) << 23, b2 = (uint32_t)(g + 127) << 23;
+  float s1, s2; memcpy(&s1, &b1, 4); memcpy(&s2, &b2, 4);
+  return (p * s1) * s2;
+}
+
+/* ------------------------------------------------------------------ seeded generator */
+/* splitmix64 (Steele, Lea, Flood 2014): output i of the stream with state `key` is mix(key + (i+1)*gamma). */
+static inline uint64_t mix64(uint64_t z) {
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+static inline uint64_t stream_key(uint64_t seed, uint64_t stream) { return mix64(mix64(seed) ^ stream); }
+static inline uint64_t stream_bits(uint64_t key, uint64_t i) { return mix64(key + (i + 1) * 0x9E3779B97F4A7C15ull); }
+
+/* ln(u), u in (0, 1]: u = m * 2^e with m in [sqrt(1/2), sqrt(2)), ln m = 2 atanh(s), s = (m-1)/(m+1). */
+static inline float mk_logf(float u) {
+  uint32_t b; memcpy(&b, &u, 4);
+  int e = (int)((b >> 23) & 0xFF) - 127;
+  uint32_t mb = (b & 0x007FFFFFu) | 0x3F800000u;
+  float m; memcpy(&m, &mb, 4);
+  if (m > 1.41421356f) { m = m * 0.5f; e += 1; }
+  const float s = (m - 1.0f) / (m + 1.0f), s2 = s * s;
+  float p = 7.69230769e-2f;                 /* 1/13 */
+  p = fmaf(p, s2, 9.09090909e-2f);          /* 1/11 */
+  p = fmaf(p, s2, 1.11111111e-1f);          /* 1/9  */
+  p = fmaf(p, s2, 1.42857143e-1f);          /* 1/7  */
+  p = fmaf(p, s2, 2.00000000e-1f);          /* 1/5  */
+  p = fmaf(p, s2, 3.33333333e-1f);          /* 1/3  */
+  p = fmaf(p, s2, 1.0f);
+  const float lnm = 2.0f * s * p;
+  const float fe = (float)e;
+  return fmaf(fe, 0.693145752f, fmaf(fe, 1.42860677e-6f, lnm));
+}
+/* sin and cos of phi in [0, pi/2) by Taylor polynomials (degrees 13 and 14) in Horner form with fma. */
+static inline void mk_sincos_q(float phi, float* s, float* c) {
+  const float x2 = phi * phi;
+  float ps = 1.60590438e-10f;               /*  1/13! */
+  ps = fmaf(ps, x2, -2.50521084e-8f);       /* -1/11! */
+  ps = fmaf(ps, x2, 2.75573192e-6f);        /*  1/9!  */
+  ps = fmaf(ps, x2, -1.98412698e-4f);       /* -1/7!  */
+  ps = fmaf(ps, x2, 8.33333333e-3f);        /*  1/5!  */
+  ps = fmaf(ps, x2, -1.66666667e-1f);       /* -1/3!  */
+  ps = fmaf(ps, x2, 1.0f);
+  *s = phi * ps;
+  float pc = -1.14707456e-11f;              /* -1/14! */
+  pc = fmaf(pc, x2, 2.08767570e-9f);        /*  1/12! */
+  pc = fmaf(pc, x2, -2.75573192e-7f);       /* -1/10! */
+  pc = fmaf(pc, x2, 2.48015873e-5f);        /*  1/8!  */
+  pc = fmaf(pc, x2, -1.38888889e-3f);       /* -1/6!  */
+  pc = fmaf(pc, x2, 4.16666667e-2f);        /*  1/4!  */
+  pc = fmaf(pc, x2, -0.5f);                 /* -1/2!  */
+  pc = fmaf(pc, x2, 1.0f);
+  *c = pc;
+}
+/* standard normal for element i of a stream: pair i/2 gives (r cos t, r sin t) by Box-Muller. */
+static inline float mk_normal(uint64_t key, uint64_t i) {
+  const uint64_t bits = stream_bits(key, i >> 1);
+  const uint32_t a = (uint32_t)(bits >> 40), b = (uint32_t)((bits >> 16) & 0xFFFFFFu);
+  const float u1 = (float)(a + 1u) * 5.96046448e-8f;          /* 2^-24 */
+  const float r = sqrtf(-2.0f * mk_logf(u1));
+  const uint32_t q = b >> 22;
+  const float phi = (float)(b & 0x3FFFFFu) * 2.38418579e-7f * 1.57079637f;   /* 2^-22 * pi/2 */
+  float s, c; mk_sincos_q(phi, &s, &c);
+  float cs, sn;
+  switch (q) { case 0: cs = c; sn = s; break; case 1: cs = -s; sn = c; break;
+               case 2: cs = -c; sn = -s; break; default: cs = s; sn = -c; break; }
+  return r * ((i & 1) ? sn : cs);
+}
+
+EXPORT uint64_t orc_splitmix64(uint64_t state, uint64_t i) { return stream_bits(state, i); }
+EXPORT uint64_t orc_stream_key(uint64_t seed, uint64_t stream) { return stream_key(seed, stream); }
+EXPORT float orc_expf(float x) { return mk_expf(x); }
+EXPORT float orc_logf(float x) { return mk_logf(x); }
+EXPORT void orc_sincos_q(float phi, float* s, float* c) { mk_sincos_q(phi, s, c); }
+
+/* n values of stream `stream` starting at element `start`, bf16(scale * z) (natural element order). */
+EXPORT void orc_gen_normal_bf16(uint64_t seed, uint64_t stream, uint64_t start, uint64_t n, float scale, uint16_t* out) {
+  const uint64_t key = stream_key(seed, stream);
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < (int64_t)n; ++i) out[i] = f2bf(scale * mk_normal(key, start + (uint64_t)i));
+}
+EXPORT void orc_gen_normal_f32(uint64_t seed, uint64_t stream, uint64_t start, uint64_t n, float* out) {
+  const uint64_t key = stream_key(seed, stream);
+  for (uint64_t i = 0; i < n; ++i) out[i] = mk_normal(key, start + i);
+}
+/* uniform integers in [0, bound): (top 32 bits * bound) >> 32 */
+EXPORT void orc_gen_tokens(uint64_t seed, uint64_t stream, uint64_t n, uint32_t bound, int32_t* out) {
+  const uint64_t key = stream_key(seed, stream);
+  for (uint64_t i = 0; i < n; ++i) out[i] = (int32_t)(((stream_bits(key, i) >> 32) * (uint64_t)bound) >> 32);
+}
+
+/* ------------------------------------------------------------------ reductions */
+static inline float butterfly64(float* a) {
+  for (int off = 32; off; off >>= 1) {
+    float t[64];
+    for (int l = 0; l < 64; ++l) t[l] = a[l] + a[l ^ off];
+    memcpy(a, t, sizeof t);
+  }
+  return a[0];
+}
+/* canonical dot: w bf16, x fp32 (bf16-valued in every use), K a multiple of 64 */
+static inline float dot64(const uint16_t* w, const float* x, int K) {
+  float acc[64];
+  for (int l = 0; l < 64; ++l) acc[l] = 0.0f;
+  for (int k0 = 0; k0 < K; k0 += 64)
+    for (int l = 0; l < 64; ++l) acc[l] = fmaf(bf2f(w[k0 + l]), x[k0 + l], acc[l]);
+  return butterfly64(acc);
+}
+static inline float sumsq64(const float* x, int K) {
+  float acc[64];
+  for (int l = 0; l < 64; ++l) acc[l] = 0.0f;
+  for (int k0 = 0; k0 < K; k0 += 64)
+    for (int l = 0; l < 64; ++l) acc[l] = fmaf(x[k0 + l], x[k0 + l], acc[l]);
+  return butterfly64(acc);
+}
+/* sum over n values in the same 64-lane pattern with plain adds (n need not be a multiple of 64) */
+static inline float sum64(const float* v, int n) {
+  float acc[64];
+  for (int l = 0; l < 64; ++l) acc[l] = 0.0f;
+  for (int k = 0; k < n; ++k) acc[k & 63] = acc[k & 63] + v[k];
+  return butterfly64(acc);
+}
+EXPORT float orc_dot64(const uint16_t* w, const float* x, int K) { return dot64(w, x, K); }
+EXPORT float orc_sum64(const float* v, int n) { return sum64(v, n); }
+
+/* ------------------------------------------------------------------ model pieces */
+/* ref_numpy.py:71-73 rmsnorm: r = 1/sqrt(mean(x^2) + eps); out = bfr(w * bfr(x * r)) */
+static void rmsnorm(const float* x, const uint16_t* w, int n, float eps, float* out) {
+  const float ss = sumsq64(x, n);
+  const float r = 1.0f / sqrtf(ss / (float)n + eps);
+  for (int i = 0; i < n; ++i) out[i] = bfr((w ? bf2f(w[i]) : 1.0f) * bfr(x[i] * r));
+}
+EXPORT void orc_rmsnorm(const float* x, const uint16_t* w, int n, float eps, float* out) { rmsnorm(x, w, n, eps, out); }
+
+/* ref_numpy.py:76-81 rope_tables: inv = 1/theta^(2i/hd), f = pos*inv (fp32), bf16(cos f), bf16(sin f) */
+EXPORT void orc_rope_tables(float theta, int hd, int ctx, float* cos_out, float* sin_out) {
+  const int half = hd / 2;
+  for (int i = 0; i < half; ++i) {
+    const float inv = 1.0f / powf(theta, (float)(2 * i) / (float)hd);
+    for (int p = 0; p < ctx; ++p) {
+      const float f = (float)p * inv;
+      cos_out[(size_t)p * half + i] = bfr(cosf(f));
+      sin_out[(size_t)p * half + i] = bfr(sinf(f));
+    }
+  }
+}
+/* ref_numpy.py:84-88 apply_rope (rotate_half): bfr(bfr(v*c) + bfr(rot*s)) */
+static void apply_rope(float* v, int hd, const float* cs, const float* sn) {
+  const int half = hd / 2;
+  float t[512];
+  for (int d = 0; d < hd; ++d) {
+    const int i = d < half ? d : d - half;
+    const float rot = d < half ? -v[d + half] : v[d - half];
+    t[d] = bfr(bfr(v[d] * cs[i]) + bfr(rot * sn[i]));
+  }
+  memcpy(v, t, sizeof(float) * (size_t)hd);
+}
+EXPORT void orc_apply_rope(float* v, int hd, const float* cs, const float* sn) { apply_rope(v, hd, cs, sn); }
+
+/* ref_numpy.py:91-92 silu */
+static inline float silu(float g) { return g / (1.0f + mk_expf(-g)); }
+EXPORT float orc_silu(float g) { return silu(g); }
+
+/* paged KV addressing (etx/ops/attnprep.py:146-168; etx/importer/spec.py:274-281):
+ * K [block][NKV][HD/8][BS][8], V [block][NKV][HD][BS]; physical block = block_table[pos / BS]. */
+static inline size_t kv_k_index(int blk, int off, int h, int d, int NKV, int HD, int BS) {
+  return ((((size_t)blk * NKV + h) * (HD / 8) + d / 8) * BS + off) * 8 + d % 8;
+}
+static inline size_t kv_v_index(int blk, int off, int h, int d, int NKV, int HD, int BS) {
+  return (((size_t)blk * NKV + h) * HD + d) * BS + off;
+}
+EXPORT int64_t orc_kv_k_index(int blk, int off, int h, int d, int NKV, int HD, int BS) { return (int64_t)kv_k_index(blk, off, h, d, NKV, HD, BS); }
+EXPORT int64_t orc_kv_v_index(int blk, int off, int h, int d, int NKV, int HD, int BS) { return (int64_t)kv_v_index(blk, off, h, d, NKV, HD, BS); }
+
+#define ATT_CHUNK 64
+/* one q head over positions 0..n-1 of kv head `h` (ref_numpy.py:122-129 in the chunked order above).
+ * `q` is bf16-valued fp32 [HD]; the scale is fp32(1/sqrt(HD)) applied after the dot, as the reference does. */
+static void attention_head(const float* q, const uint16_t* kc, const uint16_t* vc, const int32_t* btab,
+                           int n, int h, int NKV, int HD, int BS, float* o) {
+  const float scale = (float)(1.0 / sqrt((double)HD));
+  float A[512], a[512];
+  float L = 0.0f, M = -INFINITY;
+  const int nch = (n + ATT_CHUNK - 1) / ATT_CHUNK;
+  float mc[4096];
+  for (int c = 0; c < nch; ++c) {
+    const int t0 = c * ATT_CHUNK, t1 = t0 + ATT_CHUNK < n ? t0 + ATT_CHUNK : n;
+    float m = -INFINITY;
+    for (int t = t0; t < t1; ++t) {
+      const int blk = btab[t / BS], off = t % BS;
+      float s = 0.0f;
+      for (int d = 0; d < HD; ++d) s = fmaf(q[d], bf2f(kc[kv_k_index(blk, off, h, d, NKV, HD, BS)]), s);
+      s = s * scale;
+      if (s > m) m = s;
+    }
+    mc[c] = m;
+    if (m > M) M = m;
+  }
+  for (int d = 0; d < HD; ++d) A[d] = 0.0f;
+  for (int c = 0; c < nch; ++c) {
+    const int t0 = c * ATT_CHUNK, t1 = t0 + ATT_CHUNK < n ? t0 + ATT_CHUNK : n;
+    float l = 0.0f;
+    for (int d = 0; d < HD; ++d) a[d] = 0.0f;
+    for (int t = t0; t < t1; ++t) {
+      const int blk = btab[t / BS], off = t % BS;
+      float s = 0.0f;
+      for (int d = 0; d < HD; ++d) s = fmaf(q[d], bf2f(kc[kv_k_index(blk, off, h, d, NKV, HD, BS)]), s);
+      s = s * scale;
+      const float p = mk_expf(s - mc[c]);
+      l = l + p;
+      for (int d = 0; d < HD; ++d) a[d] = fmaf(p, bf2f(vc[kv_v_index(blk, off, h, d, NKV, HD, BS)]), a[d]);
+    }
+    const float w = mk_expf(mc[c] - M);
+    L = fmaf(w, l, L);
+    for (int d = 0; d < HD; ++d) A[d] = fmaf(w, a[d], A[d]);
+  }
+  for (int d = 0; d < HD; ++d) o[d] = bfr(A[d] / L);
+}
+EXPORT void orc_attention_head(const float* q, const uint16_t* kc, const uint16_t* vc, const int32_t* btab,
+                               int n, int h, int NKV, int HD, int BS, float* o) {
+  attention_head(q, kc, vc, btab, n, h, NKV, HD, BS, o);
+}
+
+/* ref_numpy.py:135-140: fp32 softmax over E logits, top-k by probability with ties to the lower id,
+ * optional renormalisation (selection-order sum), bf16 weights. */
+static void route(const float* logits, int E, int K, int renorm, int32_t* ids, float* wts) {
+  float M = -INFINITY;
+  for (int e = 0; e < E; ++e) if (logits[e] > M) M = logits[e];
+  float p[1024];
+  for (int e = 0; e < E; ++e) p[e] = mk_expf(logits[e] - M);
+  const float S = sum64(p, E);
+  for (int e = 0; e < E; ++e) p[e] = p[e] / S;
+  unsigned char taken[1024] = {0};
+  float sel = 0.0f, wv[64];
+  for (int k = 0; k < K; ++k) {
+    int bi = -1; float bv = -1.0f;
+    for (int e = 0; e < E; ++e) if (!taken[e] && p[e] > bv) { bv = p[e]; bi = e; }
+    taken[bi] = 1; ids[k] = bi; wv[k] = bv; sel = sel + bv;
+  }
+  for (int k = 0; k < K; ++k) wts[k] = bfr(renorm ? wv[k] / sel : wv[k]);
+}
+EXPORT void orc_route(const float* logits, int E, int K, int renorm, int32_t* ids, float* wts) { route(logits, E, K, renorm, ids, wts); }
+
+/* ------------------------------------------------------------------ model */
+typedef struct {
+  int32_t H, NH, NKV, HD, I, E, TOPK, MI, L, V;
+  int32_t moe, qk_norm, norm_topk, block_size, max_ctx, batch;
+  float eps, theta;
+} orc_config;
+
+/* tensor streams of the seeded generator: kind << 48 | (layer + 1) << 24 | expert */
+enum { S_EMBED = 1, S_LMHEAD = 2, S_WQKV = 3, S_WO = 4, S_ROUTER = 5, S_W13 = 6, S_W2 = 7, S_WGU = 8, S_WD = 9,
+       S_KINIT = 10, S_VINIT = 11, S_XIN = 12, S_PROMPT = 13 };
+static inline uint64_t sid(int kind, int layer, int expert) {
+  return ((uint64_t)kind << 48) | ((uint64_t)(layer + 1) << 24) | (uint64_t)expert;
+}
+EXPORT uint64_t orc_stream_id(int kind, int layer, int expert) { return sid(kind, layer, expert); }
+
+typedef struct {
+  uint16_t *wqkv, *wo, *wr, *wgu, *wd;
+  uint16_t **w13, **w2;           /* per expert, generated on first use */
+  uint16_t *kc, *vc;
+} orc_layer;
+
+typedef struct {
+  orc_config c;
+  uint64_t seed;
+  uint16_t *embed, *lm_head;
+  orc_layer* ly;
+  int32_t* btab;
+  int nblocks;
+  float *rcos, *rsin;
+  float scale;
+} orc_model;
+
+static uint16_t* gen_tensor(uint64_t seed, uint64_t stream, size_t n, float scale) {
+  uint16_t* p = (uint16_t*)malloc(n * sizeof(uint16_t));
+  if (p) orc_gen_normal_bf16(seed, stream, 0, n, scale, p);
+  return p;
+}
+
+EXPORT void* orc_model_create(const orc_config* cfg, uint64_t seed, float wscale) {
+  orc_model* m = (orc_model*)calloc(1, sizeof(orc_model));
+  m->c = *cfg; m->seed = seed; m->scale = wscale;
+  const orc_config* c = &m->c;
+  const int NQKV = (c->NH + 2 * c->NKV) * c->HD;
+  m->embed = gen_tensor(seed, sid(S_EMBED, -1, 0), (size_t)c->V * c->H, wscale);
+  m->lm_head = gen_tensor(seed, sid(S_LMHEAD, -1, 0), (size_t)c->V * c->H, wscale);
+  m->nblocks = (c->max_ctx + c->block_size - 1) / c->block_size;
+  m->btab = (int32_t*)malloc(sizeof(int32_t) * (size_t)m->nblocks);
+  for (int i = 0; i < m->nblocks; ++i) m->btab[i] = i;
+  m->ly = (orc_layer*)calloc((size_t)c->L, sizeof(orc_layer));
+  const size_t kvn = (size_t)m->nblocks * c->block_size * c->NKV * c->HD;
+  for (int l = 0; l < c->L; ++l) {
+    orc_layer* y = &m->ly[l];
+    y->wqkv = gen_tensor(seed, sid(S_WQKV, l, 0), (size_t)NQKV * c->H, wscale);
+    y->wo = gen_tensor(seed, sid(S_WO, l, 0), (size_t)c->H * c->NH * c->HD, wscale);
+    if (c->moe) {
+      y->wr = gen_tensor(seed, sid(S_ROUTER, l, 0), (size_t)c->E * c->H, wscale);
+      y->w13 = (uint16_t**)calloc((size_t)c->E, sizeof(uint16_t*));
+      y->w2 = (uint16_t**)calloc((size_t)c->E, sizeof(uint16_t*));
+    } else {
+      y->wgu = gen_tensor(seed, sid(S_WGU, l, 0), (size_t)2 * c->I * c->H, wscale);
+      y->wd = gen_tensor(seed, sid(S_WD, l, 0), (size_t)c->H * c->I, wscale);
+    }
+    y->kc = (uint16_t*)calloc(kvn, sizeof(uint16_t));
+    y->vc = (uint16_t*)calloc(kvn, sizeof(uint16_t));
+  }
+  const int half = c->HD / 2;
+  m->rcos = (float*)malloc(sizeof(float) * (size_t)c->max_ctx * half);
+  m->rsin = (float*)malloc(sizeof(float) * (size_t)c->max_ctx * half);
+  orc_rope_tables(c->theta, c->HD, c->max_ctx, m->rcos, m->rsin);
+  return m;
+}
+
+EXPORT void orc_model_destroy(void* h) {
+  orc_model* m = (orc_model*)h;
+  if (!m) return;
+  for (int l = 0; l < m->c.L; ++l) {
+    orc_layer* y = &m->ly[l];
+    free(y->wqkv); free(y->wo); free(y->wr); free(y->wgu); free(y->wd); free(y->kc); free(y->vc);
+    if (y->w13) for (int e = 0; e < m->c.E; ++e) { free(y->w13[e]); free(y->w2[e]); }
+    free(y->w13); free(y->w2);
+  }
+  free(m->ly); free(m->embed); free(m->lm_head); free(m->btab); free(m->rcos); free(m->rsin); free(m);
+}
+
+/* block table override: physical block of logical block i */
+EXPORT void orc_set_block_table(void* h, const int32_t* bt, int n) {
+  orc_model* m = (orc_model*)h;
+  for (int i = 0; i < n && i < m->nblocks; ++i) m->btab[i] = bt[i];
+}
+EXPORT int orc_num_blocks(void* h) { return ((orc_model*)h)->nblocks; }
+EXPORT const uint16_t* orc_kcache(void* h, int layer) { return ((orc_model*)h)->ly[layer].kc; }
+EXPORT const uint16_t* orc_vcache(void* h, int layer) { return ((orc_model*)h)->ly[layer].vc; }
+
+/* fill positions [0, n) of every layer's cache with bf16 N(0,1) (the single-layer configuration) */
+EXPORT void orc_fill_kv_random(void* h, int n) {
+  orc_model* m = (orc_model*)h; const orc_config* c = &m->c;
+  const int NKV = c->NKV, HD = c->HD, BS = c->block_size;
+  for (int l = 0; l < c->L; ++l) {
+    const uint64_t kk = stream_key(m->seed, sid(S_KINIT, l, 0)), vk = stream_key(m->seed, sid(S_VINIT, l, 0));
+#pragma omp parallel for schedule(static)
+    for (int t = 0; t < n; ++t)
+      for (int hh = 0; hh < NKV; ++hh)
+        for (int d = 0; d < HD; ++d) {
+          const uint64_t idx = ((uint64_t)t * NKV + hh) * HD + d;
+          const int blk = m->btab[t / BS], off = t % BS;
+          m->ly[l].kc[kv_k_index(blk, off, hh, d, NKV, HD, BS)] = f2bf(mk_normal(kk, idx));
+          m->ly[l].vc[kv_v_index(blk, off, hh, d, NKV, HD, BS)] = f2bf(mk_normal(vk, idx));
+        }
+  }
+}
+
+static void ensure_expert(orc_model* m, int l, int e) {
+  const orc_config* c = &m->c;
+  orc_layer* y = &m->ly[l];
+  if (!y->w13[e]) y->w13[e] = gen_tensor(m->seed, sid(S_W13, l, e), (size_t)2 * c->MI * c->H, m->scale);
+  if (!y->w2[e]) y->w2[e] = gen_tensor(m->seed, sid(S_W2, l, e), (size_t)c->H * c->MI, m->scale);
+}
+
+/* GEMV rows [0, R) into out, rounding each to bf16 */
+static void gemv_bf(const uint16_t* W, int R, int K, const float* x, float* out) {
+#pragma omp parallel for schedule(static)
+  for (int r = 0; r < R; ++r) out[r] = bfr(dot64(W + (size_t)r * K, x, K));
+}
+
+/* one decoder layer at position pos on residual x (in place); dump_ids / dump_wts / dump_logits optional */
+static void layer_step(orc_model* m, int l, float* x, int pos, int32_t* ids_out, float* wts_out, float* logits_out) {
+  const orc_config* c = &m->c;
+  orc_layer* y = &m->ly[l];
+  const int H = c->H, NH = c->NH, NKV = c->NKV, HD = c->HD, G = NH / NKV, BS = c->block_size;
+  const int NQKV = (NH + 2 * NKV) * HD;
+  float* xs = (float*)malloc(sizeof(float) * (size_t)(H > c->I ? H : c->I) * 2 + 64);
+  float* qkv = (float*)malloc(sizeof(float) * (size_t)NQKV);
+  float* o = (float*)malloc(sizeof(float) * (size_t)NH * HD);
+  rmsnorm(x, NULL, H, c->eps, xs);                                 /* input_layernorm (weight 1.0) */
+  gemv_bf(y->wqkv, NQKV, H, xs, qkv);                               /* :112-115 */
+  const float* cs = m->rcos + (size_t)pos * (HD / 2);
+  const float* sn = m->rsin + (size_t)pos * (HD / 2);
+  float tmp[512];
+  for (int hh = 0; hh < NH + NKV; ++hh) {                          /* :116-120 q/k norm, RoPE */
+    float* v = qkv + (size_t)hh * HD;
+    if (c->qk_norm) { rmsnorm(v, NULL, HD, c->eps, tmp); memcpy(v, tmp, sizeof(float) * (size_t)HD); }
+    apply_rope(v, HD, cs, sn);
+  }
+  const int blk = m->btab[pos / BS], off = pos % BS;               /* :121 KV append, paged */
+  for (int hh = 0; hh < NKV; ++hh)
+    for (int d = 0; d < HD; ++d) {
+      y->kc[kv_k_index(blk, off, hh, d, NKV, HD, BS)] = f2bf(qkv[(size_t)(NH + hh) * HD + d]);
+      y->vc[kv_v_index(blk, off, hh, d, NKV, HD, BS)] = f2bf(qkv[(size_t)(NH + NKV + hh) * HD + d]);
+    }
+#pragma omp parallel for schedule(static)
+  for (int hh = 0; hh < NH; ++hh)                                   /* :122-129 */
+    attention_head(qkv + (size_t)hh * HD, y->kc, y->vc, m->btab, pos + 1, hh / G, NKV, HD, BS, o + (size_t)hh * HD);
+  float* t = (float*)malloc(sizeof(float) * (size_t)(H > c->I ? H : c->I) * 2 + 64);
+  gemv_bf(y->wo, H, NH * HD, o, t);                                 /* :130 */
+  for (int i = 0; i < H; ++i) x[i] = bfr(x[i] + t[i]);
+  rmsnorm(x, NULL, H, c->eps, xs);                                 /* :131 post_attention_layernorm */
+  if (c->moe) {
+    const int E = c->E, K = c->TOPK, MI = c->MI;
+    float logits[1024];
+    gemv_bf(y->wr, E, H, xs, logits);                                /* :134 */
+    if (logits_out) memcpy(logits_out, logits, sizeof(float) * (size_t)E);
+    int32_t ids[64]; float wts[64];
+    route(logits, E, K, c->norm_topk, ids, wts);                     /* :135-140 */
+    if (ids_out) memcpy(ids_out, ids, sizeof(int32_t) * (size_t)K);
+    if (wts_out) memcpy(wts_out, wts, sizeof(float) * (size_t)K);
+    for (int k = 0; k < K; ++k) ensure_expert(m, l, ids[k]);
+    int order[64];                                                   /* :141 ascending expert id */
+    for (int k = 0; k < K; ++k) order[k] = k;
+    for (int a = 1; a < K; ++a)
+      for (int b = a; b > 0 && ids[order[b]] < ids[order[b - 1]]; --b) { int q = order[b]; order[b] = order[b - 1]; order[b - 1] = q; }
+    float* hbuf = (float*)malloc(sizeof(float) * (size_t)K * MI);
+    float* ys = (float*)malloc(sizeof(float) * (size_t)K * H);
+    for (int k = 0; k < K; ++k) {                                    /* :142-146 */
+      const uint16_t* W13 = y->w13[ids[k]];
+      float* hk = hbuf + (size_t)k * MI;
+#pragma omp parallel for schedule(static)
+      for (int j = 0; j < MI; ++j) {
+        const float g = bfr(dot64(W13 + (size_t)(2 * j) * H, xs, H));
+        const float u = bfr(dot64(W13 + (size_t)(2 * j + 1) * H, xs, H));
+        hk[j] = bfr(bfr(silu(g)) * u);
+      }
+      const uint16_t* W2 = y->w2[ids[k]];
+#pragma omp parallel for schedule(static)
+      for (int i = 0; i < H; ++i) ys[(size_t)k * H + i] = bfr(bfr(dot64(W2 + (size_t)i * MI, hk, MI)) * wts[k]);
+    }
+    for (int i = 0; i < H; ++i) {                                    /* :146-148 */
+      float acc = 0.0f;
+      for (int k = 0; k < K; ++k) acc = bfr(acc + ys[(size_t)order[k] * H + i]);
+      x[i] = bfr(x[i] + acc);
+    }
+    free(hbuf); free(ys);
+  } else {                                                           /* :149-152 */
+    const int I = c->I;
+    float* hb = (float*)malloc(sizeof(float) * (size_t)I);
+#pragma omp parallel for schedule(static)
+    for (int j = 0; j < I; ++j) {
+      const float g = bfr(dot64(y->wgu + (size_t)(2 * j) * H, xs, H));
+      const float u = bfr(dot64(y->wgu + (size_t)(2 * j + 1) * H, xs, H));
+      hb[j] = bfr(bfr(silu(g)) * u);
+    }
+    gemv_bf(y->wd, H, I, hb, t);
+    for (int i = 0; i < H; ++i) x[i] = bfr(x[i] + t[i]);
+    free(hb);
+  }
+  free(xs); free(qkv); free(o); free(t);
+}
+
+/* ref_numpy.py:105-158 Ref.step: token at position pos -> greedy next token.
+ * dump_x [L][H] residual after each layer; dump_ids/dump_wts [L][TOPK]; each may be NULL. */
+EXPORT int32_t orc_step(void* h, int32_t tok, int pos, float* dump_x, int32_t* dump_ids, float* dump_wts) {
+  orc_model* m = (orc_model*)h; const orc_config* c = &m->c;
+  const int H = c->H;
+  float* x = (float*)malloc(sizeof(float) * (size_t)H);
+  for (int i = 0; i < H; ++i) x[i] = bf2f(m->embed[(size_t)tok * H + i]);
+  for (int l = 0; l < c->L; ++l) {
+    layer_step(m, l, x, pos, dump_ids ? dump_ids + (size_t)l * c->TOPK : NULL,
+               dump_wts ? dump_wts + (size_t)l * c->TOPK : NULL, NULL);
+    if (dump_x) memcpy(dump_x + (size_t)l * H, x, sizeof(float) * (size_t)H);
+  }
+  float* xs = (float*)malloc(sizeof(float) * (size_t)H);
+  rmsnorm(x, NULL, H, c->eps, xs);                                  /* :155 final norm (weight 1.0) */
+  const int V = c->V;
+  float* lg = (float*)malloc(sizeof(float) * (size_t)V);
+  gemv_bf(m->lm_head, V, H, xs, lg);                                 /* :157 */
+  int best = 0;
+  for (int v = 1; v < V; ++v) if (lg[v] > lg[best]) best = v;        /* :158 first maximum */
+  free(x); free(xs); free(lg);
+  return best;
+}
+
+/* the single-layer configuration: run layer `l` on the given residual x (in place) at position pos */
+EXPORT void orc_layer_step(void* h, int l, float* x, int pos, int32_t* ids_out, float* wts_out, float* logits_out) {
+  layer_step((orc_model*)h, l, x, pos, ids_out, wts_out, logits_out);
+}
+
+/* generate every expert of every layer now (so that timing excludes generation) */
+EXPORT void orc_materialize_experts(void* h) {
+  orc_model* m = (orc_model*)h;
+  if (!m->c.moe) return;
+  for (int l = 0; l < m->c.L; ++l)
+    for (int e = 0; e < m->c.E; ++e) ensure_expert(m, l, e);
+}
+
+/* raw weight access for tests (natural layout); expert tensors are generated on first use */
+EXPORT const uint16_t* orc_weight(void* h, int kind, int l, int e) {
+  orc_model* m = (orc_model*)h;
+  switch (kind) {
+    case S_EMBED: return m->embed;
+    case S_LMHEAD: return m->lm_head;
+    case S_WQKV: return m->ly[l].wqkv;
+    case S_WO: return m->ly[l].wo;
+    case S_ROUTER: return m->ly[l].wr;
+    case S_W13: ensure_expert(m, l, e); return m->ly[l].w13[e];
+    case S_W2: ensure_expert(m, l, e); return m->ly[l].w2[e];
+    case S_WGU: return m->ly[l].wgu;
+    case S_WD: return m->ly[l].wd;
+    default: return NULL;
+  }
+}
+EXPORT int orc_num_threads(void) { return omp_get_max_threads(); }

@@ -1,0 +1,236 @@
+"""ctypes view of the CPU oracle (oracle/mk_oracle.c).  TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import this module; it is the
+checker the HIP library is compared against, never part of the product path.  It restates
+examples/llm/ref_numpy.py (Ref.step, :105-158) of the reference; see mk_oracle.c for the fixed
+evaluation order.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB = HERE / "build" / "liboracle.so"
+
+# tensor kinds of the seeded generator (stream id = kind << 48 | (layer + 1) << 24 | expert)
+S_EMBED, S_LMHEAD, S_WQKV, S_WO, S_ROUTER, S_W13, S_W2, S_WGU, S_WD, S_KINIT, S_VINIT, S_XIN, S_PROMPT = range(1, 14)
+
+
+class OrcConfig(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in ("H", "NH", "NKV", "HD", "I", "E", "TOPK", "MI", "L", "V",
+                                          "moe", "qk_norm", "norm_topk", "block_size", "max_ctx", "batch")] + \
+               [("eps", C.c_float), ("theta", C.c_float)]
+
+
+def build(force: bool = False) -> Path:
+    if force or not LIB.exists() or LIB.stat().st_mtime < (HERE / "mk_oracle.c").stat().st_mtime:
+        subprocess.run(["make", "-s", "-C", str(HERE)] + (["-B"] if force else []), check=True)
+    return LIB
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not LIB.exists():
+            build()
+        L = C.CDLL(str(LIB))
+        u16p, f32p, i32p = (np.ctypeslib.ndpointer(t, flags="C_CONTIGUOUS") for t in (np.uint16, np.float32, np.int32))
+        sig = {
+            "orc_splitmix64": (C.c_uint64, [C.c_uint64, C.c_uint64]),
+            "orc_stream_key": (C.c_uint64, [C.c_uint64, C.c_uint64]),
+            "orc_stream_id": (C.c_uint64, [C.c_int, C.c_int, C.c_int]),
+            "orc_expf": (C.c_float, [C.c_float]),
+            "orc_logf": (C.c_float, [C.c_float]),
+            "orc_silu": (C.c_float, [C.c_float]),
+            "orc_sincos_q": (None, [C.c_float, C.POINTER(C.c_float), C.POINTER(C.c_float)]),
+            "orc_gen_normal_bf16": (None, [C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint64, C.c_float, u16p]),
+            "orc_gen_normal_f32": (None, [C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint64, f32p]),
+            "orc_gen_tokens": (None, [C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint32, i32p]),
+            "orc_dot64": (C.c_float, [u16p, f32p, C.c_int]),
+            "orc_sum64": (C.c_float, [f32p, C.c_int]),
+            "orc_rmsnorm": (None, [f32p, C.c_void_p, C.c_int, C.c_float, f32p]),
+            "orc_rope_tables": (None, [C.c_float, C.c_int, C.c_int, f32p, f32p]),
+            "orc_apply_rope": (None, [f32p, C.c_int, f32p, f32p]),
+            "orc_attention_head": (None, [f32p, u16p, u16p, i32p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, f32p]),
+            "orc_route": (None, [f32p, C.c_int, C.c_int, C.c_int, i32p, f32p]),
+            "orc_kv_k_index": (C.c_int64, [C.c_int] * 7),
+            "orc_kv_v_index": (C.c_int64, [C.c_int] * 7),
+            "orc_model_create": (C.c_void_p, [C.POINTER(OrcConfig), C.c_uint64, C.c_float]),
+            "orc_model_destroy": (None, [C.c_void_p]),
+            "orc_set_block_table": (None, [C.c_void_p, i32p, C.c_int]),
+            "orc_num_blocks": (C.c_int, [C.c_void_p]),
+            "orc_kcache": (C.POINTER(C.c_uint16), [C.c_void_p, C.c_int]),
+            "orc_vcache": (C.POINTER(C.c_uint16), [C.c_void_p, C.c_int]),
+            "orc_fill_kv_random": (None, [C.c_void_p, C.c_int]),
+            "orc_step": (C.c_int32, [C.c_void_p, C.c_int32, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p]),
+            "orc_layer_step": (None, [C.c_void_p, C.c_int, f32p, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p]),
+            "orc_weight": (C.POINTER(C.c_uint16), [C.c_void_p, C.c_int, C.c_int, C.c_int]),
+            "orc_num_threads": (C.c_int, []),
+            "orc_materialize_experts": (None, [C.c_void_p]),
+        }
+        for name, (res, args) in sig.items():
+            f = getattr(L, name)
+            f.restype, f.argtypes = res, args
+        _lib = L
+    return _lib
+
+
+# ---------------------------------------------------------------- element helpers
+def bf16_bits_to_f32(b: np.ndarray) -> np.ndarray:
+    return (np.asarray(b, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    u = np.ascontiguousarray(np.asarray(x, np.float32)).view(np.uint32)
+    return ((u + np.uint32(0x7FFF) + ((u >> 16) & np.uint32(1))) >> 16).astype(np.uint16)
+
+
+def stream_id(kind: int, layer: int, expert: int = 0) -> int:
+    return (kind << 48) | ((layer + 1) << 24) | expert
+
+
+def gen_normal_bf16(seed: int, stream: int, n: int, start: int = 0, scale: float = 0.02) -> np.ndarray:
+    out = np.empty(n, np.uint16)
+    lib().orc_gen_normal_bf16(seed, stream, start, n, scale, out)
+    return out
+
+
+def gen_normal_f32(seed: int, stream: int, n: int, start: int = 0) -> np.ndarray:
+    out = np.empty(n, np.float32)
+    lib().orc_gen_normal_f32(seed, stream, start, n, out)
+    return out
+
+
+def gen_tokens(seed: int, n: int, bound: int, stream: int | None = None) -> np.ndarray:
+    out = np.empty(n, np.int32)
+    lib().orc_gen_tokens(seed, stream_id(S_PROMPT, -1) if stream is None else stream, n, bound, out)
+    return out
+
+
+def dot64(w_bits: np.ndarray, x: np.ndarray) -> float:
+    return float(lib().orc_dot64(np.ascontiguousarray(w_bits, np.uint16), np.ascontiguousarray(x, np.float32), len(x)))
+
+
+def rmsnorm(x: np.ndarray, eps: float, w_bits: np.ndarray | None = None) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty_like(x)
+    wp = None if w_bits is None else np.ascontiguousarray(w_bits, np.uint16).ctypes.data
+    lib().orc_rmsnorm(x, wp, len(x), eps, out)
+    return out
+
+
+def rope_tables(theta: float, hd: int, ctx: int):
+    c = np.empty((ctx, hd // 2), np.float32)
+    s = np.empty((ctx, hd // 2), np.float32)
+    lib().orc_rope_tables(theta, hd, ctx, c, s)
+    return c, s
+
+
+def apply_rope(v: np.ndarray, cos: np.ndarray, sin: np.ndarray) -> np.ndarray:
+    v = np.array(v, np.float32)
+    lib().orc_apply_rope(v, len(v), np.ascontiguousarray(cos, np.float32), np.ascontiguousarray(sin, np.float32))
+    return v
+
+
+def route(logits: np.ndarray, k: int, renorm: bool):
+    logits = np.ascontiguousarray(logits, np.float32)
+    ids = np.empty(k, np.int32)
+    w = np.empty(k, np.float32)
+    lib().orc_route(logits, len(logits), k, int(renorm), ids, w)
+    return ids, w
+
+
+def attention_head(q, kc, vc, btab, n, h, NKV, HD, BS):
+    o = np.empty(HD, np.float32)
+    lib().orc_attention_head(np.ascontiguousarray(q, np.float32), np.ascontiguousarray(kc, np.uint16),
+                             np.ascontiguousarray(vc, np.uint16), np.ascontiguousarray(btab, np.int32),
+                             n, h, NKV, HD, BS, o)
+    return o
+
+
+# ---------------------------------------------------------------- model
+class OracleModel:
+    """Seeded random-init decoder held on the CPU; step() is ref_numpy.py's Ref.step."""
+
+    def __init__(self, cfg: dict, seed: int, wscale: float = 0.02):
+        self.cfg = dict(cfg)
+        c = OrcConfig(**{k: cfg[k] for k, _ in OrcConfig._fields_})
+        self._h = lib().orc_model_create(C.byref(c), seed, wscale)
+        if not self._h:
+            raise MemoryError("oracle model allocation failed")
+
+    def close(self):
+        if self._h:
+            lib().orc_model_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        self.close()
+
+    def set_block_table(self, bt):
+        bt = np.ascontiguousarray(bt, np.int32)
+        lib().orc_set_block_table(self._h, bt, len(bt))
+
+    @property
+    def num_blocks(self) -> int:
+        return lib().orc_num_blocks(self._h)
+
+    def fill_kv_random(self, n: int):
+        lib().orc_fill_kv_random(self._h, n)
+
+    def kv(self, layer: int):
+        c = self.cfg
+        n = self.num_blocks * c["block_size"] * c["NKV"] * c["HD"]
+        k = np.ctypeslib.as_array(lib().orc_kcache(self._h, layer), shape=(n,)).copy()
+        v = np.ctypeslib.as_array(lib().orc_vcache(self._h, layer), shape=(n,)).copy()
+        return k, v
+
+    def weight(self, kind: int, layer: int = -1, expert: int = 0, shape=None) -> np.ndarray:
+        c = self.cfg
+        H, NQKV = c["H"], (c["NH"] + 2 * c["NKV"]) * c["HD"]
+        shapes = {S_EMBED: (c["V"], H), S_LMHEAD: (c["V"], H), S_WQKV: (NQKV, H), S_WO: (H, c["NH"] * c["HD"]),
+                  S_ROUTER: (c["E"], H), S_W13: (2 * c["MI"], H), S_W2: (H, c["MI"]),
+                  S_WGU: (2 * c["I"], H), S_WD: (H, c["I"])}
+        shp = shape or shapes[kind]
+        p = lib().orc_weight(self._h, kind, layer, expert)
+        return np.ctypeslib.as_array(p, shape=(int(np.prod(shp)),)).reshape(shp).copy()
+
+    def step(self, tok: int, pos: int, dump: bool = False):
+        c = self.cfg
+        if not dump:
+            return int(lib().orc_step(self._h, int(tok), int(pos), None, None, None))
+        x = np.empty((c["L"], c["H"]), np.float32)
+        k = max(c["TOPK"], 1)
+        ids = np.zeros((c["L"], k), np.int32)
+        w = np.zeros((c["L"], k), np.float32)
+        t = int(lib().orc_step(self._h, int(tok), int(pos), x.ctypes.data, ids.ctypes.data, w.ctypes.data))
+        return t, x, ids, w
+
+    def materialize_experts(self):
+        lib().orc_materialize_experts(self._h)
+
+    def layer_step(self, layer: int, x: np.ndarray, pos: int):
+        c = self.cfg
+        x = np.array(x, np.float32)
+        k = max(c["TOPK"], 1)
+        ids = np.zeros(k, np.int32)
+        w = np.zeros(k, np.float32)
+        lg = np.zeros(max(c["E"], 1), np.float32)
+        lib().orc_layer_step(self._h, layer, x, pos, ids.ctypes.data, w.ctypes.data, lg.ctypes.data)
+        return x, ids, w, lg
+
+
+def num_threads() -> int:
+    return int(lib().orc_num_threads())
+
+
+def env_threads() -> int:
+    return int(os.environ.get("OMP_NUM_THREADS", "0")) or num_threads()

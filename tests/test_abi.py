@@ -1,0 +1,53 @@
+"""The C ABI library: loads, exports every declared symbol, sizes and refuses shapes without a GPU."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from etx.runtime import native as N
+from etx.models import configs
+
+
+def test_library_exports_every_declared_symbol():
+    L = N.load()
+    names = N.declared_functions()
+    assert len(names) >= 20
+    missing = [n for n in names if not hasattr(L, n)]
+    assert not missing
+    assert L.etxmk_abi_version() == 1
+
+
+def test_sizes_of_real_configurations():
+    s = N.sizes(configs.QWEN3_30B_A3B)
+    c = configs.QWEN3_30B_A3B
+    per_layer = ((c.NH + 2 * c.NKV) * c.HD * c.H + c.H * c.NH * c.HD + c.E * c.H + c.E * 3 * c.MI * c.H) * 2
+    assert s["weights"] >= per_layer * c.L + 2 * c.V * c.H * 2
+    assert s["weights"] < per_layer * c.L * 1.01 + 2 * c.V * c.H * 2 + 1e6
+    assert s["kv"] == 2 * 2 * c.L * ((c.max_ctx + 15) // 16) * 16 * c.NKV * c.HD
+    s8 = N.sizes(configs.QWEN3_8B)
+    assert 15.0e9 < s8["weights"] < 16.5e9
+
+
+@pytest.mark.parametrize("bad", [dict(HD=64), dict(H=3000), dict(batch=2), dict(block_size=48), dict(max_ctx=10**6),
+                                 dict(TOPK=9), dict(E=0), dict(NKV=3)])
+def test_config_refused(bad):
+    d = configs.TINY_MOE.as_dict()
+    d.update(bad)
+    cfg = N.ModelConfig(**d)
+    with pytest.raises(N.EtxmkError) as e:
+        N.sizes(cfg)
+    assert e.value.code == N.EINVAL
+
+
+def test_unpermute_inverts_the_lane_permutation():
+    for K in (256, 768, 2048):
+        rng = np.random.default_rng(K)
+        nat = rng.integers(0, 2 ** 16, (3, K), dtype=np.uint16)
+        stored = np.empty_like(nat)
+        for base in range(0, K, 512):
+            S = min(512, K - base)
+            m = S // 64
+            for p in range(S):
+                lane, e = divmod(p, m)
+                stored[:, base + p] = nat[:, base + lane + 64 * e]
+        assert np.array_equal(N.unpermute_rows(stored), nat)
