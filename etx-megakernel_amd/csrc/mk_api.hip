@@ -128,7 +128,7 @@ WsLayout ws_layout(const etxmk_config* c) {
   const int hb = c->moe ? c->TOPK * c->MI : c->I;
   w.hbuf = take(4ull * (hb > 0 ? hb : 1));
   w.amax = take(8);
-  w.bar = take(4);
+  w.bar = take(4 * 64 * 17);          // 8 group counters, 1 global counter, 8 release flags; 256 B apart
   w.abort_w = take(4);
   w.tokens = take(4ull * (c->max_ctx + 1));
   w.out_tokens = take(4ull * (c->max_ctx + 1));
@@ -267,7 +267,7 @@ int etxmk_bind(etxmk_handle* h, void* weights, void* kv, void* workspace) {
   h->btab_host.resize(nblocks_of(&c));
   for (int i = 0; i < (int)h->btab_host.size(); ++i) h->btab_host[i] = i;
   HIPCHK(hipMemcpy(h->wsp + h->ws.btab, h->btab_host.data(), h->btab_host.size() * 4, hipMemcpyHostToDevice));
-  HIPCHK(hipMemset(h->wsp + h->ws.bar, 0, 4));
+  HIPCHK(hipMemset(h->wsp + h->ws.bar, 0, 4 * 64 * 17));
   HIPCHK(hipMemset(h->wsp + h->ws.abort_w, 0, 4));
   HIPCHK(hipMemset(h->wsp + h->ws.tokens, 0, 4ull * (c.max_ctx + 1)));
   HIPCHK(hipMemset(h->wsp + h->ws.out_tokens, 0, 4ull * (c.max_ctx + 1)));
@@ -408,6 +408,11 @@ int etxmk_set_grid(etxmk_handle* h, int32_t workgroups) {
   const int need = 8 * (c.NH / c.NKV) * ((c.NKV + 7) / 8);
   const int wg = workgroups > 0 ? workgroups : h->ncu;
   if (wg < need || wg > h->ncu) return fail(ETXMK_EINVAL, "workgroups %d outside %d..%d", wg, need, h->ncu);
+  if (wg != h->nwg && h->wsp) {            // barrier counters assume a fixed grid: restart them
+    HIPCHK(hipDeviceSynchronize());
+    HIPCHK(hipMemset(h->wsp + h->ws.bar, 0, 4 * 64 * 17));
+    h->bar_epoch = 0;
+  }
   h->nwg = wg;
   return ETXMK_OK;
 }
@@ -465,10 +470,13 @@ static int launch(etxmk_handle* h, int pos, int write_next, int l0, int l1, int 
     p.bar_base = h->bar_epoch;
     void* args[] = {&p};
     HIPCHK(hipLaunchCooperativeKernel((const void*)etxmk_fused, dim3(h->nwg), dim3(NT), args, 0, st));
-    h->bar_epoch += (uint32_t)h->barriers(l0, l1, head) * (uint32_t)h->nwg;
+    h->bar_epoch += (uint32_t)h->barriers(l0, l1, head);
   } else {
     auto ph = [&](int phase, int layer) -> int {
-      hipLaunchKernelGGL(etxmk_phase, dim3(h->nwg), dim3(NT), 0, st, p, phase, layer);
+      static void (*const kern[])(Params, int) = {etxmk_p_qkv, etxmk_p_attn, etxmk_p_oproj, etxmk_p_router,
+                                                  etxmk_p_expert_up, etxmk_p_expert_down, etxmk_p_gateup,
+                                                  etxmk_p_down, etxmk_p_head, etxmk_p_token};
+      hipLaunchKernelGGL(kern[phase], dim3(h->nwg), dim3(NT), 0, st, p, layer);
       HIPCHK(hipGetLastError());
       return ETXMK_OK;
     };
@@ -511,9 +519,10 @@ int etxmk_sync(etxmk_handle* h, void* stream) {
   HIPCHK(hipMemcpy(&ab, h->wsp + h->ws.abort_w, 4, hipMemcpyDeviceToHost));
   if (ab) {
     HIPCHK(hipMemset(h->wsp + h->ws.abort_w, 0, 4));
-    HIPCHK(hipMemset(h->wsp + h->ws.bar, 0, 4));
+    HIPCHK(hipMemset(h->wsp + h->ws.bar, 0, 4 * 64 * 17));
     h->bar_epoch = 0;
-    return fail(ETXMK_ABORTED, "device abort word %d (barrier wait exceeded its limit)", ab);
+    return fail(ETXMK_ABORTED, "device abort word %d (%s)", ab,
+                ab == 2 ? "a grid barrier wait exceeded its limit" : ab == 3 ? "no finite logit in the head" : "host abort");
   }
   return ETXMK_OK;
 }

@@ -97,21 +97,34 @@ __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 __device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
 
 // ---------------------------------------------------------------- grid barrier
-// Monotonic arrival counter: barrier k of this launch completes when the counter reaches
-// bar_base + (k + 1) * nwg.  Producers publish with an agent-scope release fence before arriving; consumers
-// read shared activations with agent-scope loads, so no cache invalidation is needed after the wait.
-// The wait is bounded by a wall-clock limit; on expiry the abort word is set and every workgroup leaves.
+// Monotonic counters (never reset): barrier k of this launch is generation gen = gen_base + k + 1.
+// Arrival is hierarchical to spread the atomics over 8 lines: workgroup w counts into group w % 8; the last
+// arrival of a group counts into the global word; the last group's last arrival writes the generation into
+// the 8 release flags, and every workgroup polls its group's flag.
+// Visibility: every value another workgroup reads is written with an agent-scope (sc1) store and read with an
+// agent-scope load; each wave waits for its own stores to complete (s_waitcnt 0) before the workgroup barrier
+// that precedes the arrival, so no L2 write-back or invalidate is needed.  The wait is bounded by a wall-clock
+// limit; on expiry the abort word is set and every workgroup leaves.
 __device__ __forceinline__ bool grid_sync(const Params& p, int& k, Smem& s) {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (threadIdx.x == 0) {
-    __hip_atomic_fetch_add(p.bar, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const uint32_t target = p.bar_base + (uint32_t)(k + 1) * (uint32_t)p.nwg;
+    const int g = blockIdx.x & 7;
+    const uint32_t ng = (uint32_t)(p.nwg - g + 7) / 8u;
+    const uint32_t gen = p.bar_base + (uint32_t)k + 1u;
+    uint32_t* grp = p.bar + 64 * g;
+    const uint32_t old = __hip_atomic_fetch_add(grp, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (old + 1u == gen * ng) {
+      const uint32_t o2 = __hip_atomic_fetch_add(p.bar + 64 * 8, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (o2 + 1u == gen * 8u)
+        for (int j = 0; j < 8; ++j) __hip_atomic_store(p.bar + 64 * (9 + j), gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    const uint32_t* flag = p.bar + 64 * (9 + g);
     const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
     int ab = 0;
     uint32_t polls = 0;
-    while ((int32_t)(__hip_atomic_load(p.bar, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - target) < 0) {
-      __builtin_amdgcn_s_sleep(2);
+    while ((int32_t)(__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - gen) < 0) {
+      __builtin_amdgcn_s_sleep(1);
       if ((++polls & 255u) == 0) {
         if (ld_ag_i(p.abort_word) != 0) { ab = 1; break; }
         if (__builtin_amdgcn_s_memrealtime() - t0 > p.spin_ticks) {
@@ -327,7 +340,11 @@ __device__ __forceinline__ void dispatch_k(int K, F&& f) {
 #define MK_K_INTER 1024, 12288
 
 // ---------------------------------------------------------------- phases
-__device__ __forceinline__ int token_of(const Params& p) { return ld_ag_i(p.tokens + p.pos); }
+// the step's input token; an id outside the vocabulary (only possible from corrupted state) reads row 0
+__device__ __forceinline__ int token_of(const Params& p) {
+  const int t = ld_ag_i(p.tokens + p.pos);
+  return (t >= 0 && t < p.V) ? t : 0;
+}
 
 // P1: input RMSNorm + fused QKV GEMV (ref_numpy.py:111-115)
 __device__ __forceinline__ void phase_qkv(const Params& p, int layer, Smem& s) {
@@ -561,6 +578,7 @@ __device__ __forceinline__ void route_topk(const Params& p, Smem& s) {
 #pragma unroll
       for (int w = 0; w < MAX_E / 64; ++w)
         if (lane + 64 * w == bi) taken[w] = true;
+      if (bi >= E) bi = 0;                               // non-finite probabilities: keep the index in range
       if (lane == 0) { s.ids[k] = bi; s.wts[k] = bv; }
       sel = sel + bv;
     }
@@ -721,7 +739,11 @@ __device__ __forceinline__ void phase_head(const Params& p, Smem& s) {
 __device__ __forceinline__ void phase_token(const Params& p) {
   if (blockIdx.x == 0 && threadIdx.x == 0) {
     const uint64_t key = ld_ag64(p.amax);
-    const int32_t tok = (int32_t)(0xFFFFFFFFu - (uint32_t)key);
+    int32_t tok = (int32_t)(0xFFFFFFFFu - (uint32_t)key);
+    if (key == 0 || tok < 0 || tok >= p.V) {              // no finite logit was seen: flag it, keep the id valid
+      st_ag_i(p.abort_word, 3);
+      tok = 0;
+    }
     st_ag_i(p.out_tokens + p.pos, tok);
     if (p.write_next) st_ag_i(p.tokens + p.pos + 1, tok);
   }
@@ -776,10 +798,22 @@ extern "C" __global__ void __launch_bounds__(NT, 1) etxmk_fused(Params p) {
   }
 }
 
-extern "C" __global__ void __launch_bounds__(NT, 1) etxmk_phase(Params p, int ph, int layer) {
-  __shared__ Smem s;
-  run_phase(p, ph, layer, s);
-}
+// unfused mode: one kernel per phase, same device functions (named per phase so profiles separate them)
+#define MK_PHASE_KERNEL(name, PH)                                               \
+  extern "C" __global__ void __launch_bounds__(NT, 1) name(Params p, int layer) { \
+    __shared__ Smem s;                                                          \
+    run_phase(p, PH, layer, s);                                                 \
+  }
+MK_PHASE_KERNEL(etxmk_p_qkv, PH_QKV)
+MK_PHASE_KERNEL(etxmk_p_attn, PH_ATTN)
+MK_PHASE_KERNEL(etxmk_p_oproj, PH_OPROJ)
+MK_PHASE_KERNEL(etxmk_p_router, PH_ROUTER)
+MK_PHASE_KERNEL(etxmk_p_expert_up, PH_EXPUP)
+MK_PHASE_KERNEL(etxmk_p_expert_down, PH_EXPDN)
+MK_PHASE_KERNEL(etxmk_p_gateup, PH_GATEUP)
+MK_PHASE_KERNEL(etxmk_p_down, PH_DOWN)
+MK_PHASE_KERNEL(etxmk_p_head, PH_HEAD)
+MK_PHASE_KERNEL(etxmk_p_token, PH_TOKEN)
 
 // ---------------------------------------------------------------- seeded initialisation / packing
 // n_t consecutive tensors of rows x cols (experts of one layer); element (r, k) of tensor e is number r*cols+k
