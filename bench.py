@@ -94,6 +94,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--unfused", action="store_true")
     ap.add_argument("--workgroups", type=int, default=0)
+    ap.add_argument("--trace", action="store_true", help="after timing, trace one fused step per phase (stderr)")
+    ap.add_argument("--kv-fill", action="store_true",
+                    help="profiling runs: fill the KV cache with seeded N(0,1) instead of prefilling the prompt")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py: this build runs on exactly one GPU (asked for {a.gpus}); multi-GPU sharding is a design "
@@ -116,13 +119,20 @@ def main():
     log(f"[gpu] weights {dec.sizes['weights'] / 1e9:.2f} GB initialised in {time.time() - t0:.1f}s; "
         f"{dec.barriers_per_step()} grid barriers per step")
     prompt = np.random.default_rng(a.seed).integers(0, cfg.V, a.ctx).astype(np.int32)
-    dec.set_tokens(prompt)
     t1 = time.time()
-    for pos in range(a.ctx):
-        dec.step(pos, write_next=pos + 1 >= a.ctx)
-        if pos % 256 == 255:
-            dec.sync()
-            log(f"[gpu] prefill {pos + 1}/{a.ctx} ({(time.time() - t1) / (pos + 1) * 1e3:.3f} ms/token)")
+    if a.kv_fill:
+        dec.fill_kv_seeded(a.seed, a.ctx)
+        toks = np.zeros(a.ctx + 1, np.int32)
+        toks[a.ctx] = prompt[-1]
+        dec.set_tokens(toks)
+        log(f"[gpu] KV cache filled with {a.ctx} seeded positions")
+    else:
+        dec.set_tokens(prompt)
+        for pos in range(a.ctx):
+            dec.step(pos, write_next=pos + 1 >= a.ctx)
+            if pos % 256 == 255:
+                dec.sync()
+                log(f"[gpu] prefill {pos + 1}/{a.ctx} ({(time.time() - t1) / (pos + 1) * 1e3:.3f} ms/token)")
     dec.sync()
     pos = a.ctx
     for _ in range(a.warmup):
@@ -149,11 +159,56 @@ def main():
     gbps = b["total"] / (ms * 1e-3) / 1e9
     log(f"[gpu] {a.steps} steps: {ms:.4f} ms/token (events), host wall {wall / a.steps:.4f} ms/token, "
         f"{gbps:.1f} GB/s = {gbps / HBM_PEAK_GBPS:.3f} of 8 TB/s; last tokens {list(toks[-4:])}")
+    phase_us = None
+    if a.trace and not a.unfused:
+        dec.enable_trace(True)
+        dec.step(pos, write_next=True)
+        pos += 1
+        t = dec.trace()                                   # [phase][wg][wait done, arrive], us from launch
+        dec.enable_trace(False)
+        names = (["qkv", "attn", "oproj", "router", "expert_up", "expert_down"] if cfg.moe
+                 else ["qkv", "attn", "oproj", "gateup", "down"])
+        nb = len(names) * cfg.L
+        end = np.nanmax(t[:, :, 1], axis=1)               # phase k complete: last arrival
+        span = np.diff(np.concatenate([[0.0], end[:nb + 1]]))
+        start_work = np.nanmedian(t[1:nb + 1, :, 0], axis=1)  # median wait-done of phase k (k >= 1)
+        per = span[:nb].reshape(cfg.L, len(names))
+        phase_us = {n: round(float(per[:, i].mean()), 2) for i, n in enumerate(names)}
+        phase_us["head"] = round(float(span[nb]), 2)
+        # barrier latency seen by the median workgroup: last arrival of phase k-1 -> its wait return in phase k
+        lag = start_work - end[:nb]
+        phase_us["barrier_median"] = round(float(np.median(lag)), 2)
+        # work of a phase: median over workgroups of arrive - wait-done (phase 0 has no wait)
+        work = np.full(nb, np.nan)
+        work[1:] = np.nanmedian(t[1:nb, :, 1] - t[1:nb, :, 0], axis=1)
+        wk = work.reshape(cfg.L, len(names))
+        log(f"[gpu] traced step {end[-2]:.1f} us; per-layer phase spans (us) {phase_us}")
+        wmax = np.full(nb, np.nan)
+        wmax[1:] = np.nanmax(t[1:nb, :, 1] - t[1:nb, :, 0], axis=1)
+        lagmax = np.full(nb, np.nan)
+        lagmax[1:] = np.nanmax(t[1:nb, :, 0], axis=1) - end[:nb - 1]
+        log("[gpu] per-workgroup work after its wait (us), median / max: " +
+            str({n: (round(float(np.nanmean(wk[:, i])), 2), round(float(np.nanmean(wmax.reshape(cfg.L, -1)[:, i])), 2))
+                 for i, n in enumerate(names)}))
+        log("[gpu] barrier lag (us), last arrival -> last wait return: " +
+            str({n: round(float(np.nanmean(lagmax.reshape(cfg.L, -1)[:, i])), 2) for i, n in enumerate(names)}))
+        issued = np.full(nb, np.nan)
+        issued[1:] = np.nanmedian(t[1:nb, :, 2] - end[:nb - 1, None], axis=1)
+        log("[gpu] first weight loads issued, median after the previous phase completed (us): " +
+            str({n: round(float(np.nanmean(issued.reshape(cfg.L, -1)[:, i])), 2) for i, n in enumerate(names)}))
+        # which workgroups are the slowest in the expert phases
+        for i, n in enumerate(names):
+            ks = np.arange(i, nb, len(names))
+            ks = ks[ks >= 1]
+            wdur = np.nan_to_num(t[ks, :, 1] - t[ks, :, 0])
+            slow = np.argsort(-wdur.mean(axis=0))[:6]
+            log(f"[gpu]   {n}: slowest workgroups {slow.tolist()} mean work {np.round(wdur.mean(axis=0)[slow], 2).tolist()}")
     out = {
         "metric": METRIC, "value": round(ms, 4), "unit": "ms/token", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
         "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic: seeded random-init bf16 weights N(0,0.02); prompt of seeded uniform token ids",
+        "data": "synthetic: seeded random-init bf16 weights N(0,0.02); " + ("KV cache of seeded N(0,1) values"
+                if a.kv_fill else "prompt of seeded uniform token ids prefilled token by token"),
         "config": {"workload": f"{cfg.name} decode, batch 1, context {a.ctx} (+{a.warmup} warmup), greedy "
                                f"(BASELINE.json configs[2])",
                    "batch": 1, "context": a.ctx, "layers": cfg.L, "experts": cfg.E, "top_k": cfg.TOPK,
@@ -167,6 +222,8 @@ def main():
                      "kernel": "etxmk_fused" if not a.unfused else "etxmk_phase (all phases)"},
         "cpu_baseline": None,
     }
+    if phase_us:
+        out["phase_us"] = phase_us
     if not a.no_cpu:
         try:
             out["cpu_baseline"] = cpu_baseline(cfg, a.ctx, a.seed)

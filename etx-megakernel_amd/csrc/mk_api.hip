@@ -61,13 +61,14 @@ int check_config(const etxmk_config* c) {
   if (c->H <= 0 || c->NH <= 0 || c->NKV <= 0 || c->L <= 0 || c->V <= 0) return fail(ETXMK_EINVAL, "non-positive dimension");
   if (c->HD != HDIM) return fail(ETXMK_EINVAL, "head_dim %d unsupported (the attention phase is built for %d)", c->HD, HDIM);
   if (c->NH % c->NKV) return fail(ETXMK_EINVAL, "NH %d not a multiple of NKV %d", c->NH, c->NKV);
+  if (c->NH / c->NKV > MAX_G) return fail(ETXMK_EINVAL, "%d q heads per kv head (at most %d)", c->NH / c->NKV, MAX_G);
   if (c->H > MAX_H || !k_in(c->H, {MK_K_HIDDEN})) return fail(ETXMK_EINVAL, "hidden size %d unsupported", c->H);
   if (!k_in(c->NH * c->HD, {MK_K_ATTN})) return fail(ETXMK_EINVAL, "NH*HD %d unsupported", c->NH * c->HD);
   if (c->batch != 1) return fail(ETXMK_EINVAL, "batch %d unsupported (batch 1 only)", c->batch);
   if (c->block_size <= 0 || CHUNK % c->block_size) return fail(ETXMK_EINVAL, "block size %d must divide %d", c->block_size, CHUNK);
   if (c->max_ctx <= 0 || c->max_ctx > MAX_CTX) return fail(ETXMK_EINVAL, "max_ctx %d outside 1..%d", c->max_ctx, MAX_CTX);
   if (c->moe) {
-    if (c->E <= 0 || c->E > MAX_E || c->TOPK <= 0 || c->TOPK > MAX_TOPK || c->TOPK > c->E)
+    if (c->E <= 0 || c->E > MAX_E || c->E % 4 || c->TOPK <= 0 || c->TOPK > MAX_TOPK || c->TOPK > c->E)
       return fail(ETXMK_EINVAL, "experts %d / top-k %d unsupported", c->E, c->TOPK);
     if (!k_in(c->MI, {MK_K_MOE}) || c->TOPK * c->MI > MAX_K) return fail(ETXMK_EINVAL, "moe intermediate %d unsupported", c->MI);
   } else {
@@ -113,7 +114,7 @@ int nblocks_of(const etxmk_config* c) { return (c->max_ctx + c->block_size - 1) 
 uint64_t kv_layer_elems(const etxmk_config* c) { return (uint64_t)nblocks_of(c) * c->block_size * c->NKV * c->HD; }
 
 struct WsLayout {
-  uint64_t x, qkv, o, logits, hbuf, amax, bar, abort_w, tokens, out_tokens, btab, rcos, rsin, layers, total;
+  uint64_t x, qkv, o, logits, hbuf, apart, acnt, amax, bar, abort_w, tokens, out_tokens, btab, rcos, rsin, layers, total;
 };
 
 WsLayout ws_layout(const etxmk_config* c) {
@@ -127,6 +128,8 @@ WsLayout ws_layout(const etxmk_config* c) {
   w.logits = take(4ull * (c->E > 0 ? c->E : 1));
   const int hb = c->moe ? c->TOPK * c->MI : c->I;
   w.hbuf = take(4ull * (hb > 0 ? hb : 1));
+  w.apart = take(4ull * c->NH * MAX_CHUNKS * PART);
+  w.acnt = take(4ull * 64 * c->NKV);     // one 256-byte line per kv head
   w.amax = take(8);
   w.bar = take(4 * 64 * 17);          // 8 group counters, 1 global counter, 8 release flags; 256 B apart
   w.abort_w = take(4);
@@ -158,6 +161,7 @@ struct etxmk_handle {
   int32_t* dump_ids = nullptr;
   float* dump_wts = nullptr;
   float* dump_logits = nullptr;
+  uint64_t* trace = nullptr;
   std::vector<int32_t> btab_host;
 
   const TensorSlot* slot(int kind, int layer) const {
@@ -272,6 +276,7 @@ int etxmk_bind(etxmk_handle* h, void* weights, void* kv, void* workspace) {
   HIPCHK(hipMemset(h->wsp + h->ws.tokens, 0, 4ull * (c.max_ctx + 1)));
   HIPCHK(hipMemset(h->wsp + h->ws.out_tokens, 0, 4ull * (c.max_ctx + 1)));
   HIPCHK(hipMemset(h->wsp + h->ws.x, 0, 4ull * c.H));
+  HIPCHK(hipMemset(h->wsp + h->ws.acnt, 0, 4ull * 64 * c.NKV));
   h->bar_epoch = 0;
   return ETXMK_OK;
 }
@@ -405,7 +410,7 @@ int etxmk_set_fused(etxmk_handle* h, int32_t fused) {
 int etxmk_set_grid(etxmk_handle* h, int32_t workgroups) {
   if (!h) return fail(ETXMK_EINVAL, "NULL handle");
   const etxmk_config& c = h->c;
-  const int need = 8 * (c.NH / c.NKV) * ((c.NKV + 7) / 8);
+  const int need = 8;                       // the grid barrier spreads arrivals over 8 groups
   const int wg = workgroups > 0 ? workgroups : h->ncu;
   if (wg < need || wg > h->ncu) return fail(ETXMK_EINVAL, "workgroups %d outside %d..%d", wg, need, h->ncu);
   if (wg != h->nwg && h->wsp) {            // barrier counters assume a fixed grid: restart them
@@ -426,10 +431,26 @@ int etxmk_set_dump(etxmk_handle* h, float* x_layers, int32_t* topk_ids, float* t
   return ETXMK_OK;
 }
 
+int etxmk_set_trace(etxmk_handle* h, uint64_t* stamps) {
+  if (!h) return fail(ETXMK_EINVAL, "NULL handle");
+  h->trace = stamps;
+  return ETXMK_OK;
+}
+
 int etxmk_barriers_per_step(etxmk_handle* h, int32_t* n) {
   if (!h || !n) return fail(ETXMK_EINVAL, "NULL argument");
   *n = h->barriers(0, h->c.L, 1);
   return ETXMK_OK;
+}
+
+// the persistent kernel instantiated for this shape, or nullptr
+static const void* fused_kernel(const etxmk_config& c) {
+  const int km = c.moe ? c.MI : c.I;
+#define MK_PICK(name, h_, ka_, km_, moe_, e_) \
+  if (c.H == h_ && c.NH * c.HD == ka_ && km == km_ && (c.moe != 0) == moe_ && (!moe_ || c.E == e_)) return (const void*)name;
+  MK_FUSED_SHAPES(MK_PICK)
+#undef MK_PICK
+  return nullptr;
 }
 
 static int launch(etxmk_handle* h, int pos, int write_next, int l0, int l1, int embed, int head, hipStream_t st) {
@@ -437,8 +458,8 @@ static int launch(etxmk_handle* h, int pos, int write_next, int l0, int l1, int 
   const etxmk_config& c = h->c;
   if (pos < 0 || pos >= c.max_ctx) return fail(ETXMK_EINVAL, "position %d outside 0..%d", pos, c.max_ctx - 1);
   if (l0 < 0 || l1 > c.L || l0 >= l1) return fail(ETXMK_EINVAL, "layer range [%d, %d) outside [0, %d)", l0, l1, c.L);
-  const int need = 8 * (c.NH / c.NKV) * ((c.NKV + 7) / 8);
-  if (h->nwg < need) return fail(ETXMK_EINVAL, "grid of %d workgroups is below the %d the attention phase needs", h->nwg, need);
+  const int need = 8;                       // the grid barrier spreads arrivals over 8 groups
+  if (h->nwg < need) return fail(ETXMK_EINVAL, "grid of %d workgroups is below the %d the grid barrier needs", h->nwg, need);
   Params p{};
   p.H = c.H; p.NH = c.NH; p.NKV = c.NKV; p.HD = c.HD; p.I = c.I; p.E = c.E; p.TOPK = c.TOPK; p.MI = c.MI; p.L = c.L; p.V = c.V;
   p.moe = c.moe; p.qk_norm = c.qk_norm; p.norm_topk = c.norm_topk; p.BS = c.block_size; p.max_ctx = c.max_ctx;
@@ -457,19 +478,25 @@ static int launch(etxmk_handle* h, int pos, int write_next, int l0, int l1, int 
   p.o = h->wsptr<float>(h->ws.o);
   p.logits = h->wsptr<float>(h->ws.logits);
   p.hbuf = h->wsptr<float>(h->ws.hbuf);
+  p.apart = h->wsptr<float>(h->ws.apart);
+  p.acnt = h->wsptr<uint32_t>(h->ws.acnt);
   p.amax = h->wsptr<uint64_t>(h->ws.amax);
   p.bar = h->wsptr<uint32_t>(h->ws.bar);
   p.abort_word = h->wsptr<int32_t>(h->ws.abort_w);
   p.tokens = h->wsptr<int32_t>(h->ws.tokens);
   p.out_tokens = h->wsptr<int32_t>(h->ws.out_tokens);
   p.dump_x = h->dump_x; p.dump_ids = h->dump_ids; p.dump_wts = h->dump_wts; p.dump_logits = h->dump_logits;
+  p.trace = h->fused ? h->trace : nullptr;
   p.pos = pos; p.write_next = write_next; p.l0 = l0; p.l1 = l1; p.do_embed = embed; p.do_head = head;
   p.nwg = h->nwg;
   p.spin_ticks = 200000000ull;            // 2 s of the 100 MHz s_memrealtime clock
   if (h->fused) {
+    const void* fn = fused_kernel(c);
+    if (!fn) return fail(ETXMK_EINVAL, "no persistent kernel for H %d, NH*HD %d, %s %d (use the unfused mode)", c.H,
+                         c.NH * c.HD, c.moe ? "MI" : "I", c.moe ? c.MI : c.I);
     p.bar_base = h->bar_epoch;
     void* args[] = {&p};
-    HIPCHK(hipLaunchCooperativeKernel((const void*)etxmk_fused, dim3(h->nwg), dim3(NT), args, 0, st));
+    HIPCHK(hipLaunchCooperativeKernel(fn, dim3(h->nwg), dim3(NT), args, 0, st));
     h->bar_epoch += (uint32_t)h->barriers(l0, l1, head);
   } else {
     auto ph = [&](int phase, int layer) -> int {
@@ -520,6 +547,7 @@ int etxmk_sync(etxmk_handle* h, void* stream) {
   if (ab) {
     HIPCHK(hipMemset(h->wsp + h->ws.abort_w, 0, 4));
     HIPCHK(hipMemset(h->wsp + h->ws.bar, 0, 4 * 64 * 17));
+    HIPCHK(hipMemset(h->wsp + h->ws.acnt, 0, 4ull * 64 * h->c.NKV));
     h->bar_epoch = 0;
     return fail(ETXMK_ABORTED, "device abort word %d (%s)", ab,
                 ab == 2 ? "a grid barrier wait exceeded its limit" : ab == 3 ? "no finite logit in the head" : "host abort");

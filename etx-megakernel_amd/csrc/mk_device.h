@@ -1,14 +1,15 @@
 #pragma once
 // Batch-small decode step for gfx950 (MI355X): one persistent cooperative launch per token that runs every
-// layer's phases back to back with grid barriers, or (unfused mode) one ordinary launch per phase with the
-// same device functions.
+// layer's phases back to back, separated by split grid barriers (arrive at the end of a phase, wait inside the
+// next one after its weight loads are in flight), or (unfused mode) one ordinary launch per phase with the same
+// device functions.
 //
 // Reference path (relative to the reference checkout): examples/llm/ref_numpy.py:105-158 is the numerical
 // specification; examples/llm/tiles.hip:23-357 and etx/codegen/kernel.py:471-605 are the tile bodies and
 // the persistent worker loop this file replaces.
 //
-// Phases of one layer (MoE):   P1 norm + QKV GEMV | P2 q/k norm, RoPE, paged KV append, attention |
-//                              P3 O projection + residual | P4 norm + router GEMV |
+// Phases of one layer (MoE):   P1 norm + QKV GEMV | P2 q/k norm, RoPE, paged KV append, chunked attention with
+//                              a last-arriver merge | P3 O projection + residual | P4 norm + router GEMV |
 //                              P5 top-k + expert gate/up GEMV + SiLU*up | P6 expert down GEMV, weight, combine, residual
 // Dense layers replace P4-P6 by gate/up (+SiLU*up) and down (+residual).  Head: final norm + lm_head GEMV with
 // a 64-bit packed argmax key, then the token write.
@@ -24,15 +25,16 @@ namespace mk {
 
 constexpr int NT = 512;                 // threads per workgroup: 8 waves, two per SIMD
 constexpr int NWAVE = NT / 64;
-constexpr int CHUNK = 64;               // attention positions per chunk
+constexpr int CHUNK = 64;               // attention positions per chunk (one lane per position)
 constexpr int HDIM = 128;               // head dim handled by the attention phase
 constexpr int MAX_H = 4096;
 constexpr int MAX_K = 12288;
 constexpr int MAX_CTX = 4096;
+constexpr int MAX_CHUNKS = MAX_CTX / CHUNK;
+constexpr int MAX_G = 16;               // q heads per kv head
 constexpr int MAX_E = 256;
 constexpr int MAX_TOPK = 8;
-
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+constexpr int PART = HDIM + 2;          // attention partial: a[HD], m, l
 
 struct LayerW {
   const uint16_t *ln1, *ln2, *qn, *kn;
@@ -56,6 +58,8 @@ struct Params {
   float* o;
   float* logits;
   float* hbuf;
+  float* apart;                         // [NH][MAX_CHUNKS][PART] attention partials
+  uint32_t* acnt;                       // [NKV] chunk arrival counters, 256 B apart (zero between steps)
   uint64_t* amax;
   uint32_t* bar;
   int32_t* abort_word;
@@ -65,6 +69,7 @@ struct Params {
   int32_t* dump_ids;
   float* dump_wts;
   float* dump_logits;
+  uint64_t* trace;                      // optional: [phase][workgroup][wait done, arrive, loads issued] stamps
   int pos, write_next, l0, l1, do_embed, do_head;
   uint32_t bar_base;
   int nwg;
@@ -75,29 +80,44 @@ struct Smem {
   union {
     struct {
       float xf[MAX_H];                  // residual (natural order, fp32)
-      alignas(16) uint16_t xs[MAX_K];   // GEMV input vector, lane-permuted bf16
+      alignas(16) uint16_t xs[MAX_K];   // GEMV input vector(s), lane-permuted bf16
     } g;
     struct {
-      float q[HDIM], k[HDIM], v[HDIM];
-      float p[MAX_CTX];                 // exp(s - m_c) per position
-      float mc[MAX_CTX / CHUNK];
-      float lc[MAX_CTX / CHUNK];
-      float ac[MAX_CTX / CHUNK][HDIM];
+      u32x4 kt[HDIM / 8][CHUNK];        // K tile: [8-dim group][position in chunk], 16 bytes each
+      u32x4 vt[CHUNK / 8][2][CHUNK];    // V tile: [8-position group][dim half][dim in half], 16 bytes each
+      alignas(16) float q[MAX_G][HDIM]; // roped q heads of the kv group
+      float knew[HDIM], vnew[HDIM];     // this step's k (roped) and v of the kv group
+      float p[MAX_G][2 * CHUNK];        // exp(s - m_c) of the chunk per head; merge: chunk weights and sums
+      float m[MAX_G];
     } a;
   };
   float rs;
   int32_t ids[MAX_TOPK];
   float wts[MAX_TOPK];
   int32_t order[MAX_TOPK];
-  float prob[MAX_E];
+  alignas(16) float prob[MAX_E];
   int32_t abort;
+  int32_t last;
+  int32_t phase;                        // arrivals so far (the current phase index), for trace stamps
 };
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+// one layer's pointer table, read through the constant address space (scalar loads)
+__device__ __forceinline__ LayerW layer_w(const Params& p, int layer) {
+  static_assert(sizeof(LayerW) % 8 == 0, "pointer table");
+  const __attribute__((address_space(4))) uint64_t* src = (const __attribute__((address_space(4))) uint64_t*)(p.layers + layer);
+  LayerW r;
+  uint64_t* dst = (uint64_t*)&r;
+#pragma unroll
+  for (int i = 0; i < (int)(sizeof(LayerW) / 8); ++i) dst[i] = src[i];
+  return r;
+}
 __device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
+// the wave index as a value the compiler knows is uniform (kept in a scalar register)
+__device__ __forceinline__ int wave_u() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
-// ---------------------------------------------------------------- grid barrier
-// Monotonic counters (never reset): barrier k of this launch is generation gen = gen_base + k + 1.
+// ---------------------------------------------------------------- grid barrier (split: arrive / wait)
+// Monotonic counters (never reset): the j-th arrival of this launch publishes generation bar_base + j + 1.
 // Arrival is hierarchical to spread the atomics over 8 lines: workgroup w counts into group w % 8; the last
 // arrival of a group counts into the global word; the last group's last arrival writes the generation into
 // the 8 release flags, and every workgroup polls its group's flag.
@@ -105,21 +125,31 @@ __device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
 // agent-scope load; each wave waits for its own stores to complete (s_waitcnt 0) before the workgroup barrier
 // that precedes the arrival, so no L2 write-back or invalidate is needed.  The wait is bounded by a wall-clock
 // limit; on expiry the abort word is set and every workgroup leaves.
-__device__ __forceinline__ bool grid_sync(const Params& p, int& k, Smem& s) {
+__device__ __forceinline__ void grid_arrive(const Params& p, int& k, Smem& s) {
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (threadIdx.x == 0) {
+    s.phase = k + 1;
+    if (p.trace) *(MK_G uint64_t*)(p.trace + ((size_t)k * p.nwg + blockIdx.x) * 3 + 1) = __builtin_amdgcn_s_memrealtime();
     const int g = blockIdx.x & 7;
     const uint32_t ng = (uint32_t)(p.nwg - g + 7) / 8u;
     const uint32_t gen = p.bar_base + (uint32_t)k + 1u;
-    uint32_t* grp = p.bar + 64 * g;
-    const uint32_t old = __hip_atomic_fetch_add(grp, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t old = __hip_atomic_fetch_add(p.bar + 64 * g, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (old + 1u == gen * ng) {
       const uint32_t o2 = __hip_atomic_fetch_add(p.bar + 64 * 8, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (o2 + 1u == gen * 8u)
         for (int j = 0; j < 8; ++j) __hip_atomic_store(p.bar + 64 * (9 + j), gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    const uint32_t* flag = p.bar + 64 * (9 + g);
+  }
+  ++k;
+}
+
+// wait until the k-th arrival's generation is published (nothing to wait for when k == 0)
+__device__ __forceinline__ bool grid_wait(const Params& p, int k, Smem& s) {
+  if (k == 0) return true;
+  if (threadIdx.x == 0) {
+    const uint32_t gen = p.bar_base + (uint32_t)k;
+    const uint32_t* flag = p.bar + 64 * (9 + (blockIdx.x & 7));
     const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
     int ab = 0;
     uint32_t polls = 0;
@@ -135,45 +165,125 @@ __device__ __forceinline__ bool grid_sync(const Params& p, int& k, Smem& s) {
       }
     }
     s.abort = ab;
+    if (p.trace) *(MK_G uint64_t*)(p.trace + ((size_t)k * p.nwg + blockIdx.x) * 3) = __builtin_amdgcn_s_memrealtime();
   }
   __syncthreads();
-  ++k;
   return s.abort == 0;
 }
 
 // ---------------------------------------------------------------- vectors into LDS
-// x (fp32 global, or the bf16 embedding row for the first layer) -> s.g.xf; normed and lane-permuted -> s.g.xs.
-// ref_numpy.py:71-73: r = 1/sqrt(mean(x^2) + eps), out = bfr(w * bfr(x * r)); the sum of squares in dot order.
-__device__ __forceinline__ void build_norm_x(const Params& p, const float* xg, const uint16_t* xrow, const uint16_t* w, Smem& s) {
-  const int H = p.H;
-  if (xrow) {
-    for (int i = threadIdx.x; i < H; i += NT) s.g.xf[i] = bf2f(xrow[i]);
-  } else {
-    for (int i = threadIdx.x; i < H / 2; i += NT) {
-      const uint64_t u = ld_ag64((const uint64_t*)xg + i);
-      s.g.xf[2 * i] = bits2f((uint32_t)u);
-      s.g.xf[2 * i + 1] = bits2f((uint32_t)(u >> 32));
-    }
+// Each helper issues all of a thread's global loads before it uses any of them (one memory latency, not one
+// per element).
+
+// x (n fp32, agent-scope) -> dst[n] natural order
+__device__ __forceinline__ void load_x(const float* xg, int n, float* dst) {
+  constexpr int PER = (MAX_H / 2 + NT - 1) / NT;
+  const int n2 = n / 2;
+  uint64_t v[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int i = threadIdx.x + j * NT;
+    if (i < n2) v[j] = ld_ag64((const uint64_t*)xg + i);
   }
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int i = threadIdx.x + j * NT;
+    if (i < n2) { dst[2 * i] = bits2f((uint32_t)v[j]); dst[2 * i + 1] = bits2f((uint32_t)(v[j] >> 32)); }
+  }
+}
+// a bf16 row of n elements (the embedding row) -> dst[n] fp32
+__device__ __forceinline__ void load_row_bf16(const uint16_t* row, int n, float* dst) {
+  constexpr int PER = (MAX_H / 8 + NT - 1) / NT;
+  const int n8 = n / 8;
+  u32x4 v[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int i = threadIdx.x + j * NT;
+    if (i < n8) v[j] = ld16(row + 8 * i);
+  }
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int i = threadIdx.x + j * NT;
+    if (i < n8)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) { dst[8 * i + 2 * e] = bf_lo(v[j][e]); dst[8 * i + 2 * e + 1] = bf_hi(v[j][e]); }
+  }
+}
+// the residual entering a phase: the embedding row of the step's token for the first layer, else x
+__device__ __forceinline__ void load_residual(const Params& p, bool first, int tok, float* dst) {
+  if (first) load_row_bf16(p.embed + (size_t)tok * p.H, p.H, dst);
+  else load_x(p.x, p.H, dst);
+}
+
+// x -> s.g.xf; RMSNorm with weight w, lane-permuted bf16 -> s.g.xs (ref_numpy.py:71-73:
+// r = 1/sqrt(mean(x^2) + eps), out = bfr(w * bfr(x * r)); the sum of squares in dot order).
+// Thread t writes stored chunk t (8 stored positions = 16 bytes of LDS).
+template <int H>
+__device__ __forceinline__ void build_norm_x(const Params& p, const float* xg, const uint16_t* xrow, const uint16_t* w,
+                                             Smem& s) {
+  constexpr int N8 = H / 8, PER = (N8 + NT - 1) / NT;
+  uint16_t wv[PER][8];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int c = threadIdx.x + j * NT;
+    if (c < N8)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) wv[j][e] = ld_u16(w + perm_logical(8 * c + e, H));
+  }
+  if (xrow) load_row_bf16(xrow, H, s.g.xf);
+  else load_x(xg, H, s.g.xf);
   __syncthreads();
   if (wave_id() == 0) {
     float acc = 0.0f;
+#pragma unroll 8
     for (int k = lane_id(); k < H; k += 64) acc = __builtin_fmaf(s.g.xf[k], s.g.xf[k], acc);
-    acc = wave_sum_xor(acc);
+    acc = wave_sum(acc);
     if (lane_id() == 0) s.rs = 1.0f / __builtin_sqrtf(acc / (float)H + p.eps);
   }
   __syncthreads();
   const float r = s.rs;
-  for (int q = threadIdx.x; q < H; q += NT) {
-    const int k = perm_logical(q, H);
-    s.g.xs[q] = f2bf(bfr(bf2f(w[k]) * bfr(s.g.xf[k] * r)));
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int c = threadIdx.x + j * NT;
+    if (c < N8) {
+      uint32_t o[4];
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        const int k0 = perm_logical(8 * c + e, H), k1 = perm_logical(8 * c + e + 1, H);
+        const uint32_t b0 = f2bf(bfr(bf2f(wv[j][e]) * bfr(s.g.xf[k0] * r)));
+        const uint32_t b1 = f2bf(bfr(bf2f(wv[j][e + 1]) * bfr(s.g.xf[k1] * r)));
+        o[e / 2] = b0 | (b1 << 16);
+      }
+      *(u32x4*)(s.g.xs + 8 * c) = u32x4{o[0], o[1], o[2], o[3]};
+    }
   }
   __syncthreads();
 }
 
-// a bf16-valued fp32 vector of length K (global, shared between workgroups) -> lane-permuted bf16 at dst
-__device__ __forceinline__ void load_vec_perm(const float* src, int K, uint16_t* dst) {
-  for (int q = threadIdx.x; q < K; q += NT) dst[q] = f2bf(ld_ag(src + perm_logical(q, K)));
+// nv bf16-valued fp32 vectors of length K (agent-scope, contiguous) -> lane-permuted bf16 at dst (contiguous)
+template <int K, int MAXV>
+__device__ __forceinline__ void load_vec_perm(const float* src, int nv, uint16_t* dst) {
+  constexpr int C8 = K / 8, PER = (MAXV * C8 + NT - 1) / NT;
+  float v[PER][8];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int c = threadIdx.x + j * NT;
+    if (c < nv * C8) {
+      const int vec = c / C8, q = 8 * (c - vec * C8);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[j][e] = ld_ag(src + (size_t)vec * K + perm_logical(q + e, K));
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int c = threadIdx.x + j * NT;
+    if (c < nv * C8) {
+      uint32_t o[4];
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) o[e / 2] = (uint32_t)f2bf(v[j][e]) | ((uint32_t)f2bf(v[j][e + 1]) << 16);
+      *(u32x4*)(dst + 8 * c) = u32x4{o[0], o[1], o[2], o[3]};
+    }
+  }
 }
 
 // ---------------------------------------------------------------- streaming GEMV
@@ -184,6 +294,7 @@ struct KS {
   static constexpr int TM = (K % 512) / 64;      // stored elements per lane in the tail block
   static_assert(TM % 2 == 0, "tail block must give each lane whole dwords");
   static constexpr int TW = TM / 2;
+  static constexpr int REGS = 4 * KB + TW;       // VGPRs one row occupies in flight
 };
 
 template <int K>
@@ -195,10 +306,10 @@ struct RowRegs {
 template <int K>
 __device__ __forceinline__ void load_row(RowRegs<K>& r, const uint16_t* row, int lane) {
 #pragma unroll
-  for (int b = 0; b < KS<K>::KB; ++b) r.w[b] = __builtin_nontemporal_load((const u32x4*)(row + 512 * b + lane * 8));
+  for (int b = 0; b < KS<K>::KB; ++b) r.w[b] = ld_nt16(row + 512 * b + lane * 8);
 #pragma unroll
   for (int t = 0; t < KS<K>::TW; ++t)
-    r.t[t] = __builtin_nontemporal_load((const uint32_t*)(row + 512 * KS<K>::KB + lane * KS<K>::TM + 2 * t));
+    r.t[t] = ld_nt4(row + 512 * KS<K>::KB + lane * KS<K>::TM + 2 * t);
 }
 
 template <int K>
@@ -219,7 +330,7 @@ __device__ __forceinline__ float dot_row(const RowRegs<K>& r, const uint16_t* xs
     acc = __builtin_fmaf(bf_lo(r.t[t]), bf_lo(xv), acc);
     acc = __builtin_fmaf(bf_hi(r.t[t]), bf_hi(xv), acc);
   }
-  return wave_sum_xor(acc);
+  return wave_sum(acc);
 }
 
 // Long rows (more than 16 blocks of 512): streamed in segments of 8 blocks, the next segment's loads in flight
@@ -232,7 +343,7 @@ __device__ __forceinline__ float dot_row_long(const uint16_t* row, const uint16_
   float acc = 0.0f;
   auto ld = [&](u32x4(&R)[SEG], int sg) {
 #pragma unroll
-    for (int b = 0; b < SEG; ++b) R[b] = __builtin_nontemporal_load((const u32x4*)(row + 512 * (sg * SEG + b) + lane * 8));
+    for (int b = 0; b < SEG; ++b) R[b] = ld_nt16(row + 512 * (sg * SEG + b) + lane * 8);
   };
   auto acc_seg = [&](const u32x4(&R)[SEG], int sg) {
 #pragma unroll
@@ -253,19 +364,23 @@ __device__ __forceinline__ float dot_row_long(const uint16_t* row, const uint16_
     if (sg + 2 < NS) ld(A, sg + 2);
     if (sg + 1 < NS) acc_seg(B, sg + 1);
   }
-  return wave_sum_xor(acc);
+  return wave_sum(acc);
 }
 
-// Groups of NR rows are dealt round-robin to the grid's waves; a wave streams its groups with the next
-// group's loads in flight while it reduces the current one.  rowf(g, i) gives row i of group g (nullptr when
-// absent), xf(i) its LDS input vector, epi(g, v) consumes the NR dot products (every lane holds them).
-template <int K, int NR, class RowF, class XF, class EpiF>
-__device__ __forceinline__ void gemv_run(int ngroups, int gw, int nw, RowF rowf, XF xf, EpiF epi) {
+// Groups of NR rows are dealt round-robin to the grid's waves (group g to global wave g mod nw).  A wave loads up
+// to D of its groups at once (about 96 VGPRs of weights), then reduces them; the first batch is issued before
+// `prologue` runs, so the weight stream overlaps the grid-barrier wait and the input-vector build that the
+// prologue does.  Every thread calls prologue() exactly once (it may synchronise the workgroup); it returns false
+// to abandon the phase.  rowf(g, i) gives row i of group g (nullptr when absent), xf(i) its LDS input vector,
+// epi(g, v) consumes the NR dot products (every lane holds them).  All group logic is wave-uniform.
+template <int K, int NR, class RowF, class XF, class EpiF, class Pro>
+__device__ __forceinline__ bool gemv_run(int ngroups, RowF rowf, XF xf, EpiF epi, Pro prologue, int nwg,
+                                         uint64_t* trace = nullptr, int s_phase = 0) {
   const int lane = lane_id();
-  int g = gw;
-  if (g >= ngroups) return;
+  const int gw = blockIdx.x * NWAVE + wave_u(), nw = nwg * NWAVE;
   if constexpr (KS<K>::KB > 16) {
-    for (; g < ngroups; g += nw) {
+    if (!prologue()) return false;
+    for (int g = gw; g < ngroups; g += nw) {
       float v[NR];
 #pragma unroll
       for (int i = 0; i < NR; ++i) {
@@ -274,44 +389,47 @@ __device__ __forceinline__ void gemv_run(int ngroups, int gw, int nw, RowF rowf,
       }
       epi(g, v);
     }
-    return;
-  }
-  constexpr bool DB = NR * (KS<K>::KB + KS<K>::TW) <= 16;
-  RowRegs<K> A[NR];
-  auto load = [&](RowRegs<K>(&R)[NR], int gg) {
-#pragma unroll
-    for (int i = 0; i < NR; ++i) {
-      const uint16_t* rp = rowf(gg, i);
-      if (rp) load_row<K>(R[i], rp, lane);
-    }
-  };
-  auto comp = [&](RowRegs<K>(&R)[NR], int gg) {
-    float v[NR];
-#pragma unroll
-    for (int i = 0; i < NR; ++i) v[i] = rowf(gg, i) ? dot_row<K>(R[i], xf(i), lane) : 0.0f;
-    epi(gg, v);
-  };
-  load(A, g);
-  if constexpr (DB) {
-    RowRegs<K> B[NR];
-    for (;;) {
-      const int g2 = g + nw;
-      if (g2 < ngroups) load(B, g2);
-      comp(A, g);
-      if (g2 >= ngroups) break;
-      const int g3 = g2 + nw;
-      if (g3 < ngroups) load(A, g3);
-      comp(B, g2);
-      if (g3 >= ngroups) break;
-      g = g3;
-    }
+    return true;
   } else {
-    for (;;) {
-      comp(A, g);
-      g += nw;
-      if (g >= ngroups) break;
-      load(A, g);
+    constexpr int RPG = NR * KS<K>::REGS;
+    constexpr int D = (96 / RPG) < 1 ? 1 : (96 / RPG) > 8 ? 8 : (96 / RPG);
+    RowRegs<K> R[D][NR];
+    auto issue = [&](int g0) {
+#pragma unroll
+      for (int d = 0; d < D; ++d) {
+        const int g = g0 + d * nw;
+        if (g < ngroups) {
+#pragma unroll
+          for (int i = 0; i < NR; ++i) {
+            const uint16_t* rp = rowf(g, i);
+            if (rp) load_row<K>(R[d][i], rp, lane);
+          }
+        }
+      }
+    };
+    int g0 = gw;
+    issue(g0);
+    if (trace && threadIdx.x == 0)
+      *(MK_G uint64_t*)(trace + ((size_t)s_phase * nwg + blockIdx.x) * 3 + 2) = __builtin_amdgcn_s_memrealtime();
+    if (!prologue()) return false;
+    while (g0 < ngroups) {
+#pragma unroll
+      for (int d = 0; d < D; ++d) {
+        const int g = g0 + d * nw;
+        if (g < ngroups) {
+          float v[NR];
+#pragma unroll
+          for (int i = 0; i < NR; ++i) {
+            const uint16_t* rp = rowf(g, i);
+            v[i] = rp ? dot_row<K>(R[d][i], xf(i), lane) : 0.0f;
+          }
+          epi(g, v);
+        }
+      }
+      g0 += D * nw;
+      if (g0 < ngroups) issue(g0);
     }
+    return true;
   }
 }
 
@@ -340,6 +458,8 @@ __device__ __forceinline__ void dispatch_k(int K, F&& f) {
 #define MK_K_INTER 1024, 12288
 
 // ---------------------------------------------------------------- phases
+// Every phase takes `wait`, the grid-barrier wait for its inputs (a no-op in unfused mode), and calls it exactly
+// once from every thread, as late as its data dependences allow.
 // the step's input token; an id outside the vocabulary (only possible from corrupted state) reads row 0
 __device__ __forceinline__ int token_of(const Params& p) {
   const int t = ld_ag_i(p.tokens + p.pos);
@@ -347,273 +467,357 @@ __device__ __forceinline__ int token_of(const Params& p) {
 }
 
 // P1: input RMSNorm + fused QKV GEMV (ref_numpy.py:111-115)
-__device__ __forceinline__ void phase_qkv(const Params& p, int layer, Smem& s) {
-  const LayerW& Lw = p.layers[layer];
+template <int KK, class Wait>
+__device__ __forceinline__ void phase_qkv(const Params& p, int layer, Smem& s, Wait wait) {
+  const LayerW Lw = layer_w(p, layer);
   const bool first = layer == p.l0 && p.do_embed;
-  const uint16_t* xrow = first ? p.embed + (size_t)token_of(p) * p.H : nullptr;
-  build_norm_x(p, p.x, xrow, Lw.ln1, s);
-  if (blockIdx.x == 0) {
-    if (p.dump_x && layer > p.l0)
-      for (int i = threadIdx.x; i < p.H; i += NT) p.dump_x[(size_t)(layer - 1) * p.H + i] = s.g.xf[i];
-    if (layer == p.l0 && p.do_head && threadIdx.x == 0)
-      __hip_atomic_store(p.amax, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
   const int rows = (p.NH + 2 * p.NKV) * p.HD;
-  const int gw = blockIdx.x * NWAVE + wave_id(), nw = p.nwg * NWAVE;
   float* qkv = p.qkv;
   const uint16_t* W = Lw.wqkv;
-  dispatch_k<MK_K_HIDDEN>(p.H, [&](auto kc_) {
-    constexpr int KK = decltype(kc_)::value;
-    gemv_run<KK, 2>(
-      (rows + 1) / 2, gw, nw,
+  gemv_run<KK, 2>(
+      (rows + 1) / 2,
       [&](int g, int i) -> const uint16_t* { const int r = 2 * g + i; return r < rows ? W + (size_t)r * KK : nullptr; },
       [&](int) { return (const uint16_t*)s.g.xs; },
       [&](int g, const float(&v)[2]) {
         lane_store<2>(v, [&](int i, float val) { const int r = 2 * g + i; if (r < rows) st_ag(qkv + r, bfr(val)); });
-      });
-  });
+      },
+      [&]() {
+        if (!wait()) return false;
+        const uint16_t* xrow = first ? p.embed + (size_t)token_of(p) * KK : nullptr;
+        build_norm_x<KK>(p, p.x, xrow, Lw.ln1, s);
+        if (blockIdx.x == 0) {
+          if (p.dump_x && layer > p.l0)
+            for (int i = threadIdx.x; i < KK; i += NT) st_f(p.dump_x + (size_t)(layer - 1) * KK + i, s.g.xf[i]);
+          if (layer == p.l0 && p.do_head && threadIdx.x == 0)
+            __hip_atomic_store(p.amax, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        return true;
+      },
+      p.nwg);
 }
 
-// P2: per q head: q/k RMSNorm, neox RoPE, paged KV append, chunked softmax attention (ref_numpy.py:116-129)
-__device__ __forceinline__ void phase_attn(const Params& p, int layer, Smem& s) {
+// P2: per (kv head, 64-position chunk): q/k RMSNorm and neox RoPE of the group's heads (ref_numpy.py:116-120),
+// paged KV append by the chunk holding `pos` (:121), then per q head the chunk's scores, max, exp, sum and
+// probability-weighted V (:122-129 in chunked form).  The chunk partials (a[HD], m, l) go to global memory; the
+// last chunk of a kv head to arrive merges them in ascending chunk order and writes o.
+// per-head RMSNorm of (a0, a1) = dims (lane, lane + 64) with weights (w0, w1)
+__device__ __forceinline__ void qk_norm(float& a0, float& a1, float w0, float w1, float eps) {
+  float acc = __builtin_fmaf(a0, a0, 0.0f);
+  acc = __builtin_fmaf(a1, a1, acc);
+  acc = wave_sum(acc);
+  const float r = 1.0f / __builtin_sqrtf(acc / (float)HDIM + eps);
+  a0 = bfr(w0 * bfr(a0 * r));
+  a1 = bfr(w1 * bfr(a1 * r));
+}
+
+template <class Wait>
+__device__ __forceinline__ void phase_attn(const Params& p, int layer, Smem& s, Wait wait) {
   const int NKV = p.NKV, NH = p.NH, G = NH / NKV, HD = HDIM, BS = p.BS;
-  // the G q heads of kv head g run on workgroups g%8 + 8*(j + G*(g/8)): one XCD per kv head
-  const int wg = blockIdx.x;
-  const int glo = wg & 7, t8 = wg >> 3, j = t8 % G, ghi = t8 / G, g = ghi * 8 + glo;
-  if (g >= NKV || ghi * 8 + 8 > ((NKV + 7) & ~7)) return;
-  const int h = g * G + j;
-  const LayerW& Lw = p.layers[layer];
-  const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
-  if (tid < HD) {
-    s.a.q[tid] = ld_ag(p.qkv + (size_t)h * HD + tid);
-    s.a.k[tid] = ld_ag(p.qkv + (size_t)(NH + g) * HD + tid);
-    s.a.v[tid] = ld_ag(p.qkv + (size_t)(NH + NKV + g) * HD + tid);
-  }
-  __syncthreads();
-  if (wave < 2) {
-    float* vec = wave == 0 ? s.a.q : s.a.k;
-    float a0 = vec[lane], a1 = vec[lane + 64];
-    if (p.qk_norm) {                                   // ref_numpy.py:116-118, per-head RMSNorm
-      const uint16_t* w = wave == 0 ? Lw.qn : Lw.kn;
-      float acc = __builtin_fmaf(a0, a0, 0.0f);
-      acc = __builtin_fmaf(a1, a1, acc);
-      acc = wave_sum_xor(acc);
-      const float r = 1.0f / __builtin_sqrtf(acc / (float)HD + p.eps);
-      a0 = bfr(bf2f(w[lane]) * bfr(a0 * r));
-      a1 = bfr(bf2f(w[lane + 64]) * bfr(a1 * r));
-    }
-    const float c = p.rope_cos[(size_t)p.pos * (HD / 2) + lane];   // ref_numpy.py:84-88 rotate_half
-    const float sn = p.rope_sin[(size_t)p.pos * (HD / 2) + lane];
-    vec[lane] = bfr(bfr(a0 * c) + bfr(-a1 * sn));
-    vec[lane + 64] = bfr(bfr(a1 * c) + bfr(a0 * sn));
-  }
-  __syncthreads();
   const int pos = p.pos, n = pos + 1, nch = (n + CHUNK - 1) / CHUNK;
-  {                                                     // paged append: K [blk][NKV][HD/8][BS][8], V [blk][NKV][HD][BS]
-    const int blk = p.btab[pos / BS], off = pos % BS;
-    if (j == 0 && tid < HD) {
-      Lw.kc[((((size_t)blk * NKV + g) * (HD / 8) + tid / 8) * BS + off) * 8 + tid % 8] = f2bf(s.a.k[tid]);
-      Lw.vc[(((size_t)blk * NKV + g) * HD + tid) * BS + off] = f2bf(s.a.v[tid]);
+  const LayerW Lw = layer_w(p, layer);
+  const int lane = lane_id(), wave = wave_u();
+  const float* cs = p.rope_cos + (size_t)pos * (HD / 2);
+  const float* sn = p.rope_sin + (size_t)pos * (HD / 2);
+  // The chunk's cached K and V go straight from HBM into LDS tiles (global_load_lds, 16 bytes per lane); they do
+  // not depend on this step, so the first item's copies are issued before the wait.  Wave w copies K dim-groups
+  // 2w, 2w+1 (lane = position) and the V position-group w (lane = dim, both halves).
+  auto load_kv = [&](int item) {
+    const int g = item % NKV, c = item / NKV;
+    const int t0 = c * CHUNK, len = min(CHUNK, n - t0);
+    const int t = t0 + lane;
+    if (lane < len && t != pos) {
+      const int blk = ld_i(p.btab + t / BS), off = t % BS;
+      const uint16_t* kp = Lw.kc + (((size_t)blk * NKV + g) * (HD / 8)) * BS * 8 + off * 8;
+#pragma unroll
+      for (int jj = 2 * wave; jj < 2 * wave + 2; ++jj)
+        __builtin_amdgcn_global_load_lds((const MK_G void*)(kp + (size_t)jj * BS * 8),
+                                         (__attribute__((address_space(3))) void*)&s.a.kt[jj][0], 16, 0, 0);
     }
-  }
-  // scores: lane = position inside a chunk; s_t = (q . k_t in ascending d) * scale
-  for (int c = wave; c < nch; c += NWAVE) {
-    const int t = c * CHUNK + lane;
-    float sc = -__builtin_huge_valf();
-    if (t < n) {
-      float acc = 0.0f;
-      if (t == pos) {
-#pragma unroll 16
-        for (int d = 0; d < HD; ++d) acc = __builtin_fmaf(s.a.q[d], s.a.k[d], acc);
-      } else {
-        const int blk = p.btab[t / BS], off = t % BS;
-        const uint16_t* kp = Lw.kc + (((size_t)blk * NKV + g) * (HD / 8)) * BS * 8 + off * 8;
-#pragma unroll 4
+    const int tb = t0 + wave * 8;                         // 8 positions per 16-byte load
+    if (tb < t0 + len) {
+      const int blk = ld_i(p.btab + tb / BS), off = tb % BS;
+      const uint16_t* vp = Lw.vc + ((size_t)blk * NKV + g) * HD * BS + off;
+      __builtin_amdgcn_global_load_lds((const MK_G void*)(vp + (size_t)lane * BS),
+                                       (__attribute__((address_space(3))) void*)&s.a.vt[wave][0][0], 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const MK_G void*)(vp + (size_t)(lane + 64) * BS),
+                                       (__attribute__((address_space(3))) void*)&s.a.vt[wave][1][0], 16, 0, 0);
+    }
+  };
+  const float rc = ld_f(cs + lane), rs = ld_f(sn + lane);
+  const float qn0 = bf2f(ld_u16(Lw.qn + lane)), qn1 = bf2f(ld_u16(Lw.qn + lane + 64));
+  const float kn0 = bf2f(ld_u16(Lw.kn + lane)), kn1 = bf2f(ld_u16(Lw.kn + lane + 64));
+  if ((int)blockIdx.x < NKV * nch) load_kv(blockIdx.x);
+  if (!wait()) return;
+  for (int item = blockIdx.x; item < NKV * nch; item += p.nwg) {
+    const int g = item % NKV, c = item / NKV;
+    const int t0 = c * CHUNK, len = min(CHUNK, n - t0);
+    const bool has_new = pos < t0 + len;                 // this chunk holds the current position
+    if (item != (int)blockIdx.x) load_kv(item);
+    for (int j = wave; j < G; j += NWAVE) {               // roped q of head g*G + j (ref_numpy.py:116-120)
+      const float* src = p.qkv + (size_t)(g * G + j) * HD;
+      float a0 = ld_ag(src + lane), a1 = ld_ag(src + lane + 64);
+      if (p.qk_norm) qk_norm(a0, a1, qn0, qn1, p.eps);
+      s.a.q[j][lane] = bfr(bfr(a0 * rc) + bfr(-a1 * rs));
+      s.a.q[j][lane + 64] = bfr(bfr(a1 * rc) + bfr(a0 * rs));
+    }
+    if (has_new && wave == NWAVE - 1) {                   // this step's k (normed, roped) and v
+      const float* ks = p.qkv + (size_t)(NH + g) * HD;
+      const float* vs = p.qkv + (size_t)(NH + NKV + g) * HD;
+      float a0 = ld_ag(ks + lane), a1 = ld_ag(ks + lane + 64);
+      const float v0 = ld_ag(vs + lane), v1 = ld_ag(vs + lane + 64);
+      if (p.qk_norm) qk_norm(a0, a1, kn0, kn1, p.eps);
+      s.a.knew[lane] = bfr(bfr(a0 * rc) + bfr(-a1 * rs));
+      s.a.knew[lane + 64] = bfr(bfr(a1 * rc) + bfr(a0 * rs));
+      s.a.vnew[lane] = v0;
+      s.a.vnew[lane + 64] = v1;
+    }
+    __builtin_amdgcn_s_waitcnt(0);                        // this wave's tile copies have landed in LDS
+    __syncthreads();
+    if (has_new && threadIdx.x < HD / 2) {                // this step's k, v (bf16 values) into the tiles
+      const int tp = pos - t0, d0 = 2 * threadIdx.x;      // two dims per thread
+      const uint32_t kw = (uint32_t)f2bf(s.a.knew[d0]) | ((uint32_t)f2bf(s.a.knew[d0 + 1]) << 16);
+      ((uint32_t*)&s.a.kt[d0 / 8][tp])[(d0 % 8) / 2] = kw;
+      uint16_t* v0 = (uint16_t*)&s.a.vt[tp / 8][d0 / 64][d0 % 64] + (tp % 8);
+      uint16_t* v1 = (uint16_t*)&s.a.vt[tp / 8][(d0 + 1) / 64][(d0 + 1) % 64] + (tp % 8);
+      *v0 = f2bf(s.a.vnew[d0]);
+      *v1 = f2bf(s.a.vnew[d0 + 1]);
+    }
+    __syncthreads();
+    if (has_new && threadIdx.x < HD) {                    // paged append (:121): K [blk][NKV][HD/8][BS][8], V [blk][NKV][HD][BS]
+      const int blk = ld_i(p.btab + pos / BS), off = pos % BS, d = threadIdx.x;
+      st_u16(Lw.kc + ((((size_t)blk * NKV + g) * (HD / 8) + d / 8) * BS + off) * 8 + d % 8, f2bf(s.a.knew[d]));
+      st_u16(Lw.vc + (((size_t)blk * NKV + g) * HD + d) * BS + off, f2bf(s.a.vnew[d]));
+    }
+    // scores (:126): lane = position t0 + lane; s_t = (q . k_t in ascending d) * scale; chunk max; p = exp(s - m)
+    {
+      const int t = t0 + lane;
+      const bool valid = lane < len;
+      for (int j = wave; j < G; j += NWAVE) {
+        float acc = 0.0f;
+#pragma unroll
         for (int jj = 0; jj < HD / 8; ++jj) {
-          const u32x4 kv = *(const u32x4*)(kp + (size_t)jj * BS * 8);
+          const u32x4 kw = s.a.kt[jj][lane];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            acc = __builtin_fmaf(s.a.q[8 * jj + 2 * e], bf_lo(kv[e]), acc);
-            acc = __builtin_fmaf(s.a.q[8 * jj + 2 * e + 1], bf_hi(kv[e]), acc);
+            acc = __builtin_fmaf(s.a.q[j][8 * jj + 2 * e], bf_lo(kw[e]), acc);
+            acc = __builtin_fmaf(s.a.q[j][8 * jj + 2 * e + 1], bf_hi(kw[e]), acc);
+          }
+        }
+        const float sc = valid ? acc * p.attn_scale : -__builtin_huge_valf();
+        const float m = wave_max(sc);
+        s.a.p[j][lane] = valid ? expf_mk(sc - m) : 0.0f;
+        if (lane == 0) s.a.m[j] = m;
+      }
+    }
+    __syncthreads();
+    // V (:127-128): lanes = dims (lane, lane + 64); a = sum_t p_t v_t[d] and l = sum_t p_t, ascending t
+    for (int j = wave; j < G; j += NWAVE) {
+      float a0 = 0.0f, a1 = 0.0f, l = 0.0f;
+#pragma unroll
+      for (int hb = 0; hb < CHUNK / 8; ++hb) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int tt = hb * 8 + e;
+          if (tt < len) {
+            const float pt = s.a.p[j][tt];
+            const uint32_t w0 = s.a.vt[hb][0][lane][e >> 1], w1 = s.a.vt[hb][1][lane][e >> 1];
+            const float v0 = (e & 1) ? bf_hi(w0) : bf_lo(w0);
+            const float v1 = (e & 1) ? bf_hi(w1) : bf_lo(w1);
+            a0 = __builtin_fmaf(pt, v0, a0);
+            a1 = __builtin_fmaf(pt, v1, a1);
+            l = l + pt;
           }
         }
       }
-      sc = acc * p.attn_scale;
+      float* part = p.apart + ((size_t)(g * G + j) * MAX_CHUNKS + c) * PART;
+      st_ag(part + lane, a0);
+      st_ag(part + lane + 64, a1);
+      if (lane == 0) { st_ag(part + HD, s.a.m[j]); st_ag(part + HD + 1, l); }
     }
-    const float m = wave_max(sc);
-    if (t < n) s.a.p[t] = expf_mk(sc - m);
-    if (lane == 0) s.a.mc[c] = m;
-  }
-  __syncthreads();
-  // per chunk and dim: a_c[d] = sum_t p_t v_t[d] (ascending t), l_c = sum_t p_t
-  for (int item = tid; item < nch * HD; item += NT) {
-    const int c = item / HD, d = item % HD;
-    const int t0 = c * CHUNK, t1 = min(t0 + CHUNK, n);
-    float a = 0.0f, l = 0.0f;
-    for (int tb = t0; tb < t1; tb += BS) {
-      const int blk = p.btab[tb / BS];
-      const uint16_t* vp = Lw.vc + (((size_t)blk * NKV + g) * HD + d) * BS;
-      const u32x4 va = *(const u32x4*)vp;
-      const u32x4 vb = *(const u32x4*)(vp + 8);
-      const int te = min(tb + BS, t1) - tb;
+    // the last chunk of kv head g to arrive merges: M = max m_c, w_c = exp(m_c - M), L = sum w_c l_c,
+    // A[d] = sum w_c a_c[d] (ascending c), o = bfr(A / L)
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const uint32_t old = __hip_atomic_fetch_add(p.acnt + 64 * g, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s.last = (old + 1u == (uint32_t)nch);
+    }
+    __syncthreads();
+    if (s.last) {
+      for (int j = wave; j < G; j += NWAVE) {
+        const float* part = p.apart + (size_t)(g * G + j) * MAX_CHUNKS * PART;
+        // lane cc holds chunk cc's (m, l); the chunk weights go through LDS for the ordered sums
+        float mloc = -__builtin_huge_valf(), lloc = 0.0f;
+        if (lane < nch) { mloc = ld_ag(part + (size_t)lane * PART + HD); lloc = ld_ag(part + (size_t)lane * PART + HD + 1); }
+        const float M = wave_max(mloc);
+        const float w = lane < nch ? expf_mk(mloc - M) : 0.0f;
+        s.a.p[j][lane] = w;
+        s.a.p[j][64 + lane] = lloc;
+        float Ls = 0.0f, A0 = 0.0f, A1 = 0.0f;
+        for (int c0 = 0; c0 < nch; c0 += 16) {
+          float av0[16], av1[16];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        if (i < te) {
-          const uint32_t wv = i < 8 ? va[i >> 1] : vb[(i - 8) >> 1];
-          const float vb16 = (i & 1) ? bf_hi(wv) : bf_lo(wv);
-          const int t = tb + i;
-          const float pt = s.a.p[t];
-          a = __builtin_fmaf(pt, t == pos ? s.a.v[d] : vb16, a);
-          l = l + pt;
+          for (int u = 0; u < 16; ++u)
+            if (c0 + u < nch) {
+              av0[u] = ld_ag(part + (size_t)(c0 + u) * PART + lane);
+              av1[u] = ld_ag(part + (size_t)(c0 + u) * PART + lane + 64);
+            }
+#pragma unroll
+          for (int u = 0; u < 16; ++u)
+            if (c0 + u < nch) {
+              const float wc = s.a.p[j][c0 + u];
+              Ls = __builtin_fmaf(wc, s.a.p[j][64 + c0 + u], Ls);
+              A0 = __builtin_fmaf(wc, av0[u], A0);
+              A1 = __builtin_fmaf(wc, av1[u], A1);
+            }
         }
+        st_ag(p.o + (size_t)(g * G + j) * HD + lane, bfr(A0 / Ls));
+        st_ag(p.o + (size_t)(g * G + j) * HD + lane + 64, bfr(A1 / Ls));
       }
+      if (threadIdx.x == 0) __hip_atomic_store(p.acnt + 64 * g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    s.a.ac[c][d] = a;
-    if (d == 0) s.a.lc[c] = l;
-  }
-  __syncthreads();
-  if (tid < HD) {                                       // merge chunks in ascending order
-    float M = -__builtin_huge_valf();
-    for (int c = 0; c < nch; ++c) M = fmaxf(M, s.a.mc[c]);
-    float Ls = 0.0f, A = 0.0f;
-    for (int c = 0; c < nch; ++c) {
-      const float w = expf_mk(s.a.mc[c] - M);
-      Ls = __builtin_fmaf(w, s.a.lc[c], Ls);
-      A = __builtin_fmaf(w, s.a.ac[c][tid], A);
-    }
-    st_ag(p.o + (size_t)h * HD + tid, bfr(A / Ls));
+    __syncthreads();
   }
 }
 
-// P3: O projection and residual (ref_numpy.py:130): x = bfr(x + bfr(Wo . o))
-__device__ __forceinline__ void phase_oproj(const Params& p, int layer, Smem& s) {
-  const LayerW& Lw = p.layers[layer];
-  const int K = p.NH * p.HD, H = p.H;
-  load_vec_perm(p.o, K, s.g.xs);
-  __syncthreads();
+// P3: O projection and residual (ref_numpy.py:130): x = bfr(x + bfr(Wo . o)); the residual is read into LDS in
+// the prologue together with o, so the epilogue does not wait on memory.
+template <int KK, class Wait>
+__device__ __forceinline__ void phase_oproj(const Params& p, int layer, Smem& s, Wait wait) {
+  const LayerW Lw = layer_w(p, layer);
+  const int H = p.H;
   const bool first = layer == p.l0 && p.do_embed;
-  const uint16_t* xrow = first ? p.embed + (size_t)token_of(p) * H : nullptr;
-  const int gw = blockIdx.x * NWAVE + wave_id(), nw = p.nwg * NWAVE;
   float* x = p.x;
   const uint16_t* W = Lw.wo;
-  dispatch_k<MK_K_ATTN>(K, [&](auto kc_) {
-    constexpr int KK = decltype(kc_)::value;
-    gemv_run<KK, 2>(
-      (H + 1) / 2, gw, nw,
-      [&](int g, int i) -> const uint16_t* { const int r = 2 * g + i; return r < H ? W + (size_t)r * KK : nullptr; },
+  gemv_run<KK, 1>(
+      H,
+      [&](int g, int) -> const uint16_t* { return W + (size_t)g * KK; },
       [&](int) { return (const uint16_t*)s.g.xs; },
-      [&](int g, const float(&v)[2]) {
-        lane_store<2>(v, [&](int i, float val) {
-          const int r = 2 * g + i;
-          if (r < H) {
-            const float xo = xrow ? bf2f(xrow[r]) : ld_ag(x + r);
-            st_ag(x + r, bfr(xo + bfr(val)));
-          }
-        });
-      });
-  });
+      [&](int g, const float(&v)[1]) {
+        if (lane_id() == 0) st_ag(x + g, bfr(s.g.xf[g] + bfr(v[0])));
+      },
+      [&]() {
+        if (!wait()) return false;
+        load_vec_perm<KK, 1>(p.o, 1, s.g.xs);
+        load_residual(p, first, first ? token_of(p) : 0, s.g.xf);
+        __syncthreads();
+        return true;
+      },
+      p.nwg);
 }
 
 // P4: post-attention RMSNorm + router GEMV (ref_numpy.py:131-134)
-__device__ __forceinline__ void phase_router(const Params& p, int layer, Smem& s) {
-  const LayerW& Lw = p.layers[layer];
-  build_norm_x(p, p.x, nullptr, Lw.ln2, s);
+template <int KK, class Wait>
+__device__ __forceinline__ void phase_router(const Params& p, int layer, Smem& s, Wait wait) {
+  const LayerW Lw = layer_w(p, layer);
   const int E = p.E;
-  const int gw = blockIdx.x * NWAVE + wave_id(), nw = p.nwg * NWAVE;
   float* lg = p.logits;
   const uint16_t* W = Lw.wr;
-  dispatch_k<MK_K_HIDDEN>(p.H, [&](auto kc_) {
-    constexpr int KK = decltype(kc_)::value;
-    gemv_run<KK, 2>(
-      (E + 1) / 2, gw, nw,
-      [&](int g, int i) -> const uint16_t* { const int r = 2 * g + i; return r < E ? W + (size_t)r * KK : nullptr; },
+  gemv_run<KK, 1>(
+      E,
+      [&](int g, int) -> const uint16_t* { return W + (size_t)g * KK; },
       [&](int) { return (const uint16_t*)s.g.xs; },
-      [&](int g, const float(&v)[2]) {
-        lane_store<2>(v, [&](int i, float val) { const int r = 2 * g + i; if (r < E) st_ag(lg + r, bfr(val)); });
-      });
-  });
+      [&](int g, const float(&v)[1]) { if (lane_id() == 0) st_ag(lg + g, bfr(v[0])); },
+      [&]() {
+        if (!wait()) return false;
+        build_norm_x<KK>(p, p.x, nullptr, Lw.ln2, s);
+        return true;
+      },
+      p.nwg);
 }
 
-// softmax top-k over the router logits (ref_numpy.py:135-140) into s.ids / s.wts / s.order (wave 0 computes;
-// every workgroup recomputes it, so no phase is spent on it).
+// softmax top-k over the router logits (ref_numpy.py:135-140) into s.ids / s.wts / s.order.  Wave 0 forms the
+// fp32 probabilities (max, exp, the dot-order sum, divide); then every thread t < E ranks expert t by counting the
+// experts that precede it in (probability descending, id ascending) order, which selects exactly what K rounds of
+// "largest probability, lowest id first" select.  Every workgroup recomputes it, so no phase is spent on it.
+template <int EC = 0>
 __device__ __forceinline__ void route_topk(const Params& p, Smem& s) {
-  const int E = p.E, K = p.TOPK;
+  constexpr int EMAX = EC > 0 ? EC : MAX_E;               // compile-time expert count when known
+  const int E = EC > 0 ? EC : p.E, K = p.TOPK;
+  if (threadIdx.x < MAX_TOPK) { s.ids[threadIdx.x] = 0; s.wts[threadIdx.x] = 0.0f; }
   if (wave_id() == 0) {
     const int lane = lane_id();
-    float m = -__builtin_huge_valf();
-    for (int e = lane; e < E; e += 64) {
-      const float v = ld_ag(p.logits + e);
-      s.prob[e] = v;
-      m = fmaxf(m, v);
+    constexpr int NW = (EMAX + 63) / 64;
+    float lv[NW];
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const int e = lane + 64 * w;
+      lv[w] = e < E ? ld_ag(p.logits + e) : -__builtin_huge_valf();
     }
+    float m = lv[0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) m = fmaxf(m, lv[w]);
     m = wave_max(m);
     float acc = 0.0f;
-    for (int e = lane; e < E; e += 64) {
-      const float ex = expf_mk(s.prob[e] - m);
-      s.prob[e] = ex;
-      acc = acc + ex;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const int e = lane + 64 * w;
+      lv[w] = e < E ? expf_mk(lv[w] - m) : 0.0f;
+      if (e < E) acc = acc + lv[w];
     }
-    const float S = wave_sum_xor(acc);
-    for (int e = lane; e < E; e += 64) s.prob[e] = s.prob[e] / S;
-    // K rounds of (max probability, lowest id); lane l owns experts l, l+64, l+128, l+192
-    float sel = 0.0f;
-    bool taken[MAX_E / 64] = {false, false, false, false};
+    const float S = wave_sum(acc);
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const int e = lane + 64 * w;
+      if (e < E) s.prob[e] = lv[w] / S;
+    }
+  }
+  __syncthreads();
+  const int e = threadIdx.x;
+  if (e < E) {                                            // E is a multiple of 4 (checked by the host)
+    const float pe = s.prob[e];
+    int rank = 0;
+#pragma unroll
+    for (int f = 0; f < EMAX; f += 4) {
+      if (EC > 0 || f < E) {
+        const float4 q = *(const float4*)&s.prob[f];      // the same 16 bytes for every lane: an LDS broadcast
+        rank += (q.x > pe || (q.x == pe && f < e)) ? 1 : 0;
+        rank += (q.y > pe || (q.y == pe && f + 1 < e)) ? 1 : 0;
+        rank += (q.z > pe || (q.z == pe && f + 2 < e)) ? 1 : 0;
+        rank += (q.w > pe || (q.w == pe && f + 3 < e)) ? 1 : 0;
+      }
+    }
+    if (rank < K) { s.ids[rank] = e; s.wts[rank] = pe; }
+  }
+  __syncthreads();
+  if (wave_id() == 0) {                                    // lane k holds slot k
+    const int lane = lane_id();
+    const float w = lane < K ? s.wts[lane] : 0.0f;
+    const int id = lane < K ? s.ids[lane] : 0x7fffffff;
+    float sel = 0.0f;                                     // selection-order sum of the chosen probabilities
+    int before = 0;                                       // slots whose expert id is lower: position in id order
     for (int k = 0; k < K; ++k) {
-      float bv = -1.0f;
-      int bi = 0x7fffffff;
-#pragma unroll
-      for (int w = 0; w < MAX_E / 64; ++w) {
-        const int e = lane + 64 * w;
-        if (e < E && !taken[w]) {
-          const float v = s.prob[e];
-          if (v > bv) { bv = v; bi = e; }
-        }
-      }
-#pragma unroll
-      for (int off = 32; off > 0; off >>= 1) {
-        const float ov = __shfl_xor(bv, off, 64);
-        const int oi = __shfl_xor(bi, off, 64);
-        if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-      }
-#pragma unroll
-      for (int w = 0; w < MAX_E / 64; ++w)
-        if (lane + 64 * w == bi) taken[w] = true;
-      if (bi >= E) bi = 0;                               // non-finite probabilities: keep the index in range
-      if (lane == 0) { s.ids[k] = bi; s.wts[k] = bv; }
-      sel = sel + bv;
+      sel = sel + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), k));
+      before += __builtin_amdgcn_readlane(id, k) < id ? 1 : 0;
     }
-    if (lane == 0) {
-      for (int k = 0; k < K; ++k) s.wts[k] = bfr(p.norm_topk ? s.wts[k] / sel : s.wts[k]);
-      for (int k = 0; k < K; ++k) s.order[k] = k;          // slots in ascending expert id (index_add_ order)
-      for (int a = 1; a < K; ++a)
-        for (int b = a; b > 0 && s.ids[s.order[b]] < s.ids[s.order[b - 1]]; --b) {
-          const int t = s.order[b]; s.order[b] = s.order[b - 1]; s.order[b - 1] = t;
-        }
+    if (lane < K) {
+      s.wts[lane] = bfr(p.norm_topk ? w / sel : w);
+      s.order[before] = lane;                             // slots in ascending expert id (index_add_ order)
     }
   }
   __syncthreads();
 }
 
-// P5: experts gate/up + SiLU*up for the top-k slots (ref_numpy.py:142-145)
-__device__ __forceinline__ void phase_expert_up(const Params& p, int layer, Smem& s) {
-  const LayerW& Lw = p.layers[layer];
-  route_topk(p, s);
-  if (blockIdx.x == 0 && threadIdx.x < 64) {
-    const int t = threadIdx.x;
-    if (p.dump_ids && t < p.TOPK) p.dump_ids[(size_t)layer * p.TOPK + t] = s.ids[t];
-    if (p.dump_wts && t < p.TOPK) p.dump_wts[(size_t)layer * p.TOPK + t] = s.wts[t];
-    if (p.dump_logits)
-      for (int e = t; e < p.E; e += 64) p.dump_logits[(size_t)layer * p.E + e] = ld_ag(p.logits + e);
-  }
-  build_norm_x(p, p.x, nullptr, Lw.ln2, s);
-  const int MI = p.MI, H = p.H, KT = p.TOPK;
-  const int gw = blockIdx.x * NWAVE + wave_id(), nw = p.nwg * NWAVE;
+// P5: experts gate/up + SiLU*up for the top-k slots (ref_numpy.py:142-145).  The normed input depends only on x
+// (final since the O projection), so it is built before the wait; the routing needs this phase's inputs.
+template <int KK, class Wait, int EC = 0>
+__device__ __forceinline__ void phase_expert_up(const Params& p, int layer, Smem& s, Wait wait) {
+  const LayerW Lw = layer_w(p, layer);
+  const int MI = p.MI, KT = p.TOPK;
   float* hb = p.hbuf;
   const uint16_t* W = Lw.w13;
-  dispatch_k<MK_K_HIDDEN>(H, [&](auto kc_) {
-    constexpr int KK = decltype(kc_)::value;
-    gemv_run<KK, 2>(
-      KT * MI, gw, nw,
+  build_norm_x<KK>(p, p.x, nullptr, Lw.ln2, s);
+  if (!wait()) return;
+  route_topk<EC>(p, s);
+  if (blockIdx.x == 0 && threadIdx.x < 64) {
+    const int t = threadIdx.x;
+    if (p.dump_ids && t < KT) st_i(p.dump_ids + (size_t)layer * KT + t, s.ids[t]);
+    if (p.dump_wts && t < KT) st_f(p.dump_wts + (size_t)layer * KT + t, s.wts[t]);
+    if (p.dump_logits)
+      for (int e = t; e < p.E; e += 64) st_f(p.dump_logits + (size_t)layer * p.E + e, ld_ag(p.logits + e));
+  }
+  gemv_run<KK, 2>(
+      KT * MI,
       [&](int g, int i) -> const uint16_t* {
         const int slot = g / MI, jj = g - slot * MI;
         return W + ((size_t)s.ids[slot] * 2 * MI + 2 * jj + i) * KK;
@@ -621,24 +825,21 @@ __device__ __forceinline__ void phase_expert_up(const Params& p, int layer, Smem
       [&](int) { return (const uint16_t*)s.g.xs; },
       [&](int g, const float(&v)[2]) {
         if (lane_id() == 0) st_ag(hb + g, bfr(bfr(silu(bfr(v[0]))) * bfr(v[1])));
-      });
-  });
+      },
+      [&]() { return true; }, p.nwg, p.trace, s.phase);
 }
 
-// P6: expert down, routing weight, combine in ascending expert id, residual (ref_numpy.py:146-148)
-__device__ __forceinline__ void phase_expert_down(const Params& p, int layer, Smem& s) {
-  const LayerW& Lw = p.layers[layer];
-  route_topk(p, s);
-  const int MI = p.MI, H = p.H, KT = p.TOPK;
-  for (int slot = 0; slot < KT; ++slot) load_vec_perm(p.hbuf + (size_t)slot * MI, MI, s.g.xs + (size_t)slot * MI);
-  __syncthreads();
-  const int gw = blockIdx.x * NWAVE + wave_id(), nw = p.nwg * NWAVE;
+// P6: expert down, routing weight, combine in ascending expert id, residual (ref_numpy.py:146-148).  The routing
+// comes from the router logits, final since two barriers ago, so the weights stream before the wait.
+template <int KK, class Wait, bool ROUTED = false>
+__device__ __forceinline__ void phase_expert_down(const Params& p, int layer, Smem& s, Wait wait) {
+  const LayerW Lw = layer_w(p, layer);
+  const int H = p.H, KT = p.TOPK;
+  if constexpr (!ROUTED) route_topk(p, s);                 // the persistent kernel kept expert_up's routing in LDS
   float* x = p.x;
   const uint16_t* W = Lw.w2;
-  dispatch_k<MK_K_MOE>(MI, [&](auto kc_) {
-    constexpr int KK = decltype(kc_)::value;
-    gemv_run<KK, MAX_TOPK>(
-      H, gw, nw,
+  gemv_run<KK, MAX_TOPK>(
+      H,
       [&](int g, int i) -> const uint16_t* { return i < KT ? W + ((size_t)s.ids[i] * H + g) * KK : nullptr; },
       [&](int i) { return (const uint16_t*)(s.g.xs + (size_t)i * KK); },
       [&](int g, const float(&v)[MAX_TOPK]) {
@@ -654,50 +855,60 @@ __device__ __forceinline__ void phase_expert_down(const Params& p, int layer, Sm
             for (int i = 0; i < MAX_TOPK; ++i) yk = (o == i) ? y[i] : yk;
             acc = bfr(acc + yk);
           }
-          st_ag(x + g, bfr(ld_ag(x + g) + acc));
+          st_ag(x + g, bfr(s.g.xf[g] + acc));
         }
-      });
-  });
+      },
+      [&]() {
+        if (!wait()) return false;
+        load_vec_perm<KK, MAX_TOPK>(p.hbuf, KT, s.g.xs);
+        load_x(p.x, p.H, s.g.xf);
+        __syncthreads();
+        return true;
+      },
+      p.nwg);
 }
 
 // dense MLP (ref_numpy.py:149-152): P4' gate/up + SiLU*up, P5' down + residual
-__device__ __forceinline__ void phase_gateup(const Params& p, int layer, Smem& s) {
-  const LayerW& Lw = p.layers[layer];
-  build_norm_x(p, p.x, nullptr, Lw.ln2, s);
-  const int I = p.I;
-  const int gw = blockIdx.x * NWAVE + wave_id(), nw = p.nwg * NWAVE;
+template <int KK, class Wait>
+__device__ __forceinline__ void phase_gateup(const Params& p, int layer, Smem& s, Wait wait) {
+  const LayerW Lw = layer_w(p, layer);
   float* hb = p.hbuf;
   const uint16_t* W = Lw.wgu;
-  dispatch_k<MK_K_HIDDEN>(p.H, [&](auto kc_) {
-    constexpr int KK = decltype(kc_)::value;
-    gemv_run<KK, 2>(
-      I, gw, nw,
+  gemv_run<KK, 2>(
+      p.I,
       [&](int g, int i) -> const uint16_t* { return W + ((size_t)2 * g + i) * KK; },
       [&](int) { return (const uint16_t*)s.g.xs; },
       [&](int g, const float(&v)[2]) {
         if (lane_id() == 0) st_ag(hb + g, bfr(bfr(silu(bfr(v[0]))) * bfr(v[1])));
-      });
-  });
+      },
+      [&]() {
+        if (!wait()) return false;
+        build_norm_x<KK>(p, p.x, nullptr, Lw.ln2, s);
+        return true;
+      },
+      p.nwg);
 }
 
-__device__ __forceinline__ void phase_down(const Params& p, int layer, Smem& s) {
-  const LayerW& Lw = p.layers[layer];
-  const int I = p.I, H = p.H;
-  load_vec_perm(p.hbuf, I, s.g.xs);
-  __syncthreads();
-  const int gw = blockIdx.x * NWAVE + wave_id(), nw = p.nwg * NWAVE;
+template <int KK, class Wait>
+__device__ __forceinline__ void phase_down(const Params& p, int layer, Smem& s, Wait wait) {
+  const LayerW Lw = layer_w(p, layer);
   float* x = p.x;
   const uint16_t* W = Lw.wd;
-  dispatch_k<MK_K_INTER>(I, [&](auto kc_) {
-    constexpr int KK = decltype(kc_)::value;
-    gemv_run<KK, 1>(
-      H, gw, nw,
+  gemv_run<KK, 1>(
+      p.H,
       [&](int g, int) -> const uint16_t* { return W + (size_t)g * KK; },
       [&](int) { return (const uint16_t*)s.g.xs; },
       [&](int g, const float(&v)[1]) {
-        if (lane_id() == 0) st_ag(x + g, bfr(ld_ag(x + g) + bfr(v[0])));
-      });
-  });
+        if (lane_id() == 0) st_ag(x + g, bfr(s.g.xf[g] + bfr(v[0])));
+      },
+      [&]() {
+        if (!wait()) return false;
+        load_vec_perm<KK, 1>(p.hbuf, 1, s.g.xs);
+        load_x(p.x, p.H, s.g.xf);
+        __syncthreads();
+        return true;
+      },
+      p.nwg);
 }
 
 // P7: final norm + lm_head + per-wave argmax folded into one 64-bit key (ref_numpy.py:155-158; first maximum wins)
@@ -708,18 +919,14 @@ __device__ __forceinline__ uint64_t argmax_key(float v, int idx) {
   return ((uint64_t)ord << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)idx);
 }
 
-__device__ __forceinline__ void phase_head(const Params& p, Smem& s) {
-  build_norm_x(p, p.x, nullptr, p.final_norm, s);
-  if (blockIdx.x == 0 && p.dump_x)
-    for (int i = threadIdx.x; i < p.H; i += NT) p.dump_x[(size_t)(p.l1 - 1) * p.H + i] = s.g.xf[i];
+template <int KK, class Wait>
+__device__ __forceinline__ void phase_head(const Params& p, Smem& s, Wait wait) {
   const int V = p.V;
-  const int gw = blockIdx.x * NWAVE + wave_id(), nw = p.nwg * NWAVE;
   const uint16_t* W = p.lm_head;
   uint64_t best = 0;
-  dispatch_k<MK_K_HIDDEN>(p.H, [&](auto kc_) {
-    constexpr int KK = decltype(kc_)::value;
-    gemv_run<KK, 2>(
-      (V + 1) / 2, gw, nw,
+  bool ran = false;
+  ran = gemv_run<KK, 2>(
+      (V + 1) / 2,
       [&](int g, int i) -> const uint16_t* { const int r = 2 * g + i; return r < V ? W + (size_t)r * KK : nullptr; },
       [&](int) { return (const uint16_t*)s.g.xs; },
       [&](int g, const float(&v)[2]) {
@@ -731,12 +938,21 @@ __device__ __forceinline__ void phase_head(const Params& p, Smem& s) {
             best = key > best ? key : best;
           }
         }
-      });
-  });
-  if (lane_id() == 0 && best) __hip_atomic_fetch_max(p.amax, best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      },
+      [&]() {
+        if (!wait()) return false;
+        build_norm_x<KK>(p, p.x, nullptr, p.final_norm, s);
+        if (blockIdx.x == 0 && p.dump_x)
+          for (int i = threadIdx.x; i < KK; i += NT) st_f(p.dump_x + (size_t)(p.l1 - 1) * KK + i, s.g.xf[i]);
+        return true;
+      },
+      p.nwg);
+  if (ran && lane_id() == 0 && best) __hip_atomic_fetch_max(p.amax, best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-__device__ __forceinline__ void phase_token(const Params& p) {
+template <class Wait>
+__device__ __forceinline__ void phase_token(const Params& p, Wait wait) {
+  if (!wait()) return;
   if (blockIdx.x == 0 && threadIdx.x == 0) {
     const uint64_t key = ld_ag64(p.amax);
     int32_t tok = (int32_t)(0xFFFFFFFFu - (uint32_t)key);
@@ -749,71 +965,124 @@ __device__ __forceinline__ void phase_token(const Params& p) {
   }
 }
 
+// runtime row-length dispatch (unfused per-phase kernels)
+template <class Wait>
+__device__ __forceinline__ void phase_qkv_any(const Params& p, int layer, Smem& s, Wait wait) {
+  dispatch_k<MK_K_HIDDEN>(p.H, [&](auto kc_) { phase_qkv<decltype(kc_)::value>(p, layer, s, wait); });
+}
+template <class Wait>
+__device__ __forceinline__ void phase_oproj_any(const Params& p, int layer, Smem& s, Wait wait) {
+  dispatch_k<MK_K_ATTN>(p.NH * p.HD, [&](auto kc_) { phase_oproj<decltype(kc_)::value>(p, layer, s, wait); });
+}
+template <class Wait>
+__device__ __forceinline__ void phase_router_any(const Params& p, int layer, Smem& s, Wait wait) {
+  dispatch_k<MK_K_HIDDEN>(p.H, [&](auto kc_) { phase_router<decltype(kc_)::value>(p, layer, s, wait); });
+}
+template <class Wait>
+__device__ __forceinline__ void phase_expert_up_any(const Params& p, int layer, Smem& s, Wait wait) {
+  dispatch_k<MK_K_HIDDEN>(p.H, [&](auto kc_) { phase_expert_up<decltype(kc_)::value>(p, layer, s, wait); });
+}
+template <class Wait>
+__device__ __forceinline__ void phase_expert_down_any(const Params& p, int layer, Smem& s, Wait wait) {
+  dispatch_k<MK_K_MOE>(p.MI, [&](auto kc_) { phase_expert_down<decltype(kc_)::value>(p, layer, s, wait); });
+}
+template <class Wait>
+__device__ __forceinline__ void phase_gateup_any(const Params& p, int layer, Smem& s, Wait wait) {
+  dispatch_k<MK_K_HIDDEN>(p.H, [&](auto kc_) { phase_gateup<decltype(kc_)::value>(p, layer, s, wait); });
+}
+template <class Wait>
+__device__ __forceinline__ void phase_down_any(const Params& p, int layer, Smem& s, Wait wait) {
+  dispatch_k<MK_K_INTER>(p.I, [&](auto kc_) { phase_down<decltype(kc_)::value>(p, layer, s, wait); });
+}
+template <class Wait>
+__device__ __forceinline__ void phase_head_any(const Params& p, Smem& s, Wait wait) {
+  dispatch_k<MK_K_HIDDEN>(p.H, [&](auto kc_) { phase_head<decltype(kc_)::value>(p, s, wait); });
+}
+
 // ---------------------------------------------------------------- kernels
 enum Phase { PH_QKV = 0, PH_ATTN, PH_OPROJ, PH_ROUTER, PH_EXPUP, PH_EXPDN, PH_GATEUP, PH_DOWN, PH_HEAD, PH_TOKEN };
 
-__device__ __forceinline__ void run_phase(const Params& p, int ph, int layer, Smem& s) {
-  switch (ph) {
-    case PH_QKV: phase_qkv(p, layer, s); break;
-    case PH_ATTN: phase_attn(p, layer, s); break;
-    case PH_OPROJ: phase_oproj(p, layer, s); break;
-    case PH_ROUTER: phase_router(p, layer, s); break;
-    case PH_EXPUP: phase_expert_up(p, layer, s); break;
-    case PH_EXPDN: phase_expert_down(p, layer, s); break;
-    case PH_GATEUP: phase_gateup(p, layer, s); break;
-    case PH_DOWN: phase_down(p, layer, s); break;
-    case PH_HEAD: phase_head(p, s); break;
-    case PH_TOKEN: phase_token(p); break;
-  }
-}
-
-extern "C" __global__ void __launch_bounds__(NT, 1) etxmk_fused(Params p) {
+// The persistent kernel, instantiated per model shape: hidden size H, attention width KA = NH*HD, and the MLP
+// row length KM (the expert intermediate for MoE, the dense intermediate otherwise).
+template <int H, int KA, int KM, bool MOE, int EC>
+__device__ __forceinline__ void fused_body(const Params& p) {
   __shared__ Smem s;
-  int k = 0;
+  if (threadIdx.x == 0) s.abort = 0;
+  __syncthreads();
+  int k = 0;                                              // arrivals so far in this launch
+  auto wait = [&]() { return grid_wait(p, k, s); };
+  // per-phase timeline (ETX_TRACE, etx/codegen/kernel.py:346-347): 100 MHz s_memrealtime stamps of every
+  // workgroup when its wait for the phase's inputs returns and when it arrives after the phase
+  if (p.trace && threadIdx.x == 0) *(MK_G uint64_t*)(p.trace + (size_t)blockIdx.x * 3) = __builtin_amdgcn_s_memrealtime();
+  s.phase = 0;
   for (int layer = p.l0; layer < p.l1; ++layer) {
-    phase_qkv(p, layer, s);
-    if (!grid_sync(p, k, s)) return;
-    phase_attn(p, layer, s);
-    if (!grid_sync(p, k, s)) return;
-    phase_oproj(p, layer, s);
-    if (!grid_sync(p, k, s)) return;
-    if (p.moe) {
-      phase_router(p, layer, s);
-      if (!grid_sync(p, k, s)) return;
-      phase_expert_up(p, layer, s);
-      if (!grid_sync(p, k, s)) return;
-      phase_expert_down(p, layer, s);
-      if (!grid_sync(p, k, s)) return;
+    phase_qkv<H>(p, layer, s, wait);
+    if (s.abort) return;
+    grid_arrive(p, k, s);
+    phase_attn(p, layer, s, wait);
+    if (s.abort) return;
+    grid_arrive(p, k, s);
+    phase_oproj<KA>(p, layer, s, wait);
+    if (s.abort) return;
+    grid_arrive(p, k, s);
+    if constexpr (MOE) {
+      phase_router<H>(p, layer, s, wait);
+      if (s.abort) return;
+      grid_arrive(p, k, s);
+      phase_expert_up<H, decltype(wait), EC>(p, layer, s, wait);
+      if (s.abort) return;
+      grid_arrive(p, k, s);
+      phase_expert_down<KM, decltype(wait), true>(p, layer, s, wait);
+      if (s.abort) return;
+      grid_arrive(p, k, s);
     } else {
-      phase_gateup(p, layer, s);
-      if (!grid_sync(p, k, s)) return;
-      phase_down(p, layer, s);
-      if (!grid_sync(p, k, s)) return;
+      phase_gateup<H>(p, layer, s, wait);
+      if (s.abort) return;
+      grid_arrive(p, k, s);
+      phase_down<KM>(p, layer, s, wait);
+      if (s.abort) return;
+      grid_arrive(p, k, s);
     }
   }
   if (p.do_head) {
-    phase_head(p, s);
-    if (!grid_sync(p, k, s)) return;
-    phase_token(p);
+    phase_head<H>(p, s, wait);
+    if (s.abort) return;
+    grid_arrive(p, k, s);
+    phase_token(p, wait);
   }
 }
 
+// shapes with a persistent kernel: name, H, KA, KM, MoE, E (the host picks by the same fields)
+#define MK_FUSED_SHAPES(X)                                             \
+  X(etxmk_fused_h2048_a4096_moe768_e128, 2048, 4096, 768, true, 128)  \
+  X(etxmk_fused_h4096_a4096_mlp12288, 4096, 4096, 12288, false, 0)    \
+  X(etxmk_fused_h512_a512_moe256_e16, 512, 512, 256, true, 16)        \
+  X(etxmk_fused_h512_a512_mlp1024, 512, 512, 1024, false, 0)
+#define MK_FUSED_KERNEL(name, H, KA, KM, MOE, EC) \
+  extern "C" __global__ void __launch_bounds__(NT, 1) name(Params p) { fused_body<H, KA, KM, MOE, EC>(p); }
+MK_FUSED_SHAPES(MK_FUSED_KERNEL)
+
 // unfused mode: one kernel per phase, same device functions (named per phase so profiles separate them)
-#define MK_PHASE_KERNEL(name, PH)                                               \
+struct NoWait {
+  __device__ bool operator()() const { return true; }
+};
+#define MK_PHASE_KERNEL(name, CALL)                                                   \
   extern "C" __global__ void __launch_bounds__(NT, 1) name(Params p, int layer) { \
-    __shared__ Smem s;                                                          \
-    run_phase(p, PH, layer, s);                                                 \
+    __shared__ Smem s;                                                            \
+    if (threadIdx.x == 0) s.abort = 0;                                            \
+    __syncthreads();                                                              \
+    CALL;                                                                         \
   }
-MK_PHASE_KERNEL(etxmk_p_qkv, PH_QKV)
-MK_PHASE_KERNEL(etxmk_p_attn, PH_ATTN)
-MK_PHASE_KERNEL(etxmk_p_oproj, PH_OPROJ)
-MK_PHASE_KERNEL(etxmk_p_router, PH_ROUTER)
-MK_PHASE_KERNEL(etxmk_p_expert_up, PH_EXPUP)
-MK_PHASE_KERNEL(etxmk_p_expert_down, PH_EXPDN)
-MK_PHASE_KERNEL(etxmk_p_gateup, PH_GATEUP)
-MK_PHASE_KERNEL(etxmk_p_down, PH_DOWN)
-MK_PHASE_KERNEL(etxmk_p_head, PH_HEAD)
-MK_PHASE_KERNEL(etxmk_p_token, PH_TOKEN)
+MK_PHASE_KERNEL(etxmk_p_qkv, phase_qkv_any(p, layer, s, NoWait{}))
+MK_PHASE_KERNEL(etxmk_p_attn, phase_attn(p, layer, s, NoWait{}))
+MK_PHASE_KERNEL(etxmk_p_oproj, phase_oproj_any(p, layer, s, NoWait{}))
+MK_PHASE_KERNEL(etxmk_p_router, phase_router_any(p, layer, s, NoWait{}))
+MK_PHASE_KERNEL(etxmk_p_expert_up, phase_expert_up_any(p, layer, s, NoWait{}))
+MK_PHASE_KERNEL(etxmk_p_expert_down, phase_expert_down_any(p, layer, s, NoWait{}))
+MK_PHASE_KERNEL(etxmk_p_gateup, phase_gateup_any(p, layer, s, NoWait{}))
+MK_PHASE_KERNEL(etxmk_p_down, phase_down_any(p, layer, s, NoWait{}))
+MK_PHASE_KERNEL(etxmk_p_head, phase_head_any(p, s, NoWait{}))
+MK_PHASE_KERNEL(etxmk_p_token, phase_token(p, NoWait{}))
 
 // ---------------------------------------------------------------- seeded initialisation / packing
 // n_t consecutive tensors of rows x cols (experts of one layer); element (r, k) of tensor e is number r*cols+k

@@ -6,7 +6,7 @@
 //  * seeded weights: splitmix64 counter stream (Steele, Lea, Flood 2014) and Box-Muller with
 //    polynomial log / sin / cos, again only +, *, /, sqrt and fma, so host and device agree exactly.
 //  * dot order: lane l of a wave64 accumulates elements k = l (mod 64) in ascending k with fma;
-//    lanes are combined by an xor butterfly 32, 16, 8, 4, 2, 1.
+//    lanes are combined by wave_sum() below.
 //
 // The library is compiled with -ffp-contract=off: every fma below is explicit.
 #pragma once
@@ -137,10 +137,23 @@ __host__ __device__ __forceinline__ int perm_stored(int k, int K) {    // logica
   return base + (q & 63) * m + (q >> 6);
 }
 
-__device__ __forceinline__ float wave_sum_xor(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = v + __shfl_xor(v, off, 64);
-  return v;
+// Lane reduction of a wave64 in the fixed order the CPU oracle restates: partner l^1, then l^2 (DPP quad
+// permutes), then the mirror inside 8 lanes and inside 16 lanes (DPP row_half_mirror, row_mirror); each 16-lane row
+// then holds its sum in every lane, and the four rows are combined as (row0 + row1) + (row2 + row3).
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float wave_sum(float v) {
+  v = v + dpp_mov<0xB1>(v);     // quad_perm [1,0,3,2]
+  v = v + dpp_mov<0x4E>(v);     // quad_perm [2,3,0,1]
+  v = v + dpp_mov<0x141>(v);    // row_half_mirror
+  v = v + dpp_mov<0x140>(v);    // row_mirror
+  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+  const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+  const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+  return (r0 + r1) + (r2 + r3);
 }
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
@@ -148,21 +161,39 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// ---------------------------------------------------------------- global-memory access
+// Pointers that reach the kernels through structures are generic; dereferencing them directly makes flat
+// instructions, which also count against the LDS counter (so every LDS wait would wait for the weight stream
+// too).  Every device-memory access therefore goes through an address-space-1 (global) pointer.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+#define MK_G __attribute__((address_space(1)))
+
+__device__ __forceinline__ u32x4 ld_nt16(const void* p) { return __builtin_nontemporal_load((const MK_G u32x4*)p); }
+__device__ __forceinline__ uint32_t ld_nt4(const void* p) { return __builtin_nontemporal_load((const MK_G uint32_t*)p); }
+__device__ __forceinline__ u32x4 ld16(const void* p) { return *(const MK_G u32x4*)p; }
+__device__ __forceinline__ uint32_t ld4(const void* p) { return *(const MK_G uint32_t*)p; }
+__device__ __forceinline__ uint16_t ld_u16(const uint16_t* p) { return *(const MK_G uint16_t*)p; }
+__device__ __forceinline__ float ld_f(const float* p) { return *(const MK_G float*)p; }
+__device__ __forceinline__ int32_t ld_i(const int32_t* p) { return *(const MK_G int32_t*)p; }
+__device__ __forceinline__ void st_u16(uint16_t* p, uint16_t v) { *(MK_G uint16_t*)p = v; }
+__device__ __forceinline__ void st_f(float* p, float v) { *(MK_G float*)p = v; }
+__device__ __forceinline__ void st_i(int32_t* p, int32_t v) { *(MK_G int32_t*)p = v; }
+
 // agent-scope (cross-XCD coherent) element access for activations shared between workgroups
 __device__ __forceinline__ float ld_ag(const float* p) {
-  return __uint_as_float(__hip_atomic_load((const uint32_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  return __uint_as_float(__hip_atomic_load((const MK_G uint32_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
 }
 __device__ __forceinline__ void st_ag(float* p, float v) {
-  __hip_atomic_store((uint32_t*)p, __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store((MK_G uint32_t*)p, __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ uint64_t ld_ag64(const uint64_t* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return __hip_atomic_load((const MK_G uint64_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ int32_t ld_ag_i(const int32_t* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return __hip_atomic_load((const MK_G int32_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void st_ag_i(int32_t* p, int32_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store((MK_G int32_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace mk

@@ -90,8 +90,10 @@ def load(path: Path | None = None):
     global _lib
     if _lib is not None and path is None:
         return _lib
+    # ETXMK_LIB names another build of the same library (for instance an instrumented one)
     import torch  # noqa: F401  (binds libamdhip64 before the library resolves it)
-    p = Path(path or LIB_PATH)
+    import os
+    p = Path(path or os.environ.get("ETXMK_LIB") or LIB_PATH)
     if not p.exists():
         raise FileNotFoundError(f"{p} is not built; run etx-megakernel_amd/build_lib.py (no fallback path exists)")
     L = C.CDLL(str(p))
@@ -121,6 +123,7 @@ def load(path: Path | None = None):
         "etxmk_set_dump": [vp, vp, vp, vp, vp],
         "etxmk_set_grid": [vp, i32],
         "etxmk_barriers_per_step": [vp, C.POINTER(i32)],
+        "etxmk_set_trace": [vp, vp],
     }
     for name, args in sig.items():
         f = getattr(L, name)
@@ -187,6 +190,7 @@ class Decoder:
             _check(self.L, self.L.etxmk_bind(h, self.weights.data_ptr(), self.kv.data_ptr(), self.workspace.data_ptr()))
             _check(self.L, self.L.etxmk_set_fused(h, int(fused)))
             _check(self.L, self.L.etxmk_set_grid(h, int(workgroups)))
+        self._nwg = int(workgroups)
         self._dumps = None
 
     # ---- plumbing
@@ -287,6 +291,30 @@ class Decoder:
 
     def sync(self):
         _check(self.L, self.L.etxmk_sync(self.h, self._stream()))
+
+    def enable_trace(self, on: bool = True):
+        """Per-phase, per-workgroup s_memrealtime stamps of the fused kernel; read with trace()."""
+        if on:
+            n = (self.barriers_per_step() + 1) * self.workgroups() * 3
+            self._trace = self.torch.zeros(n, dtype=self.torch.int64, device=self.device)
+            _check(self.L, self.L.etxmk_set_trace(self.h, self._trace.data_ptr()))
+        else:
+            _check(self.L, self.L.etxmk_set_trace(self.h, None))
+            self._trace = None
+
+    def trace(self) -> np.ndarray:
+        """Stamps of the last traced step in microseconds from the launch:
+        [phase][workgroup][wait done, arrive, first weight loads issued (GEMV phases; nan otherwise)]."""
+        self.sync()
+        t = self._trace.cpu().numpy().reshape(self.barriers_per_step() + 1, self.workgroups(), 3).astype(np.float64)
+        t0 = t[0, :, 0].min()
+        out = (t - t0) / 100.0
+        out[t == 0] = np.nan
+        return out
+
+    def workgroups(self) -> int:
+        import torch
+        return self._nwg or torch.cuda.get_device_properties(self.device).multi_processor_count
 
     def barriers_per_step(self) -> int:
         n = C.c_int32()

@@ -125,6 +125,13 @@ int etxmk_set_fused(etxmk_handle* h, int32_t fused);
  * (examples/vllm_llm/host.hip:954-1141). */
 int etxmk_set_dump(etxmk_handle* h, float* x_layers, int32_t* topk_ids, float* topk_w, float* router_logits);
 
+/* Phase timeline of the next fused steps (device pointer, may be NULL): uint64 [barriers_per_step + 1][workgroups][3];
+ * every workgroup writes the 100 MHz s_memrealtime clock when its wait for phase k's inputs returns ([k][wg][0];
+ * phase 0: the launch), when it arrives after phase k ([k][wg][1]) and, in GEMV phases, when its first weight
+ * loads are issued ([k][wg][2]).  Overwritten by each step.
+ * Reference: ETX_TRACE stamps (etx/codegen/kernel.py:346-347, etx/runtime/include/etx/host.h:143-145). */
+int etxmk_set_trace(etxmk_handle* h, uint64_t* stamps);
+
 /* Workgroups of the persistent launch (0 = one per CU). */
 int etxmk_set_grid(etxmk_handle* h, int32_t workgroups);
 /* Grid barriers executed by one step (diagnostics). */

@@ -11,8 +11,8 @@
  * results can be compared bit for bit:
  *
  *   dot64(w, x, K)   64 interleaved fp32 accumulators, acc[k % 64] = fma(w[k], x[k], acc[k % 64]) for
- *                    k ascending, then an xor butterfly: for off in 32,16,8,4,2,1: a[l] = a[l] + a[l ^ off];
- *                    the result is a[0].  Every matvec and every sum of squares uses it.
+ *                    k ascending, then the lane reduction of lanes_reduce() below (quad swaps, 8- and 16-lane
+ *                    mirrors, rows combined pairwise).  Every matvec and every sum of squares uses it.
  *   attention        chunks of 64 positions; per chunk the local max m_c, p_t = expf(s_t - m_c),
  *                    l_c and a_c[d] as ascending-t fma chains; chunks merged in ascending order with
  *                    w_c = expf(m_c - M):  L = fma(w_c, l_c, L), A[d] = fma(w_c, a_c[d], A[d]); o = bfr(A / L).
@@ -161,14 +161,18 @@ EXPORT void orc_gen_tokens(uint64_t seed, uint64_t stream, uint64_t n, uint32_t 
 }
 
 /* ------------------------------------------------------------------ reductions */
-static inline float butterfly64(float* a) {
-  for (int off = 32; off; off >>= 1) {
-    float t[64];
-    for (int l = 0; l < 64; ++l) t[l] = a[l] + a[l ^ off];
-    memcpy(a, t, sizeof t);
-  }
-  return a[0];
+/* The lane reduction of a wave64, in the order the gfx950 kernels combine lanes: partner l^1, then l^2 (both within
+ * a quad), then the mirror inside 8 lanes (l <-> 7-l), then the mirror inside 16 lanes (l <-> 15-l); after that
+ * each 16-lane row holds its row sum in every lane, and the rows are combined as (row0 + row1) + (row2 + row3). */
+static inline float lanes_reduce(float* a) {
+  float t[64];
+  for (int l = 0; l < 64; ++l) t[l] = a[l] + a[l ^ 1];
+  for (int l = 0; l < 64; ++l) a[l] = t[l] + t[l ^ 2];
+  for (int l = 0; l < 64; ++l) t[l] = a[l] + a[(l & ~7) | (7 - (l & 7))];
+  for (int l = 0; l < 64; ++l) a[l] = t[l] + t[(l & ~15) | (15 - (l & 15))];
+  return (a[0] + a[16]) + (a[32] + a[48]);
 }
+#define butterfly64 lanes_reduce
 /* canonical dot: w bf16, x fp32 (bf16-valued in every use), K a multiple of 64 */
 static inline float dot64(const uint16_t* w, const float* x, int K) {
   float acc[64];
