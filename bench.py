@@ -95,6 +95,8 @@ def main():
     ap.add_argument("--unfused", action="store_true")
     ap.add_argument("--workgroups", type=int, default=0)
     ap.add_argument("--trace", action="store_true", help="after timing, trace one fused step per phase (stderr)")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="profiling runs: first copy 1 GiB device to device, the known-size reference for HBM counters")
     ap.add_argument("--kv-fill", action="store_true",
                     help="profiling runs: fill the KV cache with seeded N(0,1) instead of prefilling the prompt")
     a = ap.parse_args()
@@ -112,6 +114,13 @@ def main():
     if a.ctx + a.warmup + a.steps + 1 > cfg.max_ctx:
         raise SystemExit(f"ctx {a.ctx} + warmup + steps exceeds max_ctx {cfg.max_ctx}")
     dev = torch.device("cuda:0")
+    if a.calib_copy:
+        src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+        log("[gpu] calibration copy: 1 GiB read + 1 GiB written")
     t0 = time.time()
     dec = N.Decoder(cfg, device="cuda:0", fused=not a.unfused, workgroups=a.workgroups)
     dec.init_weights(a.seed, 0.02)
@@ -224,6 +233,13 @@ def main():
     }
     if phase_us:
         out["phase_us"] = phase_us
+    # HBM bytes per launch from the committed counter passes (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of this
+    # workload, each scaled by the same counter's reading for a 1 GiB copy)
+    tf = ROOT / "profiles" / "etxmk_fused_qwen3-30b-a3b_b1_ctx1024_hbm_traffic.json"
+    if tf.exists() and not a.unfused:
+        t = json.loads(tf.read_text())
+        out["roofline"]["traffic"] = t["traffic_bytes_per_launch"]
+        out["roofline"]["traffic_source"] = f"profiles/{tf.name} (FETCH x{t['fetch_factor']}, WRITE x{t['write_factor']})"
     if not a.no_cpu:
         try:
             out["cpu_baseline"] = cpu_baseline(cfg, a.ctx, a.seed)

@@ -141,3 +141,53 @@ def test_qwen3_30b_a3b_two_layers(gpu):
     cfg = configs.with_layers(configs.QWEN3_30B_A3B, 2)
     say(f"[gpu] {cfg.name}")
     run_and_compare(cfg, prompt_len=6, n_new=6, check_every=3)
+
+
+def _full_greedy(cfg, prompt_len, n_new, seed=SEED):
+    """Full-depth model: the prompt fed token by token, then greedy steps; every token and the last step's
+    per-layer residuals and top-k against the oracle."""
+    import time
+    t0 = time.time()
+    dec, orc = make_pair(cfg, seed=seed)
+    say(f"[gpu]   weights ready in {time.time() - t0:.1f}s")
+    dec.enable_dumps(True)
+    prompt = O.gen_tokens(seed, prompt_len, cfg.V)
+    got = dec.generate(prompt, n_new)
+    d = dec.dumps()
+    seq = list(prompt)
+    for pos in range(prompt_len + n_new - 1):
+        last = pos == prompt_len + n_new - 2
+        if last:
+            tok, xo, ido, wo = orc.step(seq[pos], pos, dump=True)
+        else:
+            tok = orc.step(seq[pos], pos)
+        if pos + 1 >= prompt_len:
+            seq.append(tok)
+    ref = seq[prompt_len:]
+    say(f"[gpu]   oracle done in {time.time() - t0:.1f}s; tokens {list(got)[:8]}...")
+    match = sum(int(a == b) for a, b in zip(got, ref))
+    worst = max(rel(d["x"][L], xo[L]) for L in range(cfg.L))
+    assert match == n_new, f"{match}/{n_new} greedy tokens identical"
+    assert worst < 2e-2, f"per-layer max rel {worst:.3e}"
+    for L in range(cfg.L):
+        assert np.array_equal(d["x"][L], xo[L]), f"layer {L}: residual differs (max rel {rel(d['x'][L], xo[L]):.3e})"
+        if cfg.moe:
+            assert np.array_equal(d["ids"][L], ido[L]), f"layer {L}: top-k ids differ"
+    orc.close()
+    dec.close()
+
+
+@pytest.mark.timeout(900)
+def test_qwen3_30b_a3b_full_greedy_32(gpu):
+    """BASELINE configs[2] at full depth: 48 layers, 128 experts, vocab 151936; 32 greedy tokens identical."""
+    cfg = configs.QWEN3_30B_A3B
+    say(f"[gpu] full {cfg.name}: 32-token prompt + 32 greedy")
+    _full_greedy(cfg, prompt_len=32, n_new=32)
+
+
+@pytest.mark.timeout(900)
+def test_qwen3_8b_full_greedy_32(gpu):
+    """BASELINE configs[1] at full depth: 36 dense layers, vocab 151936; 32 greedy tokens identical."""
+    cfg = configs.QWEN3_8B
+    say(f"[gpu] full {cfg.name}: 32-token prompt + 32 greedy")
+    _full_greedy(cfg, prompt_len=32, n_new=32)
