@@ -92,10 +92,9 @@ struct Smem {
     } a;
   };
   float rs;
-  int32_t ids[MAX_TOPK];
-  float wts[MAX_TOPK];
-  int32_t order[MAX_TOPK];
-  alignas(16) float prob[MAX_E];
+  int32_t ids[NWAVE][MAX_TOPK];         // routing, one private copy per wave (no workgroup barrier needed)
+  float wts[NWAVE][MAX_TOPK];
+  int32_t order[NWAVE][MAX_TOPK];
   int32_t abort;
   int32_t last;
   int32_t phase;                        // arrivals so far (the current phase index), for trace stamps
@@ -493,7 +492,7 @@ __device__ __forceinline__ void phase_qkv(const Params& p, int layer, Smem& s, W
         }
         return true;
       },
-      p.nwg);
+      p.nwg, p.trace, s.phase);
 }
 
 // P2: per (kv head, 64-position chunk): q/k RMSNorm and neox RoPE of the group's heads (ref_numpy.py:116-120),
@@ -703,7 +702,7 @@ __device__ __forceinline__ void phase_oproj(const Params& p, int layer, Smem& s,
         __syncthreads();
         return true;
       },
-      p.nwg);
+      p.nwg, p.trace, s.phase);
 }
 
 // P4: post-attention RMSNorm + router GEMV (ref_numpy.py:131-134)
@@ -723,79 +722,82 @@ __device__ __forceinline__ void phase_router(const Params& p, int layer, Smem& s
         build_norm_x<KK>(p, p.x, nullptr, Lw.ln2, s);
         return true;
       },
-      p.nwg);
+      p.nwg, p.trace, s.phase);
 }
 
-// softmax top-k over the router logits (ref_numpy.py:135-140) into s.ids / s.wts / s.order.  Wave 0 forms the
-// fp32 probabilities (max, exp, the dot-order sum, divide); then every thread t < E ranks expert t by counting the
-// experts that precede it in (probability descending, id ascending) order, which selects exactly what K rounds of
-// "largest probability, lowest id first" select.  Every workgroup recomputes it, so no phase is spent on it.
+// softmax top-k over the router logits (ref_numpy.py:135-140).  Every wave computes it on its own, in registers:
+// fp32 probabilities (max, exp, the dot-order sum, divide), then K rounds of "largest probability, lowest id
+// first" (a wave max, then the lowest lane of the first 64-expert word whose ballot holds it); a chosen expert
+// drops to -2, below every probability and below the -1 of absent experts.  The chosen probabilities are
+// renormalised in slot order and rounded to bf16; `order` lists the slots by ascending expert id (the index_add_
+// order of the combine).  Results land in the wave's private LDS row s.ids/wts/order[wave].
 template <int EC = 0>
 __device__ __forceinline__ void route_topk(const Params& p, Smem& s) {
-  constexpr int EMAX = EC > 0 ? EC : MAX_E;               // compile-time expert count when known
+  constexpr int EMAX = EC > 0 ? EC : MAX_E;
+  constexpr int NW = (EMAX + 63) / 64;
   const int E = EC > 0 ? EC : p.E, K = p.TOPK;
-  if (threadIdx.x < MAX_TOPK) { s.ids[threadIdx.x] = 0; s.wts[threadIdx.x] = 0.0f; }
-  if (wave_id() == 0) {
-    const int lane = lane_id();
-    constexpr int NW = (EMAX + 63) / 64;
-    float lv[NW];
+  const int lane = lane_id(), wave = wave_u();
+  float pv[NW];
 #pragma unroll
-    for (int w = 0; w < NW; ++w) {
-      const int e = lane + 64 * w;
-      lv[w] = e < E ? ld_ag(p.logits + e) : -__builtin_huge_valf();
-    }
-    float m = lv[0];
-#pragma unroll
-    for (int w = 1; w < NW; ++w) m = fmaxf(m, lv[w]);
-    m = wave_max(m);
-    float acc = 0.0f;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) {
-      const int e = lane + 64 * w;
-      lv[w] = e < E ? expf_mk(lv[w] - m) : 0.0f;
-      if (e < E) acc = acc + lv[w];
-    }
-    const float S = wave_sum(acc);
-#pragma unroll
-    for (int w = 0; w < NW; ++w) {
-      const int e = lane + 64 * w;
-      if (e < E) s.prob[e] = lv[w] / S;
-    }
+  for (int w = 0; w < NW; ++w) {
+    const int e = lane + 64 * w;
+    pv[w] = e < E ? ld_ag(p.logits + e) : -__builtin_huge_valf();
   }
-  __syncthreads();
-  const int e = threadIdx.x;
-  if (e < E) {                                            // E is a multiple of 4 (checked by the host)
-    const float pe = s.prob[e];
-    int rank = 0;
+  float m = pv[0];
 #pragma unroll
-    for (int f = 0; f < EMAX; f += 4) {
-      if (EC > 0 || f < E) {
-        const float4 q = *(const float4*)&s.prob[f];      // the same 16 bytes for every lane: an LDS broadcast
-        rank += (q.x > pe || (q.x == pe && f < e)) ? 1 : 0;
-        rank += (q.y > pe || (q.y == pe && f + 1 < e)) ? 1 : 0;
-        rank += (q.z > pe || (q.z == pe && f + 2 < e)) ? 1 : 0;
-        rank += (q.w > pe || (q.w == pe && f + 3 < e)) ? 1 : 0;
+  for (int w = 1; w < NW; ++w) m = fmaxf(m, pv[w]);
+  m = wave_max(m);
+  float acc = 0.0f;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    const int e = lane + 64 * w;
+    pv[w] = e < E ? expf_mk(pv[w] - m) : 0.0f;
+    if (e < E) acc = acc + pv[w];
+  }
+  const float S = wave_sum(acc);
+#pragma unroll
+  for (int w = 0; w < NW; ++w) pv[w] = lane + 64 * w < E ? pv[w] / S : -1.0f;
+  int ids[MAX_TOPK];
+  float pk[MAX_TOPK];
+  float sel = 0.0f;
+#pragma unroll
+  for (int k = 0; k < MAX_TOPK; ++k) {
+    ids[k] = 0;
+    pk[k] = 0.0f;
+    if (k < K) {
+      float b = pv[0];
+#pragma unroll
+      for (int w = 1; w < NW; ++w) b = fmaxf(b, pv[w]);
+      b = wave_max(b);
+      int id = -1;
+#pragma unroll
+      for (int w = NW - 1; w >= 0; --w) {
+        const uint64_t hit = __ballot(pv[w] == b);
+        if (hit) id = 64 * w + __builtin_ctzll(hit);
       }
+#pragma unroll
+      for (int w = 0; w < NW; ++w)
+        if (lane + 64 * w == id) pv[w] = -2.0f;
+      ids[k] = id < 0 ? 0 : id;                           // only NaN logits leave no hit; keep the index in range
+      pk[k] = b;
+      sel = sel + b;
     }
-    if (rank < K) { s.ids[rank] = e; s.wts[rank] = pe; }
   }
-  __syncthreads();
-  if (wave_id() == 0) {                                    // lane k holds slot k
-    const int lane = lane_id();
-    const float w = lane < K ? s.wts[lane] : 0.0f;
-    const int id = lane < K ? s.ids[lane] : 0x7fffffff;
-    float sel = 0.0f;                                     // selection-order sum of the chosen probabilities
-    int before = 0;                                       // slots whose expert id is lower: position in id order
-    for (int k = 0; k < K; ++k) {
-      sel = sel + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), k));
-      before += __builtin_amdgcn_readlane(id, k) < id ? 1 : 0;
-    }
+  if (lane < MAX_TOPK) {
+    int id = 0, before = 0;
+    float wk = 0.0f;
+#pragma unroll
+    for (int k = 0; k < MAX_TOPK; ++k)
+      if (k == lane) { id = ids[k]; wk = pk[k]; }
+#pragma unroll
+    for (int k = 0; k < MAX_TOPK; ++k)
+      if (k < K && ids[k] < id) ++before;
     if (lane < K) {
-      s.wts[lane] = bfr(p.norm_topk ? w / sel : w);
-      s.order[before] = lane;                             // slots in ascending expert id (index_add_ order)
+      s.ids[wave][lane] = id;
+      s.wts[wave][lane] = bfr(p.norm_topk ? wk / sel : wk);
+      s.order[wave][before] = lane;
     }
   }
-  __syncthreads();
 }
 
 // P5: experts gate/up + SiLU*up for the top-k slots (ref_numpy.py:142-145).  The normed input depends only on x
@@ -811,8 +813,8 @@ __device__ __forceinline__ void phase_expert_up(const Params& p, int layer, Smem
   route_topk<EC>(p, s);
   if (blockIdx.x == 0 && threadIdx.x < 64) {
     const int t = threadIdx.x;
-    if (p.dump_ids && t < KT) st_i(p.dump_ids + (size_t)layer * KT + t, s.ids[t]);
-    if (p.dump_wts && t < KT) st_f(p.dump_wts + (size_t)layer * KT + t, s.wts[t]);
+    if (p.dump_ids && t < KT) st_i(p.dump_ids + (size_t)layer * KT + t, s.ids[0][t]);
+    if (p.dump_wts && t < KT) st_f(p.dump_wts + (size_t)layer * KT + t, s.wts[0][t]);
     if (p.dump_logits)
       for (int e = t; e < p.E; e += 64) st_f(p.dump_logits + (size_t)layer * p.E + e, ld_ag(p.logits + e));
   }
@@ -820,7 +822,7 @@ __device__ __forceinline__ void phase_expert_up(const Params& p, int layer, Smem
       KT * MI,
       [&](int g, int i) -> const uint16_t* {
         const int slot = g / MI, jj = g - slot * MI;
-        return W + ((size_t)s.ids[slot] * 2 * MI + 2 * jj + i) * KK;
+        return W + ((size_t)s.ids[wave_u()][slot] * 2 * MI + 2 * jj + i) * KK;
       },
       [&](int) { return (const uint16_t*)s.g.xs; },
       [&](int g, const float(&v)[2]) {
@@ -835,21 +837,21 @@ template <int KK, class Wait, bool ROUTED = false>
 __device__ __forceinline__ void phase_expert_down(const Params& p, int layer, Smem& s, Wait wait) {
   const LayerW Lw = layer_w(p, layer);
   const int H = p.H, KT = p.TOPK;
-  if constexpr (!ROUTED) route_topk(p, s);                 // the persistent kernel kept expert_up's routing in LDS
+  if constexpr (!ROUTED) route_topk(p, s);                 // the persistent kernel keeps expert_up's routing in LDS
   float* x = p.x;
   const uint16_t* W = Lw.w2;
   gemv_run<KK, MAX_TOPK>(
       H,
-      [&](int g, int i) -> const uint16_t* { return i < KT ? W + ((size_t)s.ids[i] * H + g) * KK : nullptr; },
+      [&](int g, int i) -> const uint16_t* { return i < KT ? W + ((size_t)s.ids[wave_u()][i] * H + g) * KK : nullptr; },
       [&](int i) { return (const uint16_t*)(s.g.xs + (size_t)i * KK); },
       [&](int g, const float(&v)[MAX_TOPK]) {
         if (lane_id() == 0) {
           float y[MAX_TOPK];
 #pragma unroll
-          for (int i = 0; i < MAX_TOPK; ++i) y[i] = i < KT ? bfr(bfr(v[i]) * s.wts[i]) : 0.0f;
+          for (int i = 0; i < MAX_TOPK; ++i) y[i] = i < KT ? bfr(bfr(v[i]) * s.wts[wave_u()][i]) : 0.0f;
           float acc = 0.0f;
           for (int k = 0; k < KT; ++k) {
-            const int o = s.order[k];
+            const int o = s.order[wave_u()][k];
             float yk = 0.0f;
 #pragma unroll
             for (int i = 0; i < MAX_TOPK; ++i) yk = (o == i) ? y[i] : yk;
@@ -865,7 +867,7 @@ __device__ __forceinline__ void phase_expert_down(const Params& p, int layer, Sm
         __syncthreads();
         return true;
       },
-      p.nwg);
+      p.nwg, p.trace, s.phase);
 }
 
 // dense MLP (ref_numpy.py:149-152): P4' gate/up + SiLU*up, P5' down + residual
@@ -886,7 +888,7 @@ __device__ __forceinline__ void phase_gateup(const Params& p, int layer, Smem& s
         build_norm_x<KK>(p, p.x, nullptr, Lw.ln2, s);
         return true;
       },
-      p.nwg);
+      p.nwg, p.trace, s.phase);
 }
 
 template <int KK, class Wait>
@@ -908,7 +910,7 @@ __device__ __forceinline__ void phase_down(const Params& p, int layer, Smem& s, 
         __syncthreads();
         return true;
       },
-      p.nwg);
+      p.nwg, p.trace, s.phase);
 }
 
 // P7: final norm + lm_head + per-wave argmax folded into one 64-bit key (ref_numpy.py:155-158; first maximum wins)
@@ -946,7 +948,7 @@ __device__ __forceinline__ void phase_head(const Params& p, Smem& s, Wait wait) 
           for (int i = threadIdx.x; i < KK; i += NT) st_f(p.dump_x + (size_t)(p.l1 - 1) * KK + i, s.g.xf[i]);
         return true;
       },
-      p.nwg);
+      p.nwg, p.trace, s.phase);
   if (ran && lane_id() == 0 && best) __hip_atomic_fetch_max(p.amax, best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
