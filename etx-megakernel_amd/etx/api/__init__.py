@@ -13,15 +13,16 @@ from dataclasses import dataclass
 from etx.api.types import SCHEMA_VERSION, Configuration, KernelSpec, WorkloadSpec
 
 __all__ = ["SCHEMA_VERSION", "Configuration", "KernelSpec", "WorkloadSpec", "DecodeSession", "build_model",
-           "decode_workload"]
+           "decode_workload", "checkpoint_workload"]
 
 _MODEL_KEYS = {"H", "NH", "NKV", "HD", "L", "V", "I", "E", "TOPK", "MI", "moe", "qk_norm", "norm_topk",
                "block_size", "max_ctx", "batch", "eps", "theta"}
-_RUN_KEYS = {"fused", "workgroups", "seed", "weight_scale"}
+_RUN_KEYS = {"fused", "workgroups", "seed", "weight_scale", "checkpoint"}
 
 
 def decode_workload(name: str, model: dict, **run) -> WorkloadSpec:
-    """A native decode workload: model dimensions plus run options (fused, workgroups, seed, weight_scale)."""
+    """A native decode workload: model dimensions plus run options (fused, workgroups, seed, weight_scale, or
+    checkpoint: a packed weights.bin + llm.manifest directory, whose weights replace the seeded ones)."""
     bad = set(run) - _RUN_KEYS
     if bad:
         raise ValueError(f"unknown run options {sorted(bad)}")
@@ -58,6 +59,23 @@ def build_model(workload: WorkloadSpec, device: str = "cuda:0") -> DecodeSession
     run = cfg.get("run", {})
     from etx.runtime.native import Decoder, ModelConfig
     mc = ModelConfig(name=workload.name, **model)
+    ck = None
+    if run.get("checkpoint"):
+        from etx.models.checkpoint import Checkpoint
+        ck = Checkpoint(run["checkpoint"])
+        ck.check(mc)                           # dimensions and tensors agree before any device memory is taken
     dec = Decoder(mc, device=device, fused=bool(run.get("fused", True)), workgroups=int(run.get("workgroups", 0)))
-    dec.init_weights(int(run.get("seed", 0)), float(run.get("weight_scale", 0.02)))
+    if ck is not None:
+        ck.load_into(dec)
+    else:
+        dec.init_weights(int(run.get("seed", 0)), float(run.get("weight_scale", 0.02)))
     return DecodeSession(workload, dec)
+
+
+def checkpoint_workload(path, name: str = "", max_ctx: int = 0, **run) -> WorkloadSpec:
+    """The native decode workload of a packed checkpoint directory (dimensions from its llm.manifest)."""
+    from etx.models.checkpoint import Checkpoint
+    ck = Checkpoint(path)
+    mc = ck.config(max_ctx=max_ctx)
+    model = {k: v for k, v in mc.as_dict().items() if k in _MODEL_KEYS}
+    return decode_workload(name or mc.name, model, checkpoint=str(path), **run)

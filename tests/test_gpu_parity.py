@@ -27,9 +27,13 @@ def rel(a, b):
     return float(np.max(np.abs(a - b)) / max(float(np.max(np.abs(b))), 1e-30))
 
 
-def make_pair(cfg, fused=True, seed=SEED):
+def make_pair(cfg, fused=True, seed=SEED, loader=None):
+    """The library (weights from the seeded generator, or from loader(dec)) and the oracle on the seeded weights."""
     dec = N.Decoder(cfg, fused=fused)
-    dec.init_weights(seed, 0.02)
+    if loader is None:
+        dec.init_weights(seed, 0.02)
+    else:
+        loader(dec)
     orc = O.OracleModel(cfg.as_dict(), seed, 0.02)
     return dec, orc
 
@@ -56,8 +60,8 @@ def test_seeded_weights_bit_exact(gpu, cfg):
     orc.close()
 
 
-def run_and_compare(cfg, prompt_len, n_new, fused=True, block_table=None, check_every=1):
-    dec, orc = make_pair(cfg, fused=fused)
+def run_and_compare(cfg, prompt_len, n_new, fused=True, block_table=None, check_every=1, loader=None):
+    dec, orc = make_pair(cfg, fused=fused, loader=loader)
     if block_table is not None:
         dec.set_block_table(block_table)
         orc.set_block_table(block_table)
@@ -97,6 +101,31 @@ def run_and_compare(cfg, prompt_len, n_new, fused=True, block_table=None, check_
 def test_tiny_decode_bit_exact(gpu, cfg, fused):
     say(f"[gpu] tiny decode {cfg.name} fused={fused}")
     run_and_compare(cfg, prompt_len=12, n_new=8, fused=fused)
+
+
+@pytest.mark.parametrize("cfg", [configs.TINY_MOE, configs.TINY_DENSE], ids=["moe", "dense"])
+def test_checkpoint_decode_bit_exact(gpu, tmp_path, cfg):
+    """Weights read from a packed checkpoint (weights.bin + llm.manifest, written from the seeded tensors) instead of
+    the generator: the same tokens, residuals and caches as the oracle."""
+    from test_checkpoint import write_from_oracle
+    say(f"[gpu] checkpoint decode {cfg.name}")
+    ck = write_from_oracle(tmp_path / "ck", cfg)
+    assert ck.config(max_ctx=cfg.max_ctx) == cfg
+    run_and_compare(cfg, prompt_len=10, n_new=6, loader=ck.load_into)
+
+
+def test_checkpoint_tied_head(gpu, tmp_path):
+    """A tied checkpoint has no lm_head; the library's head rows are the embedding rows."""
+    from test_checkpoint import write_from_oracle
+    cfg = configs.TINY_DENSE
+    say(f"[gpu] tied checkpoint {cfg.name}")
+    ck = write_from_oracle(tmp_path / "ck", cfg, tie=True)
+    dec = N.Decoder(cfg)
+    ck.load_into(dec)
+    emb = ck.array("embed", (cfg.V, cfg.H))
+    assert np.array_equal(dec.tensor(N.T_EMBED), emb)
+    assert np.array_equal(dec.tensor(N.T_LMHEAD), emb)
+    dec.close()
 
 
 def test_tiny_decode_shuffled_block_table(gpu):
