@@ -18,6 +18,8 @@ import json
 import os
 import sys
 import time
+
+import numpy as np
 from pathlib import Path
 
 ROOT = Path(__file__).resolve().parent
@@ -84,6 +86,39 @@ def cpu_baseline(cfg, ctx: int, seed: int) -> dict:
             "tokens_per_s": round(1e3 / ms, 3), "effective_GBps": round(bytes_per_token(cfg, ctx)["total"] / ms / 1e6, 2)}
 
 
+def trace_summary(t, cfg):
+    """Per-phase timeline of one traced step.  t[k][wg] = (wait for phase k's inputs returned, arrived after phase k,
+    first weight loads issued (GEMV phases) / chunk partials issued (attention)), microseconds from the launch."""
+    names = (["qkv", "attn", "oproj", "router", "expert_up", "expert_down"] if cfg.moe
+             else ["qkv", "attn", "oproj", "gateup", "down"])
+    nl = len(names)
+    nb = nl * cfg.L
+    end = np.nanmax(t[:, :, 1], axis=1)                   # phase k complete: last arrival
+    span = np.diff(np.concatenate([[0.0], end[:nb + 1]]))
+    per = span[:nb].reshape(cfg.L, nl)
+    phase_us = {n: round(float(per[:, i].mean()), 2) for i, n in enumerate(names)}
+    phase_us["head"] = round(float(span[nb]), 2)
+    avg = lambda v: {n: round(float(np.nanmean(v.reshape(cfg.L, nl)[:, i])), 2) for i, n in enumerate(names)}
+    lag = np.full(nb, np.nan)
+    lag[1:] = np.nanmedian(t[1:nb, :, 0], axis=1) - end[:nb - 1]
+    lagmax = np.full(nb, np.nan)
+    lagmax[1:] = np.nanmax(t[1:nb, :, 0], axis=1) - end[:nb - 1]
+    work = np.full(nb, np.nan)
+    work[1:] = np.nanmedian(t[1:nb, :, 1] - t[1:nb, :, 0], axis=1)
+    wmax = np.full(nb, np.nan)
+    wmax[1:] = np.nanmax(t[1:nb, :, 1] - t[1:nb, :, 0], axis=1)
+    s2 = np.full(nb, np.nan)
+    s2[1:] = np.nanmedian(t[1:nb, :, 2] - t[1:nb, :, 0], axis=1)
+    phase_us["barrier_median"] = round(float(np.nanmedian(lag)), 2)
+    log(f"[gpu] traced step {end[-2]:.1f} us; per-layer phase spans (us) {phase_us}")
+    log("[gpu] barrier (us), last arrival -> wait returned, median / last workgroup: "
+        + str({n: (avg(lag)[n], avg(lagmax)[n]) for n in names}))
+    log("[gpu] work after the wait (us), median / max workgroup: " + str({n: (avg(work)[n], avg(wmax)[n]) for n in names}))
+    log("[gpu] slot 2 relative to the wait (us; GEMV: weight loads issued, negative = before; attention: partials "
+        "issued): " + str(avg(s2)))
+    return phase_us
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -95,6 +130,7 @@ def main():
     ap.add_argument("--unfused", action="store_true")
     ap.add_argument("--workgroups", type=int, default=0)
     ap.add_argument("--trace", action="store_true", help="after timing, trace one fused step per phase (stderr)")
+    ap.add_argument("--trace-out", default="", help="with --trace: also save the raw stamps (.npy)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="profiling runs: first copy 1 GiB device to device, the known-size reference for HBM counters")
     ap.add_argument("--kv-fill", action="store_true",
@@ -173,45 +209,11 @@ def main():
         dec.enable_trace(True)
         dec.step(pos, write_next=True)
         pos += 1
-        t = dec.trace()                                   # [phase][wg][wait done, arrive], us from launch
+        t = dec.trace()                                   # [phase][wg][wait done, arrive, loads issued], us
         dec.enable_trace(False)
-        names = (["qkv", "attn", "oproj", "router", "expert_up", "expert_down"] if cfg.moe
-                 else ["qkv", "attn", "oproj", "gateup", "down"])
-        nb = len(names) * cfg.L
-        end = np.nanmax(t[:, :, 1], axis=1)               # phase k complete: last arrival
-        span = np.diff(np.concatenate([[0.0], end[:nb + 1]]))
-        start_work = np.nanmedian(t[1:nb + 1, :, 0], axis=1)  # median wait-done of phase k (k >= 1)
-        per = span[:nb].reshape(cfg.L, len(names))
-        phase_us = {n: round(float(per[:, i].mean()), 2) for i, n in enumerate(names)}
-        phase_us["head"] = round(float(span[nb]), 2)
-        # barrier latency seen by the median workgroup: last arrival of phase k-1 -> its wait return in phase k
-        lag = start_work - end[:nb]
-        phase_us["barrier_median"] = round(float(np.median(lag)), 2)
-        # work of a phase: median over workgroups of arrive - wait-done (phase 0 has no wait)
-        work = np.full(nb, np.nan)
-        work[1:] = np.nanmedian(t[1:nb, :, 1] - t[1:nb, :, 0], axis=1)
-        wk = work.reshape(cfg.L, len(names))
-        log(f"[gpu] traced step {end[-2]:.1f} us; per-layer phase spans (us) {phase_us}")
-        wmax = np.full(nb, np.nan)
-        wmax[1:] = np.nanmax(t[1:nb, :, 1] - t[1:nb, :, 0], axis=1)
-        lagmax = np.full(nb, np.nan)
-        lagmax[1:] = np.nanmax(t[1:nb, :, 0], axis=1) - end[:nb - 1]
-        log("[gpu] per-workgroup work after its wait (us), median / max: " +
-            str({n: (round(float(np.nanmean(wk[:, i])), 2), round(float(np.nanmean(wmax.reshape(cfg.L, -1)[:, i])), 2))
-                 for i, n in enumerate(names)}))
-        log("[gpu] barrier lag (us), last arrival -> last wait return: " +
-            str({n: round(float(np.nanmean(lagmax.reshape(cfg.L, -1)[:, i])), 2) for i, n in enumerate(names)}))
-        issued = np.full(nb, np.nan)
-        issued[1:] = np.nanmedian(t[1:nb, :, 2] - end[:nb - 1, None], axis=1)
-        log("[gpu] first weight loads issued, median after the previous phase completed (us): " +
-            str({n: round(float(np.nanmean(issued.reshape(cfg.L, -1)[:, i])), 2) for i, n in enumerate(names)}))
-        # which workgroups are the slowest in the expert phases
-        for i, n in enumerate(names):
-            ks = np.arange(i, nb, len(names))
-            ks = ks[ks >= 1]
-            wdur = np.nan_to_num(t[ks, :, 1] - t[ks, :, 0])
-            slow = np.argsort(-wdur.mean(axis=0))[:6]
-            log(f"[gpu]   {n}: slowest workgroups {slow.tolist()} mean work {np.round(wdur.mean(axis=0)[slow], 2).tolist()}")
+        if a.trace_out:
+            np.save(a.trace_out, t)
+        phase_us = trace_summary(t, cfg)
     out = {
         "metric": METRIC, "value": round(ms, 4), "unit": "ms/token", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
         "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,

@@ -614,14 +614,18 @@ __device__ __forceinline__ void phase_attn(const Params& p, int layer, Smem& s, 
       float a0 = 0.0f, a1 = 0.0f, l = 0.0f;
 #pragma unroll
       for (int hb = 0; hb < CHUNK / 8; ++hb) {
+        // one 16-byte read per dim half (8 positions of this lane's dim) and two for the 8 probabilities:
+        // conflict-free, where per-position dword reads of the 16-byte-strided tile conflict 4 ways
+        const u32x4 w0 = s.a.vt[hb][0][lane], w1 = s.a.vt[hb][1][lane];
+        const float4 pa = *(const float4*)&s.a.p[j][hb * 8], pb = *(const float4*)&s.a.p[j][hb * 8 + 4];
+        const float pp[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const int tt = hb * 8 + e;
           if (tt < len) {
-            const float pt = s.a.p[j][tt];
-            const uint32_t w0 = s.a.vt[hb][0][lane][e >> 1], w1 = s.a.vt[hb][1][lane][e >> 1];
-            const float v0 = (e & 1) ? bf_hi(w0) : bf_lo(w0);
-            const float v1 = (e & 1) ? bf_hi(w1) : bf_lo(w1);
+            const float pt = pp[e];
+            const float v0 = (e & 1) ? bf_hi(w0[e >> 1]) : bf_lo(w0[e >> 1]);
+            const float v1 = (e & 1) ? bf_hi(w1[e >> 1]) : bf_lo(w1[e >> 1]);
             a0 = __builtin_fmaf(pt, v0, a0);
             a1 = __builtin_fmaf(pt, v1, a1);
             l = l + pt;
@@ -633,6 +637,8 @@ __device__ __forceinline__ void phase_attn(const Params& p, int layer, Smem& s, 
       st_ag(part + lane + 64, a1);
       if (lane == 0) { st_ag(part + HD, s.a.m[j]); st_ag(part + HD + 1, l); }
     }
+    if (p.trace && threadIdx.x == 0)                      // slot 2 of the attention phase: chunk partials issued
+      *(MK_G uint64_t*)(p.trace + ((size_t)s.phase * p.nwg + blockIdx.x) * 3 + 2) = __builtin_amdgcn_s_memrealtime();
     // the last chunk of kv head g to arrive merges: M = max m_c, w_c = exp(m_c - M), L = sum w_c l_c,
     // A[d] = sum w_c a_c[d] (ascending c), o = bfr(A / L)
     __builtin_amdgcn_s_waitcnt(0);

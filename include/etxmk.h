@@ -128,7 +128,7 @@ int etxmk_set_dump(etxmk_handle* h, float* x_layers, int32_t* topk_ids, float* t
 /* Phase timeline of the next fused steps (device pointer, may be NULL): uint64 [barriers_per_step + 1][workgroups][3];
  * every workgroup writes the 100 MHz s_memrealtime clock when its wait for phase k's inputs returns ([k][wg][0];
  * phase 0: the launch), when it arrives after phase k ([k][wg][1]) and, in GEMV phases, when its first weight
- * loads are issued ([k][wg][2]).  Overwritten by each step.
+ * loads are issued ([k][wg][2]; attention: when its chunk partials are issued).  Overwritten by each step.
  * Reference: ETX_TRACE stamps (etx/codegen/kernel.py:346-347, etx/runtime/include/etx/host.h:143-145). */
 int etxmk_set_trace(etxmk_handle* h, uint64_t* stamps);
 
