@@ -18,6 +18,8 @@
 #include <stdint.h>
 #include <string.h>
 
+#include <type_traits>
+
 #include "etxmk.h"
 #include "mk_numerics.h"
 
@@ -610,19 +612,18 @@ __device__ __forceinline__ void phase_attn(const Params& p, int layer, Smem& s, 
     }
     __syncthreads();
     // V (:127-128): lanes = dims (lane, lane + 64); a = sum_t p_t v_t[d] and l = sum_t p_t, ascending t
-    for (int j = wave; j < G; j += NWAVE) {
-      float a0 = 0.0f, a1 = 0.0f, l = 0.0f;
+    // one 16-byte read per dim half (8 positions of this lane's dim) and two for the 8 probabilities: conflict-free,
+    // where per-position dword reads of the 16-byte-strided tile conflict 4 ways.  Full chunks take the loop without
+    // position tests (per-position tests would be hoisted as 64 scalar masks); only a head's last chunk is partial.
+    auto pv = [&](int j, auto full, float& a0, float& a1, float& l) {
 #pragma unroll
       for (int hb = 0; hb < CHUNK / 8; ++hb) {
-        // one 16-byte read per dim half (8 positions of this lane's dim) and two for the 8 probabilities:
-        // conflict-free, where per-position dword reads of the 16-byte-strided tile conflict 4 ways
         const u32x4 w0 = s.a.vt[hb][0][lane], w1 = s.a.vt[hb][1][lane];
         const float4 pa = *(const float4*)&s.a.p[j][hb * 8], pb = *(const float4*)&s.a.p[j][hb * 8 + 4];
         const float pp[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const int tt = hb * 8 + e;
-          if (tt < len) {
+          if (decltype(full)::value || hb * 8 + e < len) {
             const float pt = pp[e];
             const float v0 = (e & 1) ? bf_hi(w0[e >> 1]) : bf_lo(w0[e >> 1]);
             const float v1 = (e & 1) ? bf_hi(w1[e >> 1]) : bf_lo(w1[e >> 1]);
@@ -632,6 +633,11 @@ __device__ __forceinline__ void phase_attn(const Params& p, int layer, Smem& s, 
           }
         }
       }
+    };
+    for (int j = wave; j < G; j += NWAVE) {
+      float a0 = 0.0f, a1 = 0.0f, l = 0.0f;
+      if (len == CHUNK) pv(j, std::true_type{}, a0, a1, l);
+      else pv(j, std::false_type{}, a0, a1, l);
       float* part = p.apart + ((size_t)(g * G + j) * MAX_CHUNKS + c) * PART;
       st_ag(part + lane, a0);
       st_ag(part + lane + 64, a1);
@@ -651,24 +657,30 @@ __device__ __forceinline__ void phase_attn(const Params& p, int layer, Smem& s, 
     if (s.last) {
       for (int j = wave; j < G; j += NWAVE) {
         const float* part = p.apart + (size_t)(g * G + j) * MAX_CHUNKS * PART;
-        // lane cc holds chunk cc's (m, l); the chunk weights go through LDS for the ordered sums
+        // lane cc holds chunk cc's (m, l); the chunk weights go through LDS for the ordered sums.  The first MB
+        // chunks' a[] are loaded together with (m, l) (they do not depend on the maximum): one memory round trip.
+        constexpr int MB = 18;
+        float av0[MB], av1[MB];
+        auto load_a = [&](int c0) {
+#pragma unroll
+          for (int u = 0; u < MB; ++u) {
+            const int c = min(c0 + u, nch - 1);             // past the last chunk: a repeat, never used
+            av0[u] = ld_ag(part + (size_t)c * PART + lane);
+            av1[u] = ld_ag(part + (size_t)c * PART + lane + 64);
+          }
+        };
         float mloc = -__builtin_huge_valf(), lloc = 0.0f;
         if (lane < nch) { mloc = ld_ag(part + (size_t)lane * PART + HD); lloc = ld_ag(part + (size_t)lane * PART + HD + 1); }
+        load_a(0);
         const float M = wave_max(mloc);
         const float w = lane < nch ? expf_mk(mloc - M) : 0.0f;
         s.a.p[j][lane] = w;
         s.a.p[j][64 + lane] = lloc;
         float Ls = 0.0f, A0 = 0.0f, A1 = 0.0f;
-        for (int c0 = 0; c0 < nch; c0 += 16) {
-          float av0[16], av1[16];
+        for (int c0 = 0; c0 < nch; c0 += MB) {
+          if (c0 > 0) load_a(c0);
 #pragma unroll
-          for (int u = 0; u < 16; ++u)
-            if (c0 + u < nch) {
-              av0[u] = ld_ag(part + (size_t)(c0 + u) * PART + lane);
-              av1[u] = ld_ag(part + (size_t)(c0 + u) * PART + lane + 64);
-            }
-#pragma unroll
-          for (int u = 0; u < 16; ++u)
+          for (int u = 0; u < MB; ++u)
             if (c0 + u < nch) {
               const float wc = s.a.p[j][c0 + u];
               Ls = __builtin_fmaf(wc, s.a.p[j][64 + c0 + u], Ls);
