@@ -490,6 +490,10 @@ static int launch(etxmk_handle* h, int pos, int write_next, int l0, int l1, int 
   p.pos = pos; p.write_next = write_next; p.l0 = l0; p.l1 = l1; p.do_embed = embed; p.do_head = head;
   p.nwg = h->nwg;
   p.spin_ticks = 200000000ull;            // 2 s of the 100 MHz s_memrealtime clock
+  {                                        // QKV rows staged in LDS a layer ahead when a workgroup's share fits
+    const int rows = (c.NH + 2 * c.NKV) * c.HD, R = (rows + h->nwg - 1) / h->nwg;
+    p.qkv_rows = (h->fused && c.H % 512 == 0 && (uint64_t)R * c.H * 2 <= (uint64_t)QKVW_BYTES) ? R : 0;
+  }
   if (h->fused) {
     const void* fn = fused_kernel(c);
     if (!fn) return fail(ETXMK_EINVAL, "no persistent kernel for H %d, NH*HD %d, %s %d (use the unfused mode)", c.H,

@@ -37,6 +37,7 @@ constexpr int MAX_G = 16;               // q heads per kv head
 constexpr int MAX_E = 256;
 constexpr int MAX_TOPK = 8;
 constexpr int PART = HDIM + 2;          // attention partial: a[HD], m, l
+constexpr int QKVW_BYTES = 81920;       // the workgroup's rows of the next layer's QKV matrix, staged in LDS
 
 struct LayerW {
   const uint16_t *ln1, *ln2, *qn, *kn;
@@ -73,6 +74,7 @@ struct Params {
   float* dump_logits;
   uint64_t* trace;                      // optional: [phase][workgroup][wait done, arrive, loads issued] stamps
   int pos, write_next, l0, l1, do_embed, do_head;
+  int qkv_rows;                         // > 0: QKV rows per workgroup staged in LDS one layer ahead (fused mode)
   uint32_t bar_base;
   int nwg;
   uint64_t spin_ticks;
@@ -93,6 +95,7 @@ struct Smem {
       float m[MAX_G];
     } a;
   };
+  alignas(16) u32x4 qkvw[QKVW_BYTES / 16];  // next layer's QKV rows [row of this workgroup][K/8], lane-permuted
   float rs;
   int32_t ids[NWAVE][MAX_TOPK];         // routing, one private copy per wave (no workgroup barrier needed)
   float wts[NWAVE][MAX_TOPK];
@@ -467,6 +470,54 @@ __device__ __forceinline__ int token_of(const Params& p) {
   return (t >= 0 && t < p.V) ? t : 0;
 }
 
+// The QKV rows of layer `layer` that this workgroup computes ([b*R, b*R + R), R = p.qkv_rows), HBM -> LDS as
+// stored (lane-permuted), issued from the O projection of the layer before: that stream overlaps the attention,
+// router and expert phases, whose memory traffic leaves room, and the QKV phase then reads its weights from LDS.
+// Wave w copies rows w, w + 8, ...; each wave reads back only the rows it copied, after its own wait.
+template <int KK>
+__device__ __forceinline__ void qkv_to_lds(const Params& p, int layer, Smem& s) {
+  static_assert(KK % 512 == 0, "LDS-staged QKV rows are whole 512-element blocks");
+  const LayerW Lw = layer_w(p, layer);
+  const int rows = (p.NH + 2 * p.NKV) * p.HD, R = p.qkv_rows, r0 = (int)blockIdx.x * R;
+  const int lane = lane_id();
+  for (int i = wave_u(); i < R && r0 + i < rows; i += NWAVE) {
+    const uint16_t* src = Lw.wqkv + (size_t)(r0 + i) * KK + 8 * lane;
+#pragma unroll
+    for (int b = 0; b < KK / 512; ++b)
+      __builtin_amdgcn_global_load_lds((const MK_G void*)(src + 512 * b),
+                                       (__attribute__((address_space(3))) void*)&s.qkvw[i * (KK / 8) + 64 * b], 16, 0, 0);
+  }
+}
+
+// P1 with the weights in LDS (staged by qkv_to_lds one layer ahead): the same norm prologue, the same dot order.
+template <int KK, class Wait>
+__device__ __forceinline__ void phase_qkv_lds(const Params& p, int layer, Smem& s, Wait wait) {
+  const LayerW Lw = layer_w(p, layer);
+  const int rows = (p.NH + 2 * p.NKV) * p.HD, R = p.qkv_rows, r0 = (int)blockIdx.x * R;
+  const int lane = lane_id();
+  float* qkv = p.qkv;
+  if (!wait()) return;
+  build_norm_x<KK>(p, p.x, nullptr, Lw.ln1, s);
+  if (blockIdx.x == 0 && p.dump_x && layer > p.l0)
+    for (int i = threadIdx.x; i < KK; i += NT) st_f(p.dump_x + (size_t)(layer - 1) * KK + i, s.g.xf[i]);
+  __builtin_amdgcn_s_waitcnt(0);                          // this wave's rows have landed in LDS (long since)
+  for (int i = wave_u(); i < R && r0 + i < rows; i += NWAVE) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int b = 0; b < KK / 512; ++b) {
+      const u32x4 w = s.qkvw[i * (KK / 8) + 64 * b + lane];
+      const u32x4 xv = *(const u32x4*)(s.g.xs + 512 * b + lane * 8);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        acc = __builtin_fmaf(bf_lo(w[j]), bf_lo(xv[j]), acc);
+        acc = __builtin_fmaf(bf_hi(w[j]), bf_hi(xv[j]), acc);
+      }
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) st_ag(qkv + r0 + i, bfr(acc));
+  }
+}
+
 // P1: input RMSNorm + fused QKV GEMV (ref_numpy.py:111-115)
 template <int KK, class Wait>
 __device__ __forceinline__ void phase_qkv(const Params& p, int layer, Smem& s, Wait wait) {
@@ -698,8 +749,10 @@ __device__ __forceinline__ void phase_attn(const Params& p, int layer, Smem& s, 
 }
 
 // P3: O projection and residual (ref_numpy.py:130): x = bfr(x + bfr(Wo . o)); the residual is read into LDS in
-// the prologue together with o, so the epilogue does not wait on memory.
-template <int KK, class Wait>
+// the prologue together with o, so the epilogue does not wait on memory.  HQ > 0 (persistent kernel): the next
+// layer's QKV rows of this workgroup start streaming into LDS right behind the O rows; the attention and router
+// phases around it leave the memory system room for them.
+template <int KK, class Wait, int HQ = 0>
 __device__ __forceinline__ void phase_oproj(const Params& p, int layer, Smem& s, Wait wait) {
   const LayerW Lw = layer_w(p, layer);
   const int H = p.H;
@@ -714,6 +767,8 @@ __device__ __forceinline__ void phase_oproj(const Params& p, int layer, Smem& s,
         if (lane_id() == 0) st_ag(x + g, bfr(s.g.xf[g] + bfr(v[0])));
       },
       [&]() {
+        if constexpr (HQ > 0)
+          if (p.qkv_rows > 0 && layer + 1 < p.l1) qkv_to_lds<HQ>(p, layer + 1, s);
         if (!wait()) return false;
         load_vec_perm<KK, 1>(p.o, 1, s.g.xs);
         load_residual(p, first, first ? token_of(p) : 0, s.g.xf);
@@ -1036,13 +1091,14 @@ __device__ __forceinline__ void fused_body(const Params& p) {
   if (p.trace && threadIdx.x == 0) *(MK_G uint64_t*)(p.trace + (size_t)blockIdx.x * 3) = __builtin_amdgcn_s_memrealtime();
   s.phase = 0;
   for (int layer = p.l0; layer < p.l1; ++layer) {
-    phase_qkv<H>(p, layer, s, wait);
+    if (p.qkv_rows > 0 && layer > p.l0) phase_qkv_lds<H>(p, layer, s, wait);
+    else phase_qkv<H>(p, layer, s, wait);
     if (s.abort) return;
     grid_arrive(p, k, s);
     phase_attn(p, layer, s, wait);
     if (s.abort) return;
     grid_arrive(p, k, s);
-    phase_oproj<KA>(p, layer, s, wait);
+    phase_oproj<KA, decltype(wait), (H % 512 == 0 ? H : 0)>(p, layer, s, wait);
     if (s.abort) return;
     grid_arrive(p, k, s);
     if constexpr (MOE) {
