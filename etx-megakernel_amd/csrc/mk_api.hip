@@ -13,7 +13,7 @@
 #include <vector>
 
 #include "etxmk.h"
-#include "mk_device.h"
+#include "mk_batch.h"
 
 using namespace mk;
 
@@ -56,6 +56,22 @@ bool k_in(int k, std::initializer_list<int> ks) {
   return false;
 }
 
+// the batched persistent kernel for this shape with the smallest batch capacity that holds c.batch, or nullptr
+const void* batch_kernel(const etxmk_config& c) {
+  const int km = c.moe ? c.MI : c.I;
+  const void* best = nullptr;
+  int cap = 0;
+#define MK_PICK_B(name, h_, ka_, km_, moe_, e_, b_)                                                             \
+  if (c.H == h_ && c.NH * c.HD == ka_ && km == km_ && (c.moe != 0) == moe_ && (!moe_ || c.E == e_) && c.batch <= b_ && \
+      (!best || b_ < cap)) {                                                                                      \
+    best = (const void*)name;                                                                                     \
+    cap = b_;                                                                                                     \
+  }
+  MK_BATCH_SHAPES(MK_PICK_B)
+#undef MK_PICK_B
+  return best;
+}
+
 int check_config(const etxmk_config* c) {
   if (!c) return fail(ETXMK_EINVAL, "config is NULL");
   if (c->H <= 0 || c->NH <= 0 || c->NKV <= 0 || c->L <= 0 || c->V <= 0) return fail(ETXMK_EINVAL, "non-positive dimension");
@@ -64,7 +80,7 @@ int check_config(const etxmk_config* c) {
   if (c->NH / c->NKV > MAX_G) return fail(ETXMK_EINVAL, "%d q heads per kv head (at most %d)", c->NH / c->NKV, MAX_G);
   if (c->H > MAX_H || !k_in(c->H, {MK_K_HIDDEN})) return fail(ETXMK_EINVAL, "hidden size %d unsupported", c->H);
   if (!k_in(c->NH * c->HD, {MK_K_ATTN})) return fail(ETXMK_EINVAL, "NH*HD %d unsupported", c->NH * c->HD);
-  if (c->batch != 1) return fail(ETXMK_EINVAL, "batch %d unsupported (batch 1 only)", c->batch);
+  if (c->batch < 1 || c->batch > MAX_B) return fail(ETXMK_EINVAL, "batch %d outside 1..%d", c->batch, MAX_B);
   if (c->block_size <= 0 || CHUNK % c->block_size) return fail(ETXMK_EINVAL, "block size %d must divide %d", c->block_size, CHUNK);
   if (c->max_ctx <= 0 || c->max_ctx > MAX_CTX) return fail(ETXMK_EINVAL, "max_ctx %d outside 1..%d", c->max_ctx, MAX_CTX);
   if (c->moe) {
@@ -74,6 +90,9 @@ int check_config(const etxmk_config* c) {
   } else {
     if (!k_in(c->I, {MK_K_INTER}) || c->I > MAX_K) return fail(ETXMK_EINVAL, "intermediate %d unsupported", c->I);
   }
+  if (c->batch > 1 && !batch_kernel(*c))
+    return fail(ETXMK_EINVAL, "no batched persistent kernel for batch %d, H %d, NH*HD %d, %s %d", c->batch, c->H,
+                c->NH * c->HD, c->moe ? "MI" : "I", c->moe ? c->MI : c->I);
   return ETXMK_OK;
 }
 
@@ -109,12 +128,15 @@ std::vector<TensorSlot> weight_layout(const etxmk_config* c, uint64_t* total) {
   return v;
 }
 
-int nblocks_of(const etxmk_config* c) { return (c->max_ctx + c->block_size - 1) / c->block_size; }
+// paged KV: every sequence of the batch owns up to nbps blocks of one shared pool
+int nbps_of(const etxmk_config* c) { return (c->max_ctx + c->block_size - 1) / c->block_size; }
+int nblocks_of(const etxmk_config* c) { return c->batch * nbps_of(c); }
 
 uint64_t kv_layer_elems(const etxmk_config* c) { return (uint64_t)nblocks_of(c) * c->block_size * c->NKV * c->HD; }
 
 struct WsLayout {
-  uint64_t x, qkv, o, logits, hbuf, apart, acnt, amax, bar, abort_w, tokens, out_tokens, btab, rcos, rsin, layers, total;
+  uint64_t x, x16, qkv, o, o16, logits, hbuf, h16, apart, acnt, amax, bar, abort_w, tokens, out_tokens, btab, rcos, rsin,
+      layers, total;
 };
 
 WsLayout ws_layout(const etxmk_config* c) {
@@ -122,19 +144,23 @@ WsLayout ws_layout(const etxmk_config* c) {
   uint64_t off = 0;
   auto take = [&](uint64_t bytes) { const uint64_t o = off; off = align_up(off + bytes); return o; };
   const int NQKV = (c->NH + 2 * c->NKV) * c->HD;
-  w.x = take(4ull * c->H);
-  w.qkv = take(4ull * NQKV);
-  w.o = take(4ull * c->NH * c->HD);
-  w.logits = take(4ull * (c->E > 0 ? c->E : 1));
+  const uint64_t B = (uint64_t)c->batch;
+  w.x = take(4ull * c->H * B);
+  w.x16 = take(2ull * c->H * B);
+  w.qkv = take(4ull * NQKV * B);
+  w.o = take(4ull * c->NH * c->HD * B);
+  w.o16 = take(2ull * c->NH * c->HD * B);
+  w.logits = take(4ull * (c->E > 0 ? c->E : 1) * B);
   const int hb = c->moe ? c->TOPK * c->MI : c->I;
-  w.hbuf = take(4ull * (hb > 0 ? hb : 1));
-  w.apart = take(4ull * c->NH * MAX_CHUNKS * PART);
-  w.acnt = take(4ull * 64 * c->NKV);     // one 256-byte line per kv head
-  w.amax = take(8);
+  w.hbuf = take(4ull * (hb > 0 ? hb : 1) * B);
+  w.h16 = take(2ull * (hb > 0 ? hb : 1) * B);
+  w.apart = take(4ull * c->NH * MAX_CHUNKS * PART * B);
+  w.acnt = take(4ull * 64 * c->NKV * B); // one 256-byte line per (sequence, kv head)
+  w.amax = take(256ull * B);             // one 256-byte line per sequence
   w.bar = take(4 * 64 * 17);          // 8 group counters, 1 global counter, 8 release flags; 256 B apart
   w.abort_w = take(4);
-  w.tokens = take(4ull * (c->max_ctx + 1));
-  w.out_tokens = take(4ull * (c->max_ctx + 1));
+  w.tokens = take(4ull * (c->max_ctx + 1) * B);
+  w.out_tokens = take(4ull * (c->max_ctx + 1) * B);
   w.btab = take(4ull * nblocks_of(c));
   w.rcos = take(4ull * c->max_ctx * (c->HD / 2));
   w.rsin = take(4ull * c->max_ctx * (c->HD / 2));
@@ -267,16 +293,17 @@ int etxmk_bind(etxmk_handle* h, void* weights, void* kv, void* workspace) {
   }
   HIPCHK(hipMemcpy(h->wsp + h->ws.rcos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice));
   HIPCHK(hipMemcpy(h->wsp + h->ws.rsin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice));
-  // identity block table, counters and token buffers cleared
+  // identity block tables (sequence b owns blocks [b*nbps, (b+1)*nbps)), counters and token buffers cleared
   h->btab_host.resize(nblocks_of(&c));
   for (int i = 0; i < (int)h->btab_host.size(); ++i) h->btab_host[i] = i;
   HIPCHK(hipMemcpy(h->wsp + h->ws.btab, h->btab_host.data(), h->btab_host.size() * 4, hipMemcpyHostToDevice));
   HIPCHK(hipMemset(h->wsp + h->ws.bar, 0, 4 * 64 * 17));
   HIPCHK(hipMemset(h->wsp + h->ws.abort_w, 0, 4));
-  HIPCHK(hipMemset(h->wsp + h->ws.tokens, 0, 4ull * (c.max_ctx + 1)));
-  HIPCHK(hipMemset(h->wsp + h->ws.out_tokens, 0, 4ull * (c.max_ctx + 1)));
-  HIPCHK(hipMemset(h->wsp + h->ws.x, 0, 4ull * c.H));
-  HIPCHK(hipMemset(h->wsp + h->ws.acnt, 0, 4ull * 64 * c.NKV));
+  HIPCHK(hipMemset(h->wsp + h->ws.tokens, 0, 4ull * (c.max_ctx + 1) * c.batch));
+  HIPCHK(hipMemset(h->wsp + h->ws.out_tokens, 0, 4ull * (c.max_ctx + 1) * c.batch));
+  HIPCHK(hipMemset(h->wsp + h->ws.x, 0, 4ull * c.H * c.batch));
+  HIPCHK(hipMemset(h->wsp + h->ws.x16, 0, 2ull * c.H * c.batch));
+  HIPCHK(hipMemset(h->wsp + h->ws.acnt, 0, 4ull * 64 * c.NKV * c.batch));
   h->bar_epoch = 0;
   return ETXMK_OK;
 }
@@ -337,11 +364,15 @@ int etxmk_set_block_table(etxmk_handle* h, const int32_t* table, int32_t n, void
   if (!h || !h->wsp) return fail(ETXMK_EUNBOUND, "handle not bound");
   const int nb = nblocks_of(&h->c);
   if (!table || n <= 0 || n > nb) return fail(ETXMK_EINVAL, "block table length %d outside 1..%d", n, nb);
-  std::vector<char> seen(nb, 0);
+  std::vector<int32_t> next(h->btab_host);
   for (int i = 0; i < n; ++i) {
     if (table[i] < 0 || table[i] >= nb) return fail(ETXMK_EINVAL, "block %d maps to %d outside 0..%d", i, table[i], nb - 1);
-    if (seen[table[i]]) return fail(ETXMK_EINVAL, "physical block %d used twice", table[i]);
-    seen[table[i]] = 1;
+    next[i] = table[i];
+  }
+  std::vector<char> seen(nb, 0);                 // no physical block may serve two (sequence, logical block) slots
+  for (int i = 0; i < nb; ++i) {
+    if (seen[next[i]]) return fail(ETXMK_EINVAL, "physical block %d used twice", next[i]);
+    seen[next[i]] = 1;
   }
   for (int i = 0; i < n; ++i) h->btab_host[i] = table[i];
   HIPCHK(hipMemcpyAsync(h->wsp + h->ws.btab, h->btab_host.data(), 4ull * n, hipMemcpyHostToDevice, (hipStream_t)stream));
@@ -349,9 +380,10 @@ int etxmk_set_block_table(etxmk_handle* h, const int32_t* table, int32_t n, void
   return ETXMK_OK;
 }
 
-int etxmk_fill_kv_seeded(etxmk_handle* h, uint64_t seed, int32_t npos, void* stream) {
+int etxmk_fill_kv_seeded_seq(etxmk_handle* h, uint64_t seed, int32_t seq, int32_t npos, void* stream) {
   if (!h || !h->kv) return fail(ETXMK_EUNBOUND, "handle not bound");
   const etxmk_config& c = h->c;
+  if (seq < 0 || seq >= c.batch) return fail(ETXMK_EINVAL, "sequence %d outside 0..%d", seq, c.batch - 1);
   if (npos < 0 || npos > c.max_ctx) return fail(ETXMK_EINVAL, "npos %d outside 0..%d", npos, c.max_ctx);
   if (npos == 0) return ETXMK_OK;
   const uint64_t kvl = kv_layer_elems(&c);
@@ -359,34 +391,51 @@ int etxmk_fill_kv_seeded(etxmk_handle* h, uint64_t seed, int32_t npos, void* str
     uint16_t* kc = (uint16_t*)h->kv + (uint64_t)l * 2 * kvl;
     const size_t n = (size_t)npos * c.NKV * c.HD;
     hipLaunchKernelGGL(etxmk_gen_kv, dim3((unsigned)((n + 255) / 256 < 65536 ? (n + 255) / 256 : 65536)), dim3(256), 0,
-                       (hipStream_t)stream, kc, kc + kvl, h->wsptr<const int32_t>(h->ws.btab),
-                       stream_key(seed, stream_id(10, l, 0)), stream_key(seed, stream_id(11, l, 0)), npos, c.NKV, c.HD,
-                       c.block_size);
+                       (hipStream_t)stream, kc, kc + kvl, h->wsptr<const int32_t>(h->ws.btab) + (size_t)seq * nbps_of(&c),
+                       stream_key(seed, stream_id(10, l, seq)), stream_key(seed, stream_id(11, l, seq)), npos, c.NKV,
+                       c.HD, c.block_size);
     HIPCHK(hipGetLastError());
   }
   return ETXMK_OK;
 }
 
-int etxmk_set_tokens(etxmk_handle* h, const int32_t* tokens, int32_t n, void* stream) {
+int etxmk_fill_kv_seeded(etxmk_handle* h, uint64_t seed, int32_t npos, void* stream) {
+  return etxmk_fill_kv_seeded_seq(h, seed, 0, npos, stream);
+}
+
+int etxmk_set_tokens_seq(etxmk_handle* h, int32_t seq, const int32_t* tokens, int32_t n, void* stream) {
   if (!h || !h->wsp) return fail(ETXMK_EUNBOUND, "handle not bound");
+  if (seq < 0 || seq >= h->c.batch) return fail(ETXMK_EINVAL, "sequence %d outside 0..%d", seq, h->c.batch - 1);
   if (!tokens || n < 0 || n > h->c.max_ctx + 1) return fail(ETXMK_EINVAL, "token count %d outside 0..%d", n, h->c.max_ctx + 1);
   for (int i = 0; i < n; ++i)
     if (tokens[i] < 0 || tokens[i] >= h->c.V) return fail(ETXMK_EINVAL, "token %d = %d outside 0..%d", i, tokens[i], h->c.V - 1);
-  HIPCHK(hipMemcpyAsync(h->wsp + h->ws.tokens, tokens, 4ull * n, hipMemcpyHostToDevice, (hipStream_t)stream));
+  HIPCHK(hipMemcpyAsync(h->wsp + h->ws.tokens + 4ull * (h->c.max_ctx + 1) * seq, tokens, 4ull * n, hipMemcpyHostToDevice,
+                        (hipStream_t)stream));
+  HIPCHK(hipStreamSynchronize((hipStream_t)stream));
+  return ETXMK_OK;
+}
+
+int etxmk_set_tokens(etxmk_handle* h, const int32_t* tokens, int32_t n, void* stream) {
+  return etxmk_set_tokens_seq(h, 0, tokens, n, stream);
+}
+
+int etxmk_read_tokens_seq(etxmk_handle* h, int32_t seq, int32_t* out, int32_t n, void* stream) {
+  if (!h || !h->wsp) return fail(ETXMK_EUNBOUND, "handle not bound");
+  if (seq < 0 || seq >= h->c.batch) return fail(ETXMK_EINVAL, "sequence %d outside 0..%d", seq, h->c.batch - 1);
+  if (!out || n < 0 || n > h->c.max_ctx + 1) return fail(ETXMK_EINVAL, "token count %d outside 0..%d", n, h->c.max_ctx + 1);
+  HIPCHK(hipMemcpyAsync(out, h->wsp + h->ws.out_tokens + 4ull * (h->c.max_ctx + 1) * seq, 4ull * n, hipMemcpyDeviceToHost,
+                        (hipStream_t)stream));
   HIPCHK(hipStreamSynchronize((hipStream_t)stream));
   return ETXMK_OK;
 }
 
 int etxmk_read_tokens(etxmk_handle* h, int32_t* out, int32_t n, void* stream) {
-  if (!h || !h->wsp) return fail(ETXMK_EUNBOUND, "handle not bound");
-  if (!out || n < 0 || n > h->c.max_ctx + 1) return fail(ETXMK_EINVAL, "token count %d outside 0..%d", n, h->c.max_ctx + 1);
-  HIPCHK(hipMemcpyAsync(out, h->wsp + h->ws.out_tokens, 4ull * n, hipMemcpyDeviceToHost, (hipStream_t)stream));
-  HIPCHK(hipStreamSynchronize((hipStream_t)stream));
-  return ETXMK_OK;
+  return etxmk_read_tokens_seq(h, 0, out, n, stream);
 }
 
 int etxmk_set_residual(etxmk_handle* h, const float* x, void* stream) {
   if (!h || !h->wsp) return fail(ETXMK_EUNBOUND, "handle not bound");
+  if (h->c.batch != 1) return fail(ETXMK_EINVAL, "the residual entry points serve single-sequence handles");
   if (!x) return fail(ETXMK_EINVAL, "x is NULL");
   HIPCHK(hipMemcpyAsync(h->wsp + h->ws.x, x, 4ull * h->c.H, hipMemcpyHostToDevice, (hipStream_t)stream));
   HIPCHK(hipStreamSynchronize((hipStream_t)stream));
@@ -395,6 +444,7 @@ int etxmk_set_residual(etxmk_handle* h, const float* x, void* stream) {
 
 int etxmk_read_residual(etxmk_handle* h, float* x, void* stream) {
   if (!h || !h->wsp) return fail(ETXMK_EUNBOUND, "handle not bound");
+  if (h->c.batch != 1) return fail(ETXMK_EINVAL, "the residual entry points serve single-sequence handles");
   if (!x) return fail(ETXMK_EINVAL, "x is NULL");
   HIPCHK(hipMemcpyAsync(x, h->wsp + h->ws.x, 4ull * h->c.H, hipMemcpyDeviceToHost, (hipStream_t)stream));
   HIPCHK(hipStreamSynchronize((hipStream_t)stream));
@@ -453,13 +503,28 @@ static const void* fused_kernel(const etxmk_config& c) {
   return nullptr;
 }
 
-static int launch(etxmk_handle* h, int pos, int write_next, int l0, int l1, int embed, int head, hipStream_t st) {
+// One step: single-sequence handles take `pos`; batched handles take one position per sequence (posv[batch]).
+static int launch(etxmk_handle* h, const int32_t* posv, int pos, int write_next, int l0, int l1, int embed, int head,
+                  hipStream_t st) {
   if (!h || !h->wsp) return fail(ETXMK_EUNBOUND, "handle not bound");
   const etxmk_config& c = h->c;
-  if (pos < 0 || pos >= c.max_ctx) return fail(ETXMK_EINVAL, "position %d outside 0..%d", pos, c.max_ctx - 1);
+  const bool batched = c.batch > 1;
+  if (batched && !posv) return fail(ETXMK_EINVAL, "a batched handle steps through etxmk_step_batch");
+  if (!batched && posv) pos = posv[0];
+  for (int b = 0; b < (batched ? c.batch : 1); ++b) {
+    const int q = batched ? posv[b] : pos;
+    if (q < 0 || q >= c.max_ctx) return fail(ETXMK_EINVAL, "sequence %d position %d outside 0..%d", b, q, c.max_ctx - 1);
+  }
   if (l0 < 0 || l1 > c.L || l0 >= l1) return fail(ETXMK_EINVAL, "layer range [%d, %d) outside [0, %d)", l0, l1, c.L);
   const int need = 8;                       // the grid barrier spreads arrivals over 8 groups
   if (h->nwg < need) return fail(ETXMK_EINVAL, "grid of %d workgroups is below the %d the grid barrier needs", h->nwg, need);
+  if (batched) {
+    if (!h->fused) return fail(ETXMK_EINVAL, "batched handles run the persistent kernel only");
+    if (!embed || !head) return fail(ETXMK_EINVAL, "batched handles run whole steps");
+    if ((int64_t)h->nwg * NWAVE * (RES_ROWS / NWAVE) < c.H)
+      return fail(ETXMK_EINVAL, "grid of %d workgroups too small for H %d at batch > 1 (at least %d)", h->nwg, c.H,
+                  (c.H + RES_ROWS - 1) / RES_ROWS);
+  }
   Params p{};
   p.H = c.H; p.NH = c.NH; p.NKV = c.NKV; p.HD = c.HD; p.I = c.I; p.E = c.E; p.TOPK = c.TOPK; p.MI = c.MI; p.L = c.L; p.V = c.V;
   p.moe = c.moe; p.qk_norm = c.qk_norm; p.norm_topk = c.norm_topk; p.BS = c.block_size; p.max_ctx = c.max_ctx;
@@ -487,15 +552,26 @@ static int launch(etxmk_handle* h, int pos, int write_next, int l0, int l1, int 
   p.out_tokens = h->wsptr<int32_t>(h->ws.out_tokens);
   p.dump_x = h->dump_x; p.dump_ids = h->dump_ids; p.dump_wts = h->dump_wts; p.dump_logits = h->dump_logits;
   p.trace = h->fused ? h->trace : nullptr;
-  p.pos = pos; p.write_next = write_next; p.l0 = l0; p.l1 = l1; p.do_embed = embed; p.do_head = head;
+  p.pos = batched ? 0 : pos; p.write_next = write_next; p.l0 = l0; p.l1 = l1; p.do_embed = embed; p.do_head = head;
   p.nwg = h->nwg;
   p.spin_ticks = 200000000ull;            // 2 s of the 100 MHz s_memrealtime clock
   {                                        // QKV rows staged in LDS a layer ahead when a workgroup's share fits
     const int rows = (c.NH + 2 * c.NKV) * c.HD, R = (rows + h->nwg - 1) / h->nwg;
-    p.qkv_rows = (h->fused && c.H % 512 == 0 && (uint64_t)R * c.H * 2 <= (uint64_t)QKVW_BYTES) ? R : 0;
+    p.qkv_rows = (!batched && h->fused && c.H % 512 == 0 && (uint64_t)R * c.H * 2 <= (uint64_t)QKVW_BYTES) ? R : 0;
+  }
+  p.B = c.batch;
+  p.nbps = nbps_of(&c);
+  p.tok_stride = c.max_ctx + 1;
+  p.x16 = h->wsptr<uint16_t>(h->ws.x16);
+  p.o16 = h->wsptr<uint16_t>(h->ws.o16);
+  p.h16 = h->wsptr<uint16_t>(h->ws.h16);
+  p.ibase[0] = 0;
+  for (int b = 0; b < c.batch; ++b) {       // attention items: NKV per 64-position chunk of each sequence
+    p.posb[b] = batched ? posv[b] : pos;
+    p.ibase[b + 1] = p.ibase[b] + c.NKV * (p.posb[b] / CHUNK + 1);
   }
   if (h->fused) {
-    const void* fn = fused_kernel(c);
+    const void* fn = batched ? batch_kernel(c) : fused_kernel(c);
     if (!fn) return fail(ETXMK_EINVAL, "no persistent kernel for H %d, NH*HD %d, %s %d (use the unfused mode)", c.H,
                          c.NH * c.HD, c.moe ? "MI" : "I", c.moe ? c.MI : c.I);
     p.bar_base = h->bar_epoch;
@@ -535,12 +611,19 @@ static int launch(etxmk_handle* h, int pos, int write_next, int l0, int l1, int 
 
 int etxmk_step(etxmk_handle* h, int32_t pos, int32_t write_next, void* stream) {
   if (!h) return fail(ETXMK_EINVAL, "NULL handle");
-  return launch(h, pos, write_next, 0, h->c.L, 1, 1, (hipStream_t)stream);
+  return launch(h, nullptr, pos, write_next, 0, h->c.L, 1, 1, (hipStream_t)stream);
+}
+
+int etxmk_step_batch(etxmk_handle* h, const int32_t* positions, int32_t write_next_mask, void* stream) {
+  if (!h) return fail(ETXMK_EINVAL, "NULL handle");
+  if (!positions) return fail(ETXMK_EINVAL, "positions is NULL");
+  return launch(h, positions, 0, write_next_mask, 0, h->c.L, 1, 1, (hipStream_t)stream);
 }
 
 int etxmk_step_layers(etxmk_handle* h, int32_t pos, int32_t l0, int32_t l1, void* stream) {
   if (!h) return fail(ETXMK_EINVAL, "NULL handle");
-  return launch(h, pos, 0, l0, l1, 0, 0, (hipStream_t)stream);
+  if (h->c.batch != 1) return fail(ETXMK_EINVAL, "layer-range steps serve single-sequence handles");
+  return launch(h, nullptr, pos, 0, l0, l1, 0, 0, (hipStream_t)stream);
 }
 
 int etxmk_sync(etxmk_handle* h, void* stream) {
@@ -551,7 +634,7 @@ int etxmk_sync(etxmk_handle* h, void* stream) {
   if (ab) {
     HIPCHK(hipMemset(h->wsp + h->ws.abort_w, 0, 4));
     HIPCHK(hipMemset(h->wsp + h->ws.bar, 0, 4 * 64 * 17));
-    HIPCHK(hipMemset(h->wsp + h->ws.acnt, 0, 4ull * 64 * h->c.NKV));
+    HIPCHK(hipMemset(h->wsp + h->ws.acnt, 0, 4ull * 64 * h->c.NKV * h->c.batch));
     h->bar_epoch = 0;
     return fail(ETXMK_ABORTED, "device abort word %d (%s)", ab,
                 ab == 2 ? "a grid barrier wait exceeded its limit" : ab == 3 ? "no finite logit in the head" : "host abort");

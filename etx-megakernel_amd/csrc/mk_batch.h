@@ -1,0 +1,645 @@
+#pragma once
+// Batched decode step: B sequences (at most MAX_B) per persistent launch, each at its own position with its own
+// paged-KV block table and token row.  The phases are those of the single-sequence kernel (mk_device.h); every
+// weight row streams from HBM once per step and is dotted with the input vectors of every sequence that needs it.
+// Per (row, sequence) the arithmetic is the single-sequence dot in the same order, so a batched step equals B
+// single-sequence steps bit for bit.
+//
+// Reference path: examples/vllm_llm/host.hip:126-1159 and examples/vllm_llm/vl_tiles.hip:1-95 (per-request
+// parameters, block tables, slot mapping, greedy argmax), with examples/llm/ref_numpy.py:105-158 per sequence.
+//
+// Activations between phases (global memory, one row per sequence):
+//   x16     [B][H] bf16       residual (its values are bf16 in every case, so storing them as bf16 rounds nothing)
+//   qkv     [B][NQKV] fp32    as in the single-sequence kernel
+//   o16     [B][NH*HD] bf16   attention output, lane-permuted: the O projection copies rows straight into LDS
+//   logits  [B][E] fp32       router logits
+//   h16     MoE [pairs][MI] / dense [B][I] bf16, lane-permuted; MoE rows are the routed (sequence, slot) pairs in
+//           pair order (ascending expert, then sequence)
+// Cross-workgroup values are written with agent-scope stores and read with agent-scope loads (sc1), as in the
+// single-sequence kernel.
+#include "mk_device.h"
+
+namespace mk {
+
+constexpr int RES_ROWS = 64;            // residual rows per workgroup and sequence held for the epilogues
+constexpr int MAX_PAIRS = MAX_B * MAX_TOPK;
+
+template <int B>
+struct SmemB {
+  static constexpr int NCAP = B * MAX_H > 32768 ? 32768 : B * MAX_H;    // B * H of the norm phases
+  static constexpr int XCAP = B * MAX_K > 65536 ? 65536 : B * MAX_K;    // input rows of the other GEMVs
+  union {
+    struct {
+      alignas(16) uint16_t xr[NCAP];    // residual rows, natural order
+      alignas(16) uint16_t xs[NCAP];    // normed rows, lane-permuted
+    } n;
+    struct {
+      alignas(16) uint16_t xs[XCAP];    // input rows (o, h), lane-permuted
+      float xres[B][RES_ROWS];          // residual of this workgroup's output rows
+      float acc[B][RES_ROWS];           // expert combine carried from one pass over the pairs to the next
+    } v;
+    AttnTiles a;
+  };
+  float rs[B];                          // 1/rms per sequence
+  int32_t rids[B][MAX_TOPK];            // routing per sequence, slot order
+  float rwts[B][MAX_TOPK];
+  int32_t pexp[MAX_PAIRS];              // routed pairs sorted by (expert, sequence): expert, sequence, weight
+  int32_t pseq[MAX_PAIRS];
+  float pw[MAX_PAIRS];
+  int32_t uexp[MAX_PAIRS];              // distinct experts ascending; expert u owns pairs [ustart[u], ustart[u + 1])
+  int32_t ustart[MAX_PAIRS + 1];
+  int32_t nexp;
+  int32_t abort, last, phase;
+};
+
+__device__ __forceinline__ int token_of_b(const Params& p, int b) {
+  const int t = ld_ag_i(p.tokens + (size_t)b * p.tok_stride + p.posb[b]);
+  return (t >= 0 && t < p.V) ? t : 0;
+}
+
+// nelem bf16 (global, contiguous, a multiple of 8) -> dst (LDS), 16 bytes per lane, agent-coherent.  Lane l of a
+// wave writes the 16 bytes after its wave's base, so each wave copies 64 consecutive chunks per round.
+__device__ __forceinline__ void copy_rows_lds(const uint16_t* src, int nelem, uint16_t* dst) {
+  const int lane = lane_id(), nch = nelem / 8;
+  for (int c0 = wave_u() * 64; c0 < nch; c0 += NT)
+    if (c0 + lane < nch)
+      __builtin_amdgcn_global_load_lds((const MK_G void*)(src + 8 * (c0 + lane)),
+                                       (__attribute__((address_space(3))) void*)(dst + 8 * c0), 16, 0, LDS_SC1);
+}
+
+// The residual rows -> s.n.xr (bf16, natural order): the embedding rows of the sequences' tokens for the first
+// layer, else x16.  Then per sequence r = 1/sqrt(mean(x^2) + eps) with the sum of squares in dot order, and the
+// normed lane-permuted rows bfr(w * bfr(x * r)) -> s.n.xs (ref_numpy.py:71-73, as build_norm_x).
+template <int H, int B, class S>
+__device__ __forceinline__ void build_norm_xb(const Params& p, bool first, const uint16_t* w, S& s) {
+  static_assert(B * H <= S::NCAP, "residual rows exceed the LDS budget");
+  constexpr int C8 = H / 8, QPER = (C8 + NT - 1) / NT;
+  const int nb = p.B, lane = lane_id(), wave = wave_u();
+  uint16_t wv[QPER][8];
+#pragma unroll
+  for (int j = 0; j < QPER; ++j) {
+    const int q = threadIdx.x + j * NT;
+    if (q < C8)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) wv[j][e] = ld_u16(w + perm_logical(8 * q + e, H));
+  }
+  if (first) {
+    for (int c = threadIdx.x; c < nb * C8; c += NT) {
+      const int b = c / C8, q = c - b * C8;
+      *(u32x4*)(s.n.xr + 8 * c) = ld16(p.embed + (size_t)token_of_b(p, b) * H + 8 * q);
+    }
+  } else {
+    copy_rows_lds(p.x16, nb * H, s.n.xr);
+    __builtin_amdgcn_s_waitcnt(0);
+  }
+  __syncthreads();
+  for (int b = wave; b < nb; b += NWAVE) {
+    float acc = 0.0f;
+#pragma unroll 8
+    for (int k = lane; k < H; k += 64) {
+      const float v = bf2f(s.n.xr[b * H + k]);
+      acc = __builtin_fmaf(v, v, acc);
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) s.rs[b] = 1.0f / __builtin_sqrtf(acc / (float)H + p.eps);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < QPER; ++j) {
+    const int q = threadIdx.x + j * NT;
+    if (q < C8)
+      for (int b = 0; b < nb; ++b) {
+        const float r = s.rs[b];
+        uint32_t o[4];
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+          const int k0 = perm_logical(8 * q + e, H), k1 = perm_logical(8 * q + e + 1, H);
+          const uint32_t b0 = f2bf(bfr(bf2f(wv[j][e]) * bfr(bf2f(s.n.xr[b * H + k0]) * r)));
+          const uint32_t b1 = f2bf(bfr(bf2f(wv[j][e + 1]) * bfr(bf2f(s.n.xr[b * H + k1]) * r)));
+          o[e / 2] = b0 | (b1 << 16);
+        }
+        *(u32x4*)(s.n.xs + b * H + 8 * q) = u32x4{o[0], o[1], o[2], o[3]};
+      }
+  }
+  __syncthreads();
+}
+
+// Residual entries of this workgroup's output rows for the NR = 1 phases (O projection, down projections): row
+// g = d*nw + 8*blockIdx.x + i is wave i's row of round d and lands in xres[b][8*d + i].  Read before the phase's
+// wait: the residual was last written at least two barriers earlier.
+template <int B, class S>
+__device__ __forceinline__ void load_res_rows(const Params& p, int nrows, bool first, S& s) {
+  const int nw = p.nwg * NWAVE, per = ((nrows + nw - 1) / nw) * NWAVE;
+  for (int t = threadIdx.x; t < p.B * per; t += NT) {
+    const int b = t / per, r = t - b * per;
+    const int g = (r / NWAVE) * nw + (int)blockIdx.x * NWAVE + r % NWAVE;
+    if (g < nrows)
+      s.v.xres[b][r] = first ? bf2f(ld_u16(p.embed + (size_t)token_of_b(p, b) * p.H + g))
+                             : bf2f(ld_ag_u16(p.x16 + (size_t)b * p.H + g));
+  }
+}
+// the xres slot of row g for the calling wave
+__device__ __forceinline__ int res_slot(int g, int nw) { return (g / nw) * NWAVE + wave_u(); }
+
+// NR rows (in registers) dotted with up to B input rows in LDS (xp(b), b < nv; nv is wave-uniform).  For each
+// (row, input) the lane accumulates its elements in ascending order exactly as dot_row does, then wave_sum.
+template <int K, int NR, int B, class XP>
+__device__ __forceinline__ void dot_rows_b(const RowRegs<K> (&r)[NR], XP xp, int nv, int lane, float (&v)[NR][B]) {
+  float acc[NR][B];
+#pragma unroll
+  for (int i = 0; i < NR; ++i)
+#pragma unroll
+    for (int b = 0; b < B; ++b) acc[i][b] = 0.0f;
+#pragma unroll
+  for (int blk = 0; blk < KS<K>::KB; ++blk) {
+#pragma unroll
+    for (int b = 0; b < B; ++b)
+      if (b < nv) {
+        const u32x4 xv = *(const u32x4*)(xp(b) + 512 * blk + lane * 8);
+#pragma unroll
+        for (int i = 0; i < NR; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            acc[i][b] = __builtin_fmaf(bf_lo(r[i].w[blk][j]), bf_lo(xv[j]), acc[i][b]);
+            acc[i][b] = __builtin_fmaf(bf_hi(r[i].w[blk][j]), bf_hi(xv[j]), acc[i][b]);
+          }
+      }
+  }
+#pragma unroll
+  for (int t = 0; t < KS<K>::TW; ++t) {
+#pragma unroll
+    for (int b = 0; b < B; ++b)
+      if (b < nv) {
+        const uint32_t xv = *(const uint32_t*)(xp(b) + 512 * KS<K>::KB + lane * KS<K>::TM + 2 * t);
+#pragma unroll
+        for (int i = 0; i < NR; ++i) {
+          acc[i][b] = __builtin_fmaf(bf_lo(r[i].t[t]), bf_lo(xv), acc[i][b]);
+          acc[i][b] = __builtin_fmaf(bf_hi(r[i].t[t]), bf_hi(xv), acc[i][b]);
+        }
+      }
+  }
+#pragma unroll
+  for (int i = 0; i < NR; ++i)
+#pragma unroll
+    for (int b = 0; b < B; ++b) v[i][b] = b < nv ? wave_sum(acc[i][b]) : 0.0f;
+}
+
+// gemv_run with B input rows per group: groups of NR rows dealt round-robin to the grid's waves; two register
+// buffers alternate, so one group's weights stream while the other group is reduced (a batched group carries
+// B x NR dots, which covers the latency of the next group's loads).  The first group is issued before `prologue`
+// (which waits for the inputs).  nvec(g) is the number of input rows of group g, xvec(g, b) the LDS address of
+// its b-th; epi(g, nv, v) consumes v[NR][B].
+template <int K, int NR, int B, class RowF, class NVF, class XF, class EpiF, class Pro>
+__device__ __forceinline__ bool gemv_run_b(int ngroups, RowF rowf, NVF nvec, XF xvec, EpiF epi, Pro prologue, int nwg,
+                                           uint64_t* trace, int s_phase) {
+  static_assert(KS<K>::KB <= 16, "batched GEMV rows are at most 8192 long");
+  const int lane = lane_id();
+  const int gw = blockIdx.x * NWAVE + wave_u(), nw = nwg * NWAVE;
+  RowRegs<K> RA[NR], RB[NR];
+  auto issue = [&](RowRegs<K>(&R)[NR], int g) {
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+      const uint16_t* rp = rowf(g, i);
+      if (rp) load_row<K>(R[i], rp, lane);
+    }
+  };
+  auto compute = [&](const RowRegs<K>(&R)[NR], int g) {
+    const int nv = nvec(g);
+    float v[NR][B];
+    dot_rows_b<K, NR, B>(R, [&](int b) { return xvec(g, b); }, nv, lane, v);
+    epi(g, nv, v);
+  };
+  int g = gw;
+  if (g < ngroups) issue(RA, g);
+  if (trace && threadIdx.x == 0)
+    *(MK_G uint64_t*)(trace + ((size_t)s_phase * nwg + blockIdx.x) * 3 + 2) = __builtin_amdgcn_s_memrealtime();
+  if (!prologue()) return false;
+  while (g < ngroups) {
+    const int g1 = g + nw;
+    if (g1 < ngroups) issue(RB, g1);
+    compute(RA, g);
+    if (g1 >= ngroups) break;
+    const int g2 = g1 + nw;
+    if (g2 < ngroups) issue(RA, g2);
+    compute(RB, g1);
+    g = g2;
+  }
+  return true;
+}
+
+// store NR x B values: lane i*B + b stores (i, b) for b < nv
+template <int NR, int B, class F>
+__device__ __forceinline__ void lane_store_b(const float (&v)[NR][B], int nv, F f) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int i = 0; i < NR; ++i)
+#pragma unroll
+    for (int b = 0; b < B; ++b)
+      if (lane == i * B + b && b < nv) f(i, b, v[i][b]);
+}
+
+// ---------------------------------------------------------------- phases (batched)
+// P1: input RMSNorm + QKV GEMV per sequence (ref_numpy.py:111-115)
+template <int KK, int B, class S, class Wait>
+__device__ __forceinline__ void phase_qkv_b(const Params& p, int layer, S& s, Wait wait) {
+  const LayerW Lw = layer_w(p, layer);
+  const bool first = layer == p.l0 && p.do_embed;
+  const int rows = (p.NH + 2 * p.NKV) * p.HD, nb = p.B;
+  const uint16_t* W = Lw.wqkv;
+  gemv_run_b<KK, 2, B>(
+      (rows + 1) / 2,
+      [&](int g, int i) -> const uint16_t* { const int r = 2 * g + i; return r < rows ? W + (size_t)r * KK : nullptr; },
+      [&](int) { return nb; }, [&](int, int b) { return (const uint16_t*)(s.n.xs + b * KK); },
+      [&](int g, int nv, const float(&v)[2][B]) {
+        lane_store_b<2, B>(v, nv, [&](int i, int b, float val) {
+          const int r = 2 * g + i;
+          if (r < rows) st_ag(p.qkv + (size_t)b * rows + r, bfr(val));
+        });
+      },
+      [&]() {
+        if (!wait()) return false;
+        build_norm_xb<KK, B>(p, first, Lw.ln1, s);
+        if (blockIdx.x == 0) {
+          if (p.dump_x && layer > p.l0)
+            for (int i = threadIdx.x; i < nb * KK; i += NT)
+              st_f(p.dump_x + (size_t)(layer - 1) * nb * KK + i, bf2f(s.n.xr[i]));
+          if (layer == p.l0 && p.do_head && (int)threadIdx.x < nb)
+            __hip_atomic_store(p.amax + 32 * threadIdx.x, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        return true;
+      },
+      p.nwg, p.trace, s.phase);
+}
+
+// P3: O projection + residual per sequence (ref_numpy.py:130)
+template <int KK, int B, class S, class Wait>
+__device__ __forceinline__ void phase_oproj_b(const Params& p, int layer, S& s, Wait wait) {
+  static_assert(B * KK <= S::XCAP, "attention rows exceed the LDS budget");
+  const LayerW Lw = layer_w(p, layer);
+  const int H = p.H, nb = p.B, nw = p.nwg * NWAVE;
+  const bool first = layer == p.l0 && p.do_embed;
+  const uint16_t* W = Lw.wo;
+  gemv_run_b<KK, 1, B>(
+      H, [&](int g, int) -> const uint16_t* { return W + (size_t)g * KK; }, [&](int) { return nb; },
+      [&](int, int b) { return (const uint16_t*)(s.v.xs + b * KK); },
+      [&](int g, int nv, const float(&v)[1][B]) {
+        const int r = res_slot(g, nw);
+        lane_store_b<1, B>(v, nv, [&](int, int b, float val) {
+          st_ag_u16(p.x16 + (size_t)b * H + g, f2bf(s.v.xres[b][r] + bfr(val)));
+        });
+      },
+      [&]() {
+        load_res_rows<B>(p, H, first, s);
+        if (!wait()) return false;
+        copy_rows_lds(p.o16, nb * KK, s.v.xs);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        return true;
+      },
+      p.nwg, p.trace, s.phase);
+}
+
+// P4: post-attention RMSNorm + router GEMV per sequence (ref_numpy.py:131-134)
+template <int KK, int B, class S, class Wait>
+__device__ __forceinline__ void phase_router_b(const Params& p, int layer, S& s, Wait wait) {
+  const LayerW Lw = layer_w(p, layer);
+  const int E = p.E, nb = p.B;
+  const uint16_t* W = Lw.wr;
+  gemv_run_b<KK, 1, B>(
+      E, [&](int g, int) -> const uint16_t* { return W + (size_t)g * KK; }, [&](int) { return nb; },
+      [&](int, int b) { return (const uint16_t*)(s.n.xs + b * KK); },
+      [&](int g, int nv, const float(&v)[1][B]) {
+        lane_store_b<1, B>(v, nv, [&](int, int b, float val) { st_ag(p.logits + (size_t)b * E + g, bfr(val)); });
+      },
+      [&]() {
+        if (!wait()) return false;
+        build_norm_xb<KK, B>(p, false, Lw.ln2, s);
+        return true;
+      },
+      p.nwg, p.trace, s.phase);
+}
+
+// Top-k of every sequence (route_topk_into: wave w routes sequences w, w + 8), then the routed (sequence, slot)
+// pairs sorted by (expert, sequence) and the distinct experts in ascending order.  Every workgroup computes the
+// same lists from the same logits.
+template <int B, int EC, class S>
+__device__ __forceinline__ void route_all(const Params& p, S& s) {
+  const int nb = p.B, K = p.TOPK, np = nb * K, lane = lane_id(), wave = wave_u();
+  for (int b = wave; b < nb; b += NWAVE)
+    route_topk_into<EC>(p, p.logits + (size_t)b * p.E, &s.rids[b][0], &s.rwts[b][0], nullptr);
+  __syncthreads();
+  if ((int)threadIdx.x < np) {                             // rank of each pair among all pairs (keys are distinct)
+    const int b = threadIdx.x / K, k = threadIdx.x - b * K;
+    const int key = s.rids[b][k] * MAX_B + b;
+    int rank = 0;
+    for (int t = 0; t < np; ++t) {
+      const int bt = t / K;
+      rank += (s.rids[bt][t - bt * K] * MAX_B + bt) < key;
+    }
+    s.pexp[rank] = s.rids[b][k];
+    s.pseq[rank] = b;
+    s.pw[rank] = s.rwts[b][k];
+  }
+  __syncthreads();
+  if (wave == 0) {                                         // first pair of each expert -> ustart
+    int carry = 0;
+    for (int c0 = 0; c0 < np; c0 += 64) {
+      const int t = c0 + lane;
+      const bool head = t < np && (t == 0 || s.pexp[t] != s.pexp[t - 1]);
+      const uint64_t m = __ballot(head);
+      if (head) {
+        const int u = carry + __builtin_popcountll(m & ((1ull << lane) - 1ull));
+        s.uexp[u] = s.pexp[t];
+        s.ustart[u] = t;
+      }
+      carry += __builtin_popcountll(m);
+    }
+    if (lane == 0) {
+      s.nexp = carry;
+      s.ustart[carry] = np;
+    }
+  }
+  __syncthreads();
+}
+
+// P5: routing, then each distinct expert's gate/up rows against the normed rows of the sequences routed to it,
+// SiLU*up into that pair's h16 row (ref_numpy.py:135-145)
+template <int KK, int B, int EC, class S, class Wait>
+__device__ __forceinline__ void phase_expert_up_b(const Params& p, int layer, S& s, Wait wait) {
+  const LayerW Lw = layer_w(p, layer);
+  const int MI = p.MI, KT = p.TOPK, nb = p.B;
+  const uint16_t* W = Lw.w13;
+  build_norm_xb<KK, B>(p, false, Lw.ln2, s);              // x is final since the O projection
+  if (!wait()) return;
+  route_all<B, EC>(p, s);
+  if (blockIdx.x == 0) {
+    for (int t = threadIdx.x; t < nb * KT; t += NT) {
+      const int b = t / KT, k = t - b * KT;
+      if (p.dump_ids) st_i(p.dump_ids + ((size_t)layer * nb + b) * KT + k, s.rids[b][k]);
+      if (p.dump_wts) st_f(p.dump_wts + ((size_t)layer * nb + b) * KT + k, s.rwts[b][k]);
+    }
+    if (p.dump_logits)
+      for (int t = threadIdx.x; t < nb * p.E; t += NT) st_f(p.dump_logits + (size_t)layer * nb * p.E + t, ld_ag(p.logits + t));
+  }
+  const int U = s.nexp;
+  gemv_run_b<KK, 2, B>(
+      U * MI,
+      [&](int g, int i) -> const uint16_t* {
+        const int u = g / MI, j = g - u * MI;
+        return W + ((size_t)s.uexp[u] * 2 * MI + 2 * j + i) * KK;
+      },
+      [&](int g) { const int u = g / MI; return s.ustart[u + 1] - s.ustart[u]; },
+      [&](int g, int b) { return (const uint16_t*)(s.n.xs + s.pseq[s.ustart[g / MI] + b] * KK); },
+      [&](int g, int nv, const float(&v)[2][B]) {
+        const int u = g / MI, j = g - u * MI, lane = lane_id();
+#pragma unroll
+        for (int b = 0; b < B; ++b)
+          if (lane == b && b < nv)
+            st_ag_u16(p.h16 + (size_t)(s.ustart[u] + b) * MI + perm_stored(j, MI),
+                      f2bf(bfr(bfr(silu(bfr(v[0][b]))) * bfr(v[1][b]))));
+      },
+      [&]() { return true; }, p.nwg, p.trace, s.phase);
+}
+
+// P6: expert down, routing weight, combine per sequence in ascending expert id, residual (ref_numpy.py:146-148).
+// Each wave owns output rows; for its row it streams the rows of every distinct expert (D at a time, the next
+// batch in flight while the current one is reduced) and dots each with the h rows of that expert's pairs.  The
+// pairs' h rows are staged in LDS in passes of whole experts that fit; lane b carries sequence b's combine chain.
+template <int KK, int B, class S, class Wait>
+__device__ __forceinline__ void phase_expert_down_b(const Params& p, int layer, S& s, Wait wait) {
+  constexpr int PCAP = S::XCAP / KK;                      // pairs per pass
+  static_assert(PCAP >= MAX_B, "one expert's pairs must fit a pass");
+  constexpr int DE = KS<KK>::REGS <= 6 ? 8 : KS<KK>::REGS <= 12 ? 4 : 2;
+  const LayerW Lw = layer_w(p, layer);
+  const int H = p.H, nb = p.B, nw = p.nwg * NWAVE, lane = lane_id();
+  const int gw = blockIdx.x * NWAVE + wave_u();
+  const int U = s.nexp;                                   // routing kept from P5
+  const uint16_t* W = Lw.w2;
+  const int nrw = gw < H ? (H - 1 - gw) / nw + 1 : 0;    // output rows of this wave
+  RowRegs<KK> R[2][DE];
+  auto issue = [&](RowRegs<KK>(&Rb)[DE], int g, int ub, int u1) {
+#pragma unroll
+    for (int d = 0; d < DE; ++d)
+      if (ub + d < u1) load_row<KK>(Rb[d], W + ((size_t)s.uexp[ub + d] * H + g) * KK, lane);
+  };
+  int u0 = 0, u1 = 0;
+  auto pass_end = [&](int a) {
+    int e = a + 1;
+    while (e < U && s.ustart[e + 1] - s.ustart[a] <= PCAP) ++e;
+    return e;
+  };
+  u1 = U > 0 ? pass_end(0) : 0;
+  if (nrw > 0 && U > 0) issue(R[0], gw, 0, u1);           // the first batch streams during the wait
+  if (p.trace && threadIdx.x == 0)
+    *(MK_G uint64_t*)(p.trace + ((size_t)s.phase * p.nwg + blockIdx.x) * 3 + 2) = __builtin_amdgcn_s_memrealtime();
+  load_res_rows<B>(p, H, false, s);
+  if (!wait()) return;
+  bool first_pass = true;
+  while (u0 < U) {
+    const int p0 = s.ustart[u0];
+    const int nbt = (u1 - u0 + DE - 1) / DE, T = nrw * nbt;
+    __syncthreads();                                      // the previous pass is done with s.v.xs
+    copy_rows_lds(p.h16 + (size_t)p0 * KK, (s.ustart[u1] - p0) * KK, s.v.xs);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    const bool last_pass = u1 >= U;
+    float acc = 0.0f;
+    auto compute = [&](RowRegs<KK>(&Rb)[DE], int t) {
+      const int g = gw + (t / nbt) * nw, ub = u0 + (t % nbt) * DE, r = res_slot(g, nw);
+      if (t % nbt == 0) acc = (!first_pass && lane < nb) ? s.v.acc[lane][r] : 0.0f;
+#pragma unroll
+      for (int d = 0; d < DE; ++d)
+        if (ub + d < u1)
+          for (int pp = s.ustart[ub + d]; pp < s.ustart[ub + d + 1]; ++pp) {
+            const float y = bfr(bfr(dot_row<KK>(Rb[d], s.v.xs + (pp - p0) * KK, lane)) * s.pw[pp]);
+            if (lane == s.pseq[pp]) acc = bfr(acc + y);
+          }
+      if (t % nbt == nbt - 1 && lane < nb) {
+        if (last_pass) st_ag_u16(p.x16 + (size_t)lane * H + g, f2bf(s.v.xres[lane][r] + acc));
+        else s.v.acc[lane][r] = acc;
+      }
+    };
+    auto batch_g = [&](int t) { return gw + (t / nbt) * nw; };
+    auto batch_u = [&](int t) { return u0 + (t % nbt) * DE; };
+    if (!first_pass && T > 0) issue(R[0], batch_g(0), batch_u(0), u1);
+    for (int t = 0; t < T; t += 2) {
+      if (t + 1 < T) issue(R[1], batch_g(t + 1), batch_u(t + 1), u1);
+      compute(R[0], t);
+      if (t + 2 < T) issue(R[0], batch_g(t + 2), batch_u(t + 2), u1);
+      if (t + 1 < T) compute(R[1], t + 1);
+    }
+    first_pass = false;
+    u0 = u1;
+    if (u0 < U) u1 = pass_end(u0);
+  }
+  if (U == 0)                                             // no expert (never with TOPK >= 1): the residual passes
+    for (int g = gw; g < H; g += nw)
+      if (lane < nb) st_ag_u16(p.x16 + (size_t)lane * H + g, f2bf(s.v.xres[lane][res_slot(g, nw)]));
+}
+
+// dense MLP (ref_numpy.py:149-152): gate/up + SiLU*up per sequence into h16, then down + residual
+template <int KK, int B, class S, class Wait>
+__device__ __forceinline__ void phase_gateup_b(const Params& p, int layer, S& s, Wait wait) {
+  const LayerW Lw = layer_w(p, layer);
+  const int I = p.I, nb = p.B;
+  const uint16_t* W = Lw.wgu;
+  gemv_run_b<KK, 2, B>(
+      I, [&](int g, int i) -> const uint16_t* { return W + ((size_t)2 * g + i) * KK; }, [&](int) { return nb; },
+      [&](int, int b) { return (const uint16_t*)(s.n.xs + b * KK); },
+      [&](int g, int nv, const float(&v)[2][B]) {
+        const int lane = lane_id();
+#pragma unroll
+        for (int b = 0; b < B; ++b)
+          if (lane == b && b < nv)
+            st_ag_u16(p.h16 + (size_t)b * I + perm_stored(g, I), f2bf(bfr(bfr(silu(bfr(v[0][b]))) * bfr(v[1][b]))));
+      },
+      [&]() {
+        if (!wait()) return false;
+        build_norm_xb<KK, B>(p, false, Lw.ln2, s);
+        return true;
+      },
+      p.nwg, p.trace, s.phase);
+}
+
+template <int KK, int B, class S, class Wait>
+__device__ __forceinline__ void phase_down_b(const Params& p, int layer, S& s, Wait wait) {
+  static_assert(B * KK <= S::XCAP, "intermediate rows exceed the LDS budget");
+  const LayerW Lw = layer_w(p, layer);
+  const int H = p.H, nb = p.B, nw = p.nwg * NWAVE;
+  const uint16_t* W = Lw.wd;
+  gemv_run_b<KK, 1, B>(
+      H, [&](int g, int) -> const uint16_t* { return W + (size_t)g * KK; }, [&](int) { return nb; },
+      [&](int, int b) { return (const uint16_t*)(s.v.xs + b * KK); },
+      [&](int g, int nv, const float(&v)[1][B]) {
+        const int r = res_slot(g, nw);
+        lane_store_b<1, B>(v, nv, [&](int, int b, float val) {
+          st_ag_u16(p.x16 + (size_t)b * H + g, f2bf(s.v.xres[b][r] + bfr(val)));
+        });
+      },
+      [&]() {
+        load_res_rows<B>(p, H, false, s);
+        if (!wait()) return false;
+        copy_rows_lds(p.h16, nb * KK, s.v.xs);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        return true;
+      },
+      p.nwg, p.trace, s.phase);
+}
+
+// P7: final norm + lm_head + greedy argmax per sequence (ref_numpy.py:155-158; vl_tiles.hip:45-89)
+template <int KK, int B, class S, class Wait>
+__device__ __forceinline__ void phase_head_b(const Params& p, S& s, Wait wait) {
+  const int V = p.V, nb = p.B;
+  const uint16_t* W = p.lm_head;
+  uint64_t best[B];
+#pragma unroll
+  for (int b = 0; b < B; ++b) best[b] = 0;
+  const bool ran = gemv_run_b<KK, 2, B>(
+      (V + 1) / 2,
+      [&](int g, int i) -> const uint16_t* { const int r = 2 * g + i; return r < V ? W + (size_t)r * KK : nullptr; },
+      [&](int) { return nb; }, [&](int, int b) { return (const uint16_t*)(s.n.xs + b * KK); },
+      [&](int g, int nv, const float(&v)[2][B]) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const int r = 2 * g + i;
+          if (r < V)
+#pragma unroll
+            for (int b = 0; b < B; ++b)
+              if (b < nv) {
+                const uint64_t key = argmax_key(bfr(v[i][b]), r);
+                best[b] = key > best[b] ? key : best[b];
+              }
+        }
+      },
+      [&]() {
+        if (!wait()) return false;
+        build_norm_xb<KK, B>(p, false, p.final_norm, s);
+        if (blockIdx.x == 0 && p.dump_x)
+          for (int i = threadIdx.x; i < nb * KK; i += NT)
+            st_f(p.dump_x + (size_t)(p.l1 - 1) * nb * KK + i, bf2f(s.n.xr[i]));
+        return true;
+      },
+      p.nwg, p.trace, s.phase);
+  if (ran && lane_id() == 0)
+#pragma unroll
+    for (int b = 0; b < B; ++b)
+      if (b < nb && best[b]) __hip_atomic_fetch_max(p.amax + 32 * b, best[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <class Wait>
+__device__ __forceinline__ void phase_token_b(const Params& p, Wait wait) {
+  if (!wait()) return;
+  const int b = threadIdx.x;
+  if (blockIdx.x == 0 && b < p.B) {
+    const uint64_t key = ld_ag64(p.amax + 32 * b);
+    int32_t tok = (int32_t)(0xFFFFFFFFu - (uint32_t)key);
+    if (key == 0 || tok < 0 || tok >= p.V) {              // no finite logit was seen: flag it, keep the id valid
+      st_ag_i(p.abort_word, 3);
+      tok = 0;
+    }
+    const size_t row = (size_t)b * p.tok_stride;
+    st_ag_i(p.out_tokens + row + p.posb[b], tok);
+    if ((p.write_next >> b) & 1) st_ag_i(p.tokens + row + p.posb[b] + 1, tok);
+  }
+}
+
+// ---------------------------------------------------------------- batched persistent kernel
+template <int H, int KA, int KM, bool MOE, int EC, int B>
+__device__ __forceinline__ void fused_body_b(const Params& p) {
+  __shared__ SmemB<B> s;
+  if (threadIdx.x == 0) s.abort = 0;
+  __syncthreads();
+  int k = 0;
+  auto wait = [&]() { return grid_wait(p, k, s); };
+  if (p.trace && threadIdx.x == 0) *(MK_G uint64_t*)(p.trace + (size_t)blockIdx.x * 3) = __builtin_amdgcn_s_memrealtime();
+  s.phase = 0;
+  for (int layer = p.l0; layer < p.l1; ++layer) {
+    phase_qkv_b<H, B>(p, layer, s, wait);
+    if (s.abort) return;
+    grid_arrive(p, k, s);
+    phase_attn<B>(p, layer, s, wait);
+    if (s.abort) return;
+    grid_arrive(p, k, s);
+    phase_oproj_b<KA, B>(p, layer, s, wait);
+    if (s.abort) return;
+    grid_arrive(p, k, s);
+    if constexpr (MOE) {
+      phase_router_b<H, B>(p, layer, s, wait);
+      if (s.abort) return;
+      grid_arrive(p, k, s);
+      phase_expert_up_b<H, B, EC>(p, layer, s, wait);
+      if (s.abort) return;
+      grid_arrive(p, k, s);
+      phase_expert_down_b<KM, B>(p, layer, s, wait);
+      if (s.abort) return;
+      grid_arrive(p, k, s);
+    } else {
+      phase_gateup_b<H, B>(p, layer, s, wait);
+      if (s.abort) return;
+      grid_arrive(p, k, s);
+      phase_down_b<KM, B>(p, layer, s, wait);
+      if (s.abort) return;
+      grid_arrive(p, k, s);
+    }
+  }
+  if (p.do_head) {
+    phase_head_b<H, B>(p, s, wait);
+    if (s.abort) return;
+    grid_arrive(p, k, s);
+    phase_token_b(p, wait);
+  }
+}
+
+// batched shapes: name, H, KA, KM, MoE, E, batch capacity (the host picks the smallest capacity >= its batch)
+#define MK_BATCH_SHAPES(X)                                                    \
+  X(etxmk_fused_b4_h2048_a4096_moe768_e128, 2048, 4096, 768, true, 128, 4)   \
+  X(etxmk_fused_b16_h2048_a4096_moe768_e128, 2048, 4096, 768, true, 128, 16) \
+  X(etxmk_fused_b4_h512_a512_moe256_e16, 512, 512, 256, true, 16, 4)         \
+  X(etxmk_fused_b16_h512_a512_moe256_e16, 512, 512, 256, true, 16, 16)       \
+  X(etxmk_fused_b4_h512_a512_mlp1024, 512, 512, 1024, false, 0, 4)
+#define MK_BATCH_KERNEL(name, H, KA, KM, MOE, EC, B) \
+  extern "C" __global__ void __launch_bounds__(NT, 1) name(Params p) { fused_body_b<H, KA, KM, MOE, EC, B>(p); }
+MK_BATCH_SHAPES(MK_BATCH_KERNEL)
+
+}  // namespace mk

@@ -38,6 +38,7 @@ constexpr int MAX_E = 256;
 constexpr int MAX_TOPK = 8;
 constexpr int PART = HDIM + 2;          // attention partial: a[HD], m, l
 constexpr int QKVW_BYTES = 81920;       // the workgroup's rows of the next layer's QKV matrix, staged in LDS
+constexpr int MAX_B = 16;               // sequences per batched step
 
 struct LayerW {
   const uint16_t *ln1, *ln2, *qn, *kn;
@@ -78,6 +79,24 @@ struct Params {
   uint32_t bar_base;
   int nwg;
   uint64_t spin_ticks;
+  // batched steps: per-sequence activations are [B][...] rows of the buffers above; tokens / out_tokens rows are
+  // tok_stride long; btab rows nbps long; amax entries 256 bytes apart
+  int B, nbps, tok_stride;
+  uint16_t* x16;                        // [B][H] residual, bf16
+  uint16_t* o16;                        // [B][NH*HD] attention output, bf16 lane-permuted
+  uint16_t* h16;                        // MoE [pairs][MI] / dense [B][I] MLP activations, bf16 lane-permuted
+  int posb[MAX_B];                      // sequence b's position
+  int ibase[MAX_B + 1];                 // attention items of the sequences before b (NKV * chunks each)
+};
+
+// the attention phase's LDS (one (sequence, kv head, chunk) item at a time)
+struct AttnTiles {
+  u32x4 kt[HDIM / 8][CHUNK];            // K tile: [8-dim group][position in chunk], 16 bytes each
+  u32x4 vt[CHUNK / 8][2][CHUNK];        // V tile: [8-position group][dim half][dim in half], 16 bytes each
+  alignas(16) float q[MAX_G][HDIM];     // roped q heads of the kv group
+  float knew[HDIM], vnew[HDIM];         // this step's k (roped) and v of the kv group
+  float p[MAX_G][2 * CHUNK];            // exp(s - m_c) of the chunk per head; merge: chunk weights and sums
+  float m[MAX_G];
 };
 
 struct Smem {
@@ -86,14 +105,7 @@ struct Smem {
       float xf[MAX_H];                  // residual (natural order, fp32)
       alignas(16) uint16_t xs[MAX_K];   // GEMV input vector(s), lane-permuted bf16
     } g;
-    struct {
-      u32x4 kt[HDIM / 8][CHUNK];        // K tile: [8-dim group][position in chunk], 16 bytes each
-      u32x4 vt[CHUNK / 8][2][CHUNK];    // V tile: [8-position group][dim half][dim in half], 16 bytes each
-      alignas(16) float q[MAX_G][HDIM]; // roped q heads of the kv group
-      float knew[HDIM], vnew[HDIM];     // this step's k (roped) and v of the kv group
-      float p[MAX_G][2 * CHUNK];        // exp(s - m_c) of the chunk per head; merge: chunk weights and sums
-      float m[MAX_G];
-    } a;
+    AttnTiles a;
   };
   alignas(16) u32x4 qkvw[QKVW_BYTES / 16];  // next layer's QKV rows [row of this workgroup][K/8], lane-permuted
   float rs;
@@ -129,7 +141,8 @@ __device__ __forceinline__ int wave_u() { return __builtin_amdgcn_readfirstlane(
 // agent-scope load; each wave waits for its own stores to complete (s_waitcnt 0) before the workgroup barrier
 // that precedes the arrival, so no L2 write-back or invalidate is needed.  The wait is bounded by a wall-clock
 // limit; on expiry the abort word is set and every workgroup leaves.
-__device__ __forceinline__ void grid_arrive(const Params& p, int& k, Smem& s) {
+template <class S>
+__device__ __forceinline__ void grid_arrive(const Params& p, int& k, S& s) {
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (threadIdx.x == 0) {
@@ -149,7 +162,8 @@ __device__ __forceinline__ void grid_arrive(const Params& p, int& k, Smem& s) {
 }
 
 // wait until the k-th arrival's generation is published (nothing to wait for when k == 0)
-__device__ __forceinline__ bool grid_wait(const Params& p, int k, Smem& s) {
+template <class S>
+__device__ __forceinline__ bool grid_wait(const Params& p, int k, S& s) {
   if (k == 0) return true;
   if (threadIdx.x == 0) {
     const uint32_t gen = p.bar_base + (uint32_t)k;
@@ -562,23 +576,39 @@ __device__ __forceinline__ void qk_norm(float& a0, float& a1, float w0, float w1
   a1 = bfr(w1 * bfr(a1 * r));
 }
 
-template <class Wait>
-__device__ __forceinline__ void phase_attn(const Params& p, int layer, Smem& s, Wait wait) {
+// One attention work item: sequence b (always 0 in single-sequence kernels), kv head g, chunk c of the sequence's
+// positions 0..pos.  Items are numbered sequence by sequence (p.ibase), kv head fastest.
+struct AttnItem {
+  int b, g, c, pos;
+};
+template <int B>
+__device__ __forceinline__ AttnItem attn_item(const Params& p, int item) {
+  int b = 0, r = item;
+  if constexpr (B > 1) {
+    while (b + 1 < p.B && item >= p.ibase[b + 1]) ++b;
+    r = item - p.ibase[b];
+  }
+  return AttnItem{b, r % p.NKV, r / p.NKV, B > 1 ? p.posb[b] : p.pos};
+}
+
+template <int B, class S, class Wait>
+__device__ __forceinline__ void phase_attn(const Params& p, int layer, S& s, Wait wait) {
   const int NKV = p.NKV, NH = p.NH, G = NH / NKV, HD = HDIM, BS = p.BS;
-  const int pos = p.pos, n = pos + 1, nch = (n + CHUNK - 1) / CHUNK;
+  const int NQKV = (NH + 2 * NKV) * HD;
+  const int nitems = B > 1 ? p.ibase[p.B] : NKV * ((p.pos + CHUNK) / CHUNK);
   const LayerW Lw = layer_w(p, layer);
   const int lane = lane_id(), wave = wave_u();
-  const float* cs = p.rope_cos + (size_t)pos * (HD / 2);
-  const float* sn = p.rope_sin + (size_t)pos * (HD / 2);
   // The chunk's cached K and V go straight from HBM into LDS tiles (global_load_lds, 16 bytes per lane); they do
   // not depend on this step, so the first item's copies are issued before the wait.  Wave w copies K dim-groups
   // 2w, 2w+1 (lane = position) and the V position-group w (lane = dim, both halves).
   auto load_kv = [&](int item) {
-    const int g = item % NKV, c = item / NKV;
+    const AttnItem it = attn_item<B>(p, item);
+    const int g = it.g, c = it.c, pos = it.pos, n = pos + 1;
+    const int32_t* btab = p.btab + (size_t)it.b * p.nbps;
     const int t0 = c * CHUNK, len = min(CHUNK, n - t0);
     const int t = t0 + lane;
     if (lane < len && t != pos) {
-      const int blk = ld_i(p.btab + t / BS), off = t % BS;
+      const int blk = ld_i(btab + t / BS), off = t % BS;
       const uint16_t* kp = Lw.kc + (((size_t)blk * NKV + g) * (HD / 8)) * BS * 8 + off * 8;
 #pragma unroll
       for (int jj = 2 * wave; jj < 2 * wave + 2; ++jj)
@@ -587,7 +617,7 @@ __device__ __forceinline__ void phase_attn(const Params& p, int layer, Smem& s, 
     }
     const int tb = t0 + wave * 8;                         // 8 positions per 16-byte load
     if (tb < t0 + len) {
-      const int blk = ld_i(p.btab + tb / BS), off = tb % BS;
+      const int blk = ld_i(btab + tb / BS), off = tb % BS;
       const uint16_t* vp = Lw.vc + ((size_t)blk * NKV + g) * HD * BS + off;
       __builtin_amdgcn_global_load_lds((const MK_G void*)(vp + (size_t)lane * BS),
                                        (__attribute__((address_space(3))) void*)&s.a.vt[wave][0][0], 16, 0, 0);
@@ -595,26 +625,41 @@ __device__ __forceinline__ void phase_attn(const Params& p, int layer, Smem& s, 
                                        (__attribute__((address_space(3))) void*)&s.a.vt[wave][1][0], 16, 0, 0);
     }
   };
-  const float rc = ld_f(cs + lane), rs = ld_f(sn + lane);
+  // RoPE factors of the position (ref_numpy.py:76-81 tables), reloaded when an item's sequence has another
+  int rpos = (int)blockIdx.x < nitems ? attn_item<B>(p, blockIdx.x).pos : 0;
+  float rc = ld_f(p.rope_cos + (size_t)rpos * (HD / 2) + lane), rs = ld_f(p.rope_sin + (size_t)rpos * (HD / 2) + lane);
   const float qn0 = bf2f(ld_u16(Lw.qn + lane)), qn1 = bf2f(ld_u16(Lw.qn + lane + 64));
   const float kn0 = bf2f(ld_u16(Lw.kn + lane)), kn1 = bf2f(ld_u16(Lw.kn + lane + 64));
-  if ((int)blockIdx.x < NKV * nch) load_kv(blockIdx.x);
+  if ((int)blockIdx.x < nitems) load_kv(blockIdx.x);
   if (!wait()) return;
-  for (int item = blockIdx.x; item < NKV * nch; item += p.nwg) {
-    const int g = item % NKV, c = item / NKV;
+  for (int item = blockIdx.x; item < nitems; item += p.nwg) {
+    const AttnItem it = attn_item<B>(p, item);
+    const int g = it.g, c = it.c, pos = it.pos, n = pos + 1, nch = (n + CHUNK - 1) / CHUNK;
+    const int32_t* btab = p.btab + (size_t)it.b * p.nbps;
+    const float* qkv = p.qkv + (size_t)it.b * NQKV;
+    float* apart = p.apart + (size_t)it.b * NH * MAX_CHUNKS * PART;
+    uint32_t* acnt = p.acnt + (size_t)it.b * NKV * 64;
+    float* o = p.o + (size_t)it.b * NH * HD;
     const int t0 = c * CHUNK, len = min(CHUNK, n - t0);
     const bool has_new = pos < t0 + len;                 // this chunk holds the current position
     if (item != (int)blockIdx.x) load_kv(item);
+    if constexpr (B > 1) {
+      if (pos != rpos) {
+        rpos = pos;
+        rc = ld_f(p.rope_cos + (size_t)pos * (HD / 2) + lane);
+        rs = ld_f(p.rope_sin + (size_t)pos * (HD / 2) + lane);
+      }
+    }
     for (int j = wave; j < G; j += NWAVE) {               // roped q of head g*G + j (ref_numpy.py:116-120)
-      const float* src = p.qkv + (size_t)(g * G + j) * HD;
+      const float* src = qkv + (size_t)(g * G + j) * HD;
       float a0 = ld_ag(src + lane), a1 = ld_ag(src + lane + 64);
       if (p.qk_norm) qk_norm(a0, a1, qn0, qn1, p.eps);
       s.a.q[j][lane] = bfr(bfr(a0 * rc) + bfr(-a1 * rs));
       s.a.q[j][lane + 64] = bfr(bfr(a1 * rc) + bfr(a0 * rs));
     }
     if (has_new && wave == NWAVE - 1) {                   // this step's k (normed, roped) and v
-      const float* ks = p.qkv + (size_t)(NH + g) * HD;
-      const float* vs = p.qkv + (size_t)(NH + NKV + g) * HD;
+      const float* ks = qkv + (size_t)(NH + g) * HD;
+      const float* vs = qkv + (size_t)(NH + NKV + g) * HD;
       float a0 = ld_ag(ks + lane), a1 = ld_ag(ks + lane + 64);
       const float v0 = ld_ag(vs + lane), v1 = ld_ag(vs + lane + 64);
       if (p.qk_norm) qk_norm(a0, a1, kn0, kn1, p.eps);
@@ -636,7 +681,7 @@ __device__ __forceinline__ void phase_attn(const Params& p, int layer, Smem& s, 
     }
     __syncthreads();
     if (has_new && threadIdx.x < HD) {                    // paged append (:121): K [blk][NKV][HD/8][BS][8], V [blk][NKV][HD][BS]
-      const int blk = ld_i(p.btab + pos / BS), off = pos % BS, d = threadIdx.x;
+      const int blk = ld_i(btab + pos / BS), off = pos % BS, d = threadIdx.x;
       st_u16(Lw.kc + ((((size_t)blk * NKV + g) * (HD / 8) + d / 8) * BS + off) * 8 + d % 8, f2bf(s.a.knew[d]));
       st_u16(Lw.vc + (((size_t)blk * NKV + g) * HD + d) * BS + off, f2bf(s.a.vnew[d]));
     }
@@ -689,7 +734,7 @@ __device__ __forceinline__ void phase_attn(const Params& p, int layer, Smem& s, 
       float a0 = 0.0f, a1 = 0.0f, l = 0.0f;
       if (len == CHUNK) pv(j, std::true_type{}, a0, a1, l);
       else pv(j, std::false_type{}, a0, a1, l);
-      float* part = p.apart + ((size_t)(g * G + j) * MAX_CHUNKS + c) * PART;
+      float* part = apart + ((size_t)(g * G + j) * MAX_CHUNKS + c) * PART;
       st_ag(part + lane, a0);
       st_ag(part + lane + 64, a1);
       if (lane == 0) { st_ag(part + HD, s.a.m[j]); st_ag(part + HD + 1, l); }
@@ -701,13 +746,13 @@ __device__ __forceinline__ void phase_attn(const Params& p, int layer, Smem& s, 
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (threadIdx.x == 0) {
-      const uint32_t old = __hip_atomic_fetch_add(p.acnt + 64 * g, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const uint32_t old = __hip_atomic_fetch_add(acnt + 64 * g, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       s.last = (old + 1u == (uint32_t)nch);
     }
     __syncthreads();
     if (s.last) {
       for (int j = wave; j < G; j += NWAVE) {
-        const float* part = p.apart + (size_t)(g * G + j) * MAX_CHUNKS * PART;
+        const float* part = apart + (size_t)(g * G + j) * MAX_CHUNKS * PART;
         // lane cc holds chunk cc's (m, l); the chunk weights go through LDS for the ordered sums.  The first MB
         // chunks' a[] are loaded together with (m, l) (they do not depend on the maximum): one memory round trip.
         constexpr int MB = 18;
@@ -739,10 +784,19 @@ __device__ __forceinline__ void phase_attn(const Params& p, int layer, Smem& s, 
               A1 = __builtin_fmaf(wc, av1[u], A1);
             }
         }
-        st_ag(p.o + (size_t)(g * G + j) * HD + lane, bfr(A0 / Ls));
-        st_ag(p.o + (size_t)(g * G + j) * HD + lane + 64, bfr(A1 / Ls));
+        if constexpr (B > 1) {
+          // batched: o goes out as the O projection's lane-permuted bf16 row, where dims lane and lane + 64 of a
+          // head are adjacent (NH*HD a multiple of 512, HD = 128), so one 4-byte store per lane
+          const int KA = NH * HD;
+          const int st = perm_stored((g * G + j) * HD + lane, KA);
+          st_ag_u32((uint32_t*)(p.o16 + (size_t)it.b * KA + st),
+                    (uint32_t)f2bf(A0 / Ls) | ((uint32_t)f2bf(A1 / Ls) << 16));
+        } else {
+          st_ag(o + (size_t)(g * G + j) * HD + lane, bfr(A0 / Ls));
+          st_ag(o + (size_t)(g * G + j) * HD + lane + 64, bfr(A1 / Ls));
+        }
       }
-      if (threadIdx.x == 0) __hip_atomic_store(p.acnt + 64 * g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (threadIdx.x == 0) __hip_atomic_store(acnt + 64 * g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
   }
@@ -805,16 +859,17 @@ __device__ __forceinline__ void phase_router(const Params& p, int layer, Smem& s
 // renormalised in slot order and rounded to bf16; `order` lists the slots by ascending expert id (the index_add_
 // order of the combine).  Results land in the wave's private LDS row s.ids/wts/order[wave].
 template <int EC = 0>
-__device__ __forceinline__ void route_topk(const Params& p, Smem& s) {
+__device__ __forceinline__ void route_topk_into(const Params& p, const float* logits, int32_t* ids_out, float* wts_out,
+                                                int32_t* order_out) {
   constexpr int EMAX = EC > 0 ? EC : MAX_E;
   constexpr int NW = (EMAX + 63) / 64;
   const int E = EC > 0 ? EC : p.E, K = p.TOPK;
-  const int lane = lane_id(), wave = wave_u();
+  const int lane = lane_id();
   float pv[NW];
 #pragma unroll
   for (int w = 0; w < NW; ++w) {
     const int e = lane + 64 * w;
-    pv[w] = e < E ? ld_ag(p.logits + e) : -__builtin_huge_valf();
+    pv[w] = e < E ? ld_ag(logits + e) : -__builtin_huge_valf();
   }
   float m = pv[0];
 #pragma unroll
@@ -866,11 +921,16 @@ __device__ __forceinline__ void route_topk(const Params& p, Smem& s) {
     for (int k = 0; k < MAX_TOPK; ++k)
       if (k < K && ids[k] < id) ++before;
     if (lane < K) {
-      s.ids[wave][lane] = id;
-      s.wts[wave][lane] = bfr(p.norm_topk ? wk / sel : wk);
-      s.order[wave][before] = lane;
+      ids_out[lane] = id;
+      wts_out[lane] = bfr(p.norm_topk ? wk / sel : wk);
+      if (order_out) order_out[before] = lane;
     }
   }
+}
+template <int EC = 0>
+__device__ __forceinline__ void route_topk(const Params& p, Smem& s) {
+  const int wave = wave_u();
+  route_topk_into<EC>(p, p.logits, s.ids[wave], s.wts[wave], s.order[wave]);
 }
 
 // P5: experts gate/up + SiLU*up for the top-k slots (ref_numpy.py:142-145).  The normed input depends only on x
@@ -1095,7 +1155,7 @@ __device__ __forceinline__ void fused_body(const Params& p) {
     else phase_qkv<H>(p, layer, s, wait);
     if (s.abort) return;
     grid_arrive(p, k, s);
-    phase_attn(p, layer, s, wait);
+    phase_attn<1>(p, layer, s, wait);
     if (s.abort) return;
     grid_arrive(p, k, s);
     phase_oproj<KA, decltype(wait), (H % 512 == 0 ? H : 0)>(p, layer, s, wait);
@@ -1150,7 +1210,7 @@ struct NoWait {
     CALL;                                                                         \
   }
 MK_PHASE_KERNEL(etxmk_p_qkv, phase_qkv_any(p, layer, s, NoWait{}))
-MK_PHASE_KERNEL(etxmk_p_attn, phase_attn(p, layer, s, NoWait{}))
+MK_PHASE_KERNEL(etxmk_p_attn, phase_attn<1>(p, layer, s, NoWait{}))
 MK_PHASE_KERNEL(etxmk_p_oproj, phase_oproj_any(p, layer, s, NoWait{}))
 MK_PHASE_KERNEL(etxmk_p_router, phase_router_any(p, layer, s, NoWait{}))
 MK_PHASE_KERNEL(etxmk_p_expert_up, phase_expert_up_any(p, layer, s, NoWait{}))

@@ -202,5 +202,16 @@ __device__ __forceinline__ int32_t ld_ag_i(const int32_t* p) {
 __device__ __forceinline__ void st_ag_i(int32_t* p, int32_t v) {
   __hip_atomic_store((MK_G int32_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+__device__ __forceinline__ uint16_t ld_ag_u16(const uint16_t* p) {
+  return __hip_atomic_load((const MK_G uint16_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_ag_u16(uint16_t* p, uint16_t v) {
+  __hip_atomic_store((MK_G uint16_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_ag_u32(uint32_t* p, uint32_t v) {
+  __hip_atomic_store((MK_G uint32_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// cache-policy operand of global_load_lds for an agent-coherent (sc1) load, like the agent-scope loads above
+constexpr int LDS_SC1 = 16;
 
 }  // namespace mk

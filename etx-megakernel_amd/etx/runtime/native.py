@@ -19,6 +19,7 @@ PKG = Path(__file__).resolve().parents[2]
 LIB_PATH = PKG / "lib" / "libetxmk.so"
 HEADER = PKG.parent / "include" / "etxmk.h"
 
+ABI_VERSION = 2
 OK, EINVAL, EHIP, ABORTED, EUNBOUND = 0, 1, 2, 3, 4
 T_EMBED, T_LMHEAD, T_WQKV, T_WO, T_ROUTER, T_W13, T_W2, T_WGU, T_WD = 1, 2, 3, 4, 5, 6, 7, 8, 9
 T_LN1, T_LN2, T_QNORM, T_KNORM, T_FINAL_NORM = 20, 21, 22, 23, 24
@@ -112,9 +113,13 @@ def load(path: Path | None = None):
         "etxmk_load_tensor": [vp, i32, i32, i32, vp, vp],
         "etxmk_set_block_table": [vp, C.POINTER(i32), i32, vp],
         "etxmk_fill_kv_seeded": [vp, u64, i32, vp],
+        "etxmk_fill_kv_seeded_seq": [vp, u64, i32, i32, vp],
         "etxmk_set_tokens": [vp, C.POINTER(i32), i32, vp],
         "etxmk_read_tokens": [vp, C.POINTER(i32), i32, vp],
+        "etxmk_set_tokens_seq": [vp, i32, C.POINTER(i32), i32, vp],
+        "etxmk_read_tokens_seq": [vp, i32, C.POINTER(i32), i32, vp],
         "etxmk_step": [vp, i32, i32, vp],
+        "etxmk_step_batch": [vp, C.POINTER(i32), i32, vp],
         "etxmk_step_layers": [vp, i32, i32, i32, vp],
         "etxmk_set_residual": [vp, C.POINTER(C.c_float), vp],
         "etxmk_read_residual": [vp, C.POINTER(C.c_float), vp],
@@ -129,8 +134,8 @@ def load(path: Path | None = None):
         f = getattr(L, name)
         f.argtypes = args
         f.restype = C.c_char_p if name == "etxmk_last_error" else C.c_int
-    if L.etxmk_abi_version() != 1:
-        raise EtxmkError(EINVAL, f"ABI version {L.etxmk_abi_version()} != 1")
+    if L.etxmk_abi_version() != ABI_VERSION:
+        raise EtxmkError(EINVAL, f"ABI version {L.etxmk_abi_version()} != {ABI_VERSION}")
     if path is None:
         _lib = L
     return L
@@ -227,12 +232,17 @@ class Decoder:
         """src: torch bf16/int16 tensor on the device in natural [rows][cols] layout."""
         _check(self.L, self.L.etxmk_load_tensor(self.h, kind, layer, expert, src.data_ptr(), self._stream()))
 
+    @property
+    def blocks_per_seq(self) -> int:
+        return -(-self.cfg.max_ctx // self.cfg.block_size)
+
     def set_block_table(self, table):
-        t = np.ascontiguousarray(table, np.int32)
+        """One sequence's table, or [batch][blocks_per_seq] (flattened row by row)."""
+        t = np.ascontiguousarray(np.asarray(table, np.int32).reshape(-1))
         _check(self.L, self.L.etxmk_set_block_table(self.h, t.ctypes.data_as(C.POINTER(C.c_int32)), len(t), self._stream()))
 
-    def fill_kv_seeded(self, seed: int, npos: int):
-        _check(self.L, self.L.etxmk_fill_kv_seeded(self.h, seed, npos, self._stream()))
+    def fill_kv_seeded(self, seed: int, npos: int, seq: int = 0):
+        _check(self.L, self.L.etxmk_fill_kv_seeded_seq(self.h, seed, seq, npos, self._stream()))
 
     def kv_layer(self, layer: int):
         """(K, V) of one layer as uint16 bf16 bits, paged layout, flat."""
@@ -250,11 +260,12 @@ class Decoder:
             self._dumps = None
             return
         k = max(cfg.TOPK, 1)
+        lb = (cfg.L,) if cfg.batch == 1 else (cfg.L, cfg.batch)      # batched handles: [layer][sequence][...]
         self._dumps = dict(
-            x=torch.zeros((cfg.L, cfg.H), dtype=torch.float32, device=self.device),
-            ids=torch.full((cfg.L, k), -1, dtype=torch.int32, device=self.device),
-            w=torch.zeros((cfg.L, k), dtype=torch.float32, device=self.device),
-            logits=torch.zeros((cfg.L, max(cfg.E, 1)), dtype=torch.float32, device=self.device))
+            x=torch.zeros(lb + (cfg.H,), dtype=torch.float32, device=self.device),
+            ids=torch.full(lb + (k,), -1, dtype=torch.int32, device=self.device),
+            w=torch.zeros(lb + (k,), dtype=torch.float32, device=self.device),
+            logits=torch.zeros(lb + (max(cfg.E, 1),), dtype=torch.float32, device=self.device))
         d = self._dumps
         moe = bool(cfg.moe)
         _check(self.L, self.L.etxmk_set_dump(self.h, d["x"].data_ptr(), d["ids"].data_ptr() if moe else None,
@@ -265,17 +276,28 @@ class Decoder:
         return {k: v.cpu().numpy().copy() for k, v in self._dumps.items()}
 
     # ---- steps
-    def set_tokens(self, tokens):
+    def set_tokens(self, tokens, seq: int = 0):
         t = np.ascontiguousarray(tokens, np.int32)
-        _check(self.L, self.L.etxmk_set_tokens(self.h, t.ctypes.data_as(C.POINTER(C.c_int32)), len(t), self._stream()))
+        _check(self.L, self.L.etxmk_set_tokens_seq(self.h, seq, t.ctypes.data_as(C.POINTER(C.c_int32)), len(t),
+                                                   self._stream()))
 
-    def read_tokens(self, n: int) -> np.ndarray:
+    def read_tokens(self, n: int, seq: int = 0) -> np.ndarray:
         out = np.zeros(n, np.int32)
-        _check(self.L, self.L.etxmk_read_tokens(self.h, out.ctypes.data_as(C.POINTER(C.c_int32)), n, self._stream()))
+        _check(self.L, self.L.etxmk_read_tokens_seq(self.h, seq, out.ctypes.data_as(C.POINTER(C.c_int32)), n,
+                                                    self._stream()))
         return out
 
     def step(self, pos: int, write_next: bool = True):
         _check(self.L, self.L.etxmk_step(self.h, pos, int(write_next), self._stream()))
+
+    def step_batch(self, positions, write_next=True):
+        """One step of every sequence; write_next: one flag for all, or one per sequence."""
+        pos = np.ascontiguousarray(positions, np.int32)
+        if pos.shape != (self.cfg.batch,):
+            raise ValueError(f"{pos.shape[0] if pos.ndim else 0} positions for batch {self.cfg.batch}")
+        flags = [write_next] * self.cfg.batch if np.isscalar(write_next) else list(write_next)
+        mask = sum(1 << b for b, f in enumerate(flags) if f)
+        _check(self.L, self.L.etxmk_step_batch(self.h, pos.ctypes.data_as(C.POINTER(C.c_int32)), mask, self._stream()))
 
     def step_layers(self, pos: int, l0: int, l1: int):
         _check(self.L, self.L.etxmk_step_layers(self.h, pos, l0, l1, self._stream()))
@@ -320,6 +342,28 @@ class Decoder:
         n = C.c_int32()
         _check(self.L, self.L.etxmk_barriers_per_step(self.h, C.byref(n)))
         return int(n.value)
+
+    def generate_batch(self, prompts, n_new: int) -> np.ndarray:
+        """Batched greedy decode: sequence b reads prompts[b] token by token, then decodes; every sequence moves one
+        position per step (sequences with shorter prompts start decoding earlier).  Returns [batch][n_new] ids."""
+        B = self.cfg.batch
+        prompts = [list(int(t) for t in p) for p in prompts]
+        if len(prompts) != B or min(len(p) for p in prompts) < 1:
+            raise ValueError(f"{len(prompts)} prompts for batch {B}")
+        lens = [len(p) for p in prompts]
+        T = max(lens) + n_new - 1
+        if T + 1 > self.cfg.max_ctx + 1 or max(lens) + n_new > self.cfg.max_ctx:
+            raise ValueError(f"prompts + {n_new} new tokens exceed max_ctx {self.cfg.max_ctx}")
+        for b, p in enumerate(prompts):
+            self.set_tokens(p, seq=b)
+        # sequence b decodes positions [0, lens[b] + n_new - 1); it waits (repeats its last step's position) once
+        # done, which rewrites the same cache entry with the same values
+        for s in range(T):
+            pos = [min(s, lens[b] + n_new - 2) for b in range(B)]
+            self.step_batch(pos, write_next=[pos[b] + 1 >= lens[b] for b in range(B)])
+        self.sync()
+        return np.stack([self.read_tokens(lens[b] + n_new - 1, seq=b)[lens[b] - 1:lens[b] - 1 + n_new]
+                         for b in range(B)])
 
     def generate(self, prompt, n_new: int) -> np.ndarray:
         """Feed the prompt token by token, then n_new greedy steps; returns the generated ids

@@ -17,7 +17,7 @@
 extern "C" {
 #endif
 
-#define ETXMK_ABI_VERSION 1
+#define ETXMK_ABI_VERSION 2
 
 /* status codes */
 #define ETXMK_OK 0
@@ -43,7 +43,11 @@ extern "C" {
 #define ETXMK_T_FINAL_NORM 24
 
 /* Model dimensions: the POD copy of examples/llm/model.py:45-93 Dims (load_dims, :95-140) that the
- * reference's llm_params.h (__constant__ LlmParams, examples/llm/llm_params.h:1-73) carries. */
+ * reference's llm_params.h (__constant__ LlmParams, examples/llm/llm_params.h:1-73) carries.
+ * batch: sequences decoded together (1..16; the reference's ETX_VL_REQUESTS requests,
+ * examples/vllm_llm/vl_tiles.hip:24-28).  Each sequence owns up to ceil(max_ctx / block_size) blocks of
+ * one paged-KV pool, its own token row and its own position; a batched step equals one single-sequence step
+ * per sequence, bit for bit. */
 typedef struct etxmk_config {
   int32_t H, NH, NKV, HD, I, E, TOPK, MI, L, V;
   int32_t moe, qk_norm, norm_topk, block_size, max_ctx, batch;
@@ -86,16 +90,22 @@ int etxmk_init_weights_seeded(etxmk_handle* h, uint64_t seed, float scale, void*
  * Reference: the weight load of examples/llm/host.hip:70-121. */
 int etxmk_load_tensor(etxmk_handle* h, int kind, int layer, int expert, const void* src, void* stream);
 
-/* Paged-KV block table: logical block i of the sequence -> physical block table[i].
- * Reference: block_tables upload, examples/vllm_llm/host.hip:279-282. */
+/* Paged-KV block tables, [batch][ceil(max_ctx / block_size)] flattened: entry b * nbps + i is the physical
+ * block of sequence b's logical block i; the first n entries are replaced.  No physical block may serve two
+ * entries.  Default: the identity.  Reference: block_tables upload, examples/vllm_llm/host.hip:279-282. */
 int etxmk_set_block_table(etxmk_handle* h, const int32_t* table, int32_t n, void* stream);
 
-/* Fill KV positions [0, npos) of every layer with bf16 N(0,1) from the seeded generator (the
- * single-layer configuration's cache).  No reference counterpart (the reference prefills by decoding). */
+/* Fill KV positions [0, npos) of sequence `seq` (every layer) with bf16 N(0,1) from the seeded generator (the
+ * single-layer configuration's cache, the batched workloads' contexts; stream kinds 10 and 11, expert field =
+ * seq).  No reference counterpart (the reference prefills by decoding).  etxmk_fill_kv_seeded = sequence 0. */
+int etxmk_fill_kv_seeded_seq(etxmk_handle* h, uint64_t seed, int32_t seq, int32_t npos, void* stream);
 int etxmk_fill_kv_seeded(etxmk_handle* h, uint64_t seed, int32_t npos, void* stream);
 
-/* Token buffer: tokens[0..n) are the prompt; step s reads tokens[s] (reference: P.token_in,
- * examples/llm/tiles.hip:77-82). */
+/* Token rows, one per sequence: tokens[0..n) are the prompt; a step at position s reads tokens[s] and writes
+ * out_tokens[s] (reference: P.token_in / token_out, examples/llm/tiles.hip:77-82; per request,
+ * examples/vllm_llm/vl_tiles.hip:12-22).  The unsuffixed forms address sequence 0. */
+int etxmk_set_tokens_seq(etxmk_handle* h, int32_t seq, const int32_t* tokens, int32_t n, void* stream);
+int etxmk_read_tokens_seq(etxmk_handle* h, int32_t seq, int32_t* out_tokens, int32_t n, void* stream);
 int etxmk_set_tokens(etxmk_handle* h, const int32_t* tokens, int32_t n, void* stream);
 int etxmk_read_tokens(etxmk_handle* h, int32_t* out_tokens, int32_t n, void* stream);
 
@@ -105,8 +115,15 @@ int etxmk_read_tokens(etxmk_handle* h, int32_t* out_tokens, int32_t n, void* str
  * etx_megakernel_d0 (etx/codegen/kernel.py:471-605), after llm_set_params (examples/llm/tiles.hip:16-19). */
 int etxmk_step(etxmk_handle* h, int32_t pos, int32_t write_next, void* stream);
 
+/* One decode step of every sequence of a batched handle, sequence b at position positions[b] (host array of
+ * `batch` entries), in one persistent launch (fused mode only).  Bit b of write_next_mask: sequence b's greedy
+ * token also goes to its tokens[positions[b] + 1] (clear while the sequence is still reading its prompt).
+ * Reference: vl_set_params with one VlParams per request (examples/vllm_llm/vl_tiles.hip:92-95) + etx_host::run. */
+int etxmk_step_batch(etxmk_handle* h, const int32_t* positions, int32_t write_next_mask, void* stream);
+
 /* Layers [l0, l1) only, on the residual already in the workspace (etxmk_set_residual), no embedding and
- * no head: the single-layer configuration.  Reference: a graph of one layer (examples/llm/model.py:220-273). */
+ * no head: the single-layer configuration (single-sequence handles).  Reference: a graph of one layer
+ * (examples/llm/model.py:220-273). */
 int etxmk_step_layers(etxmk_handle* h, int32_t pos, int32_t l0, int32_t l1, void* stream);
 int etxmk_set_residual(etxmk_handle* h, const float* x, void* stream);
 int etxmk_read_residual(etxmk_handle* h, float* x, void* stream);
@@ -119,8 +136,8 @@ int etxmk_sync(etxmk_handle* h, void* stream);
  * phase with the same device functions (reference: run_unfused, etx/runtime/include/etx/host.h:418-457). */
 int etxmk_set_fused(etxmk_handle* h, int32_t fused);
 
-/* Per-layer dumps of the next steps (device pointers, may be NULL): residual after each layer [L][H] fp32,
- * top-k ids [L][TOPK] int32, weights [L][TOPK] fp32, router logits [L][E] fp32.
+/* Per-layer dumps of the next steps (device pointers, may be NULL): residual after each layer [L][batch][H] fp32,
+ * top-k ids [L][batch][TOPK] int32, weights [L][batch][TOPK] fp32, router logits [L][batch][E] fp32.
  * Reference: ref_numpy.py --dump (examples/llm/ref_numpy.py:199-201) and host --check-dsl
  * (examples/vllm_llm/host.hip:954-1141). */
 int etxmk_set_dump(etxmk_handle* h, float* x_layers, int32_t* topk_ids, float* topk_w, float* router_logits);

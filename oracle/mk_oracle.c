@@ -341,8 +341,8 @@ typedef struct {
   uint64_t seed;
   uint16_t *embed, *lm_head;
   orc_layer* ly;
-  int32_t* btab;
-  int nblocks;
+  int32_t* btab;                  /* [batch][nbps]: sequence b's logical block i -> physical block */
+  int nblocks, nbps, batch;
   float *rcos, *rsin;
   float scale;
 } orc_model;
@@ -360,7 +360,9 @@ EXPORT void* orc_model_create(const orc_config* cfg, uint64_t seed, float wscale
   const int NQKV = (c->NH + 2 * c->NKV) * c->HD;
   m->embed = gen_tensor(seed, sid(S_EMBED, -1, 0), (size_t)c->V * c->H, wscale);
   m->lm_head = gen_tensor(seed, sid(S_LMHEAD, -1, 0), (size_t)c->V * c->H, wscale);
-  m->nblocks = (c->max_ctx + c->block_size - 1) / c->block_size;
+  m->batch = c->batch > 1 ? c->batch : 1;
+  m->nbps = (c->max_ctx + c->block_size - 1) / c->block_size;
+  m->nblocks = m->batch * m->nbps;               /* one paged pool shared by the sequences of the batch */
   m->btab = (int32_t*)malloc(sizeof(int32_t) * (size_t)m->nblocks);
   for (int i = 0; i < m->nblocks; ++i) m->btab[i] = i;
   m->ly = (orc_layer*)calloc((size_t)c->L, sizeof(orc_layer));
@@ -399,32 +401,38 @@ EXPORT void orc_model_destroy(void* h) {
   free(m->ly); free(m->embed); free(m->lm_head); free(m->btab); free(m->rcos); free(m->rsin); free(m);
 }
 
-/* block table override: physical block of logical block i */
+/* block table override, [batch][blocks per sequence] flattened: entry b * nbps + i is the physical block of
+ * sequence b's logical block i (examples/vllm_llm/host.hip:279-282 uploads the same table) */
 EXPORT void orc_set_block_table(void* h, const int32_t* bt, int n) {
   orc_model* m = (orc_model*)h;
   for (int i = 0; i < n && i < m->nblocks; ++i) m->btab[i] = bt[i];
 }
 EXPORT int orc_num_blocks(void* h) { return ((orc_model*)h)->nblocks; }
+EXPORT int orc_blocks_per_seq(void* h) { return ((orc_model*)h)->nbps; }
 EXPORT const uint16_t* orc_kcache(void* h, int layer) { return ((orc_model*)h)->ly[layer].kc; }
 EXPORT const uint16_t* orc_vcache(void* h, int layer) { return ((orc_model*)h)->ly[layer].vc; }
 
-/* fill positions [0, n) of every layer's cache with bf16 N(0,1) (the single-layer configuration) */
-EXPORT void orc_fill_kv_random(void* h, int n) {
+/* fill positions [0, n) of sequence `seq`'s cache in every layer with bf16 N(0,1) (the single-layer
+ * configuration; the batched workloads' contexts): element (t, h, d) is number (t*NKV + h)*HD + d of the
+ * layer's K / V stream for that sequence */
+EXPORT void orc_fill_kv_random_seq(void* h, int seq, int n) {
   orc_model* m = (orc_model*)h; const orc_config* c = &m->c;
   const int NKV = c->NKV, HD = c->HD, BS = c->block_size;
+  const int32_t* bt = m->btab + (size_t)seq * m->nbps;
   for (int l = 0; l < c->L; ++l) {
-    const uint64_t kk = stream_key(m->seed, sid(S_KINIT, l, 0)), vk = stream_key(m->seed, sid(S_VINIT, l, 0));
+    const uint64_t kk = stream_key(m->seed, sid(S_KINIT, l, seq)), vk = stream_key(m->seed, sid(S_VINIT, l, seq));
 #pragma omp parallel for schedule(static)
     for (int t = 0; t < n; ++t)
       for (int hh = 0; hh < NKV; ++hh)
         for (int d = 0; d < HD; ++d) {
           const uint64_t idx = ((uint64_t)t * NKV + hh) * HD + d;
-          const int blk = m->btab[t / BS], off = t % BS;
+          const int blk = bt[t / BS], off = t % BS;
           m->ly[l].kc[kv_k_index(blk, off, hh, d, NKV, HD, BS)] = f2bf(mk_normal(kk, idx));
           m->ly[l].vc[kv_v_index(blk, off, hh, d, NKV, HD, BS)] = f2bf(mk_normal(vk, idx));
         }
   }
 }
+EXPORT void orc_fill_kv_random(void* h, int n) { orc_fill_kv_random_seq(h, 0, n); }
 
 static void ensure_expert(orc_model* m, int l, int e) {
   const orc_config* c = &m->c;
@@ -439,8 +447,10 @@ static void gemv_bf(const uint16_t* W, int R, int K, const float* x, float* out)
   for (int r = 0; r < R; ++r) out[r] = bfr(dot64(W + (size_t)r * K, x, K));
 }
 
-/* one decoder layer at position pos on residual x (in place); dump_ids / dump_wts / dump_logits optional */
-static void layer_step(orc_model* m, int l, float* x, int pos, int32_t* ids_out, float* wts_out, float* logits_out) {
+/* one decoder layer at position pos on residual x (in place) of the sequence whose block table is bt;
+ * dump_ids / dump_wts / dump_logits optional */
+static void layer_step(orc_model* m, int l, float* x, int pos, const int32_t* bt, int32_t* ids_out, float* wts_out,
+                       float* logits_out) {
   const orc_config* c = &m->c;
   orc_layer* y = &m->ly[l];
   const int H = c->H, NH = c->NH, NKV = c->NKV, HD = c->HD, G = NH / NKV, BS = c->block_size;
@@ -458,7 +468,7 @@ static void layer_step(orc_model* m, int l, float* x, int pos, int32_t* ids_out,
     if (c->qk_norm) { rmsnorm(v, NULL, HD, c->eps, tmp); memcpy(v, tmp, sizeof(float) * (size_t)HD); }
     apply_rope(v, HD, cs, sn);
   }
-  const int blk = m->btab[pos / BS], off = pos % BS;               /* :121 KV append, paged */
+  const int blk = bt[pos / BS], off = pos % BS;                    /* :121 KV append, paged */
   for (int hh = 0; hh < NKV; ++hh)
     for (int d = 0; d < HD; ++d) {
       y->kc[kv_k_index(blk, off, hh, d, NKV, HD, BS)] = f2bf(qkv[(size_t)(NH + hh) * HD + d]);
@@ -466,7 +476,7 @@ static void layer_step(orc_model* m, int l, float* x, int pos, int32_t* ids_out,
     }
 #pragma omp parallel for schedule(static)
   for (int hh = 0; hh < NH; ++hh)                                   /* :122-129 */
-    attention_head(qkv + (size_t)hh * HD, y->kc, y->vc, m->btab, pos + 1, hh / G, NKV, HD, BS, o + (size_t)hh * HD);
+    attention_head(qkv + (size_t)hh * HD, y->kc, y->vc, bt, pos + 1, hh / G, NKV, HD, BS, o + (size_t)hh * HD);
   float* t = (float*)malloc(sizeof(float) * (size_t)(H > c->I ? H : c->I) * 2 + 64);
   gemv_bf(y->wo, H, NH * HD, o, t);                                 /* :130 */
   for (int i = 0; i < H; ++i) x[i] = bfr(x[i] + t[i]);
@@ -522,15 +532,17 @@ static void layer_step(orc_model* m, int l, float* x, int pos, int32_t* ids_out,
   free(xs); free(qkv); free(o); free(t);
 }
 
-/* ref_numpy.py:105-158 Ref.step: token at position pos -> greedy next token.
+/* ref_numpy.py:105-158 Ref.step for sequence `seq` of the batch: token at position pos -> greedy next token.
+ * The sequences of a batch share the weights and nothing else, so a batched step is this, once per sequence.
  * dump_x [L][H] residual after each layer; dump_ids/dump_wts [L][TOPK]; each may be NULL. */
-EXPORT int32_t orc_step(void* h, int32_t tok, int pos, float* dump_x, int32_t* dump_ids, float* dump_wts) {
+EXPORT int32_t orc_step_seq(void* h, int seq, int32_t tok, int pos, float* dump_x, int32_t* dump_ids, float* dump_wts) {
   orc_model* m = (orc_model*)h; const orc_config* c = &m->c;
   const int H = c->H;
+  const int32_t* bt = m->btab + (size_t)seq * m->nbps;
   float* x = (float*)malloc(sizeof(float) * (size_t)H);
   for (int i = 0; i < H; ++i) x[i] = bf2f(m->embed[(size_t)tok * H + i]);
   for (int l = 0; l < c->L; ++l) {
-    layer_step(m, l, x, pos, dump_ids ? dump_ids + (size_t)l * c->TOPK : NULL,
+    layer_step(m, l, x, pos, bt, dump_ids ? dump_ids + (size_t)l * c->TOPK : NULL,
                dump_wts ? dump_wts + (size_t)l * c->TOPK : NULL, NULL);
     if (dump_x) memcpy(dump_x + (size_t)l * H, x, sizeof(float) * (size_t)H);
   }
@@ -544,10 +556,18 @@ EXPORT int32_t orc_step(void* h, int32_t tok, int pos, float* dump_x, int32_t* d
   free(x); free(xs); free(lg);
   return best;
 }
+EXPORT int32_t orc_step(void* h, int32_t tok, int pos, float* dump_x, int32_t* dump_ids, float* dump_wts) {
+  return orc_step_seq(h, 0, tok, pos, dump_x, dump_ids, dump_wts);
+}
 
 /* the single-layer configuration: run layer `l` on the given residual x (in place) at position pos */
+EXPORT void orc_layer_step_seq(void* h, int seq, int l, float* x, int pos, int32_t* ids_out, float* wts_out,
+                               float* logits_out) {
+  orc_model* m = (orc_model*)h;
+  layer_step(m, l, x, pos, m->btab + (size_t)seq * m->nbps, ids_out, wts_out, logits_out);
+}
 EXPORT void orc_layer_step(void* h, int l, float* x, int pos, int32_t* ids_out, float* wts_out, float* logits_out) {
-  layer_step((orc_model*)h, l, x, pos, ids_out, wts_out, logits_out);
+  orc_layer_step_seq(h, 0, l, x, pos, ids_out, wts_out, logits_out);
 }
 
 /* generate every expert of every layer now (so that timing excludes generation) */

@@ -67,6 +67,11 @@ def lib():
             "orc_model_destroy": (None, [C.c_void_p]),
             "orc_set_block_table": (None, [C.c_void_p, i32p, C.c_int]),
             "orc_num_blocks": (C.c_int, [C.c_void_p]),
+            "orc_blocks_per_seq": (C.c_int, [C.c_void_p]),
+            "orc_fill_kv_random_seq": (None, [C.c_void_p, C.c_int, C.c_int]),
+            "orc_step_seq": (C.c_int32, [C.c_void_p, C.c_int, C.c_int32, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p]),
+            "orc_layer_step_seq": (None, [C.c_void_p, C.c_int, C.c_int, f32p, C.c_int, C.c_void_p, C.c_void_p,
+                                          C.c_void_p]),
             "orc_kcache": (C.POINTER(C.c_uint16), [C.c_void_p, C.c_int]),
             "orc_vcache": (C.POINTER(C.c_uint16), [C.c_void_p, C.c_int]),
             "orc_fill_kv_random": (None, [C.c_void_p, C.c_int]),
@@ -176,15 +181,20 @@ class OracleModel:
         self.close()
 
     def set_block_table(self, bt):
-        bt = np.ascontiguousarray(bt, np.int32)
+        """bt: one sequence's table, or [batch][blocks per sequence] (flattened row by row)."""
+        bt = np.ascontiguousarray(np.asarray(bt, np.int32).reshape(-1))
         lib().orc_set_block_table(self._h, bt, len(bt))
 
     @property
     def num_blocks(self) -> int:
         return lib().orc_num_blocks(self._h)
 
-    def fill_kv_random(self, n: int):
-        lib().orc_fill_kv_random(self._h, n)
+    @property
+    def blocks_per_seq(self) -> int:
+        return lib().orc_blocks_per_seq(self._h)
+
+    def fill_kv_random(self, n: int, seq: int = 0):
+        lib().orc_fill_kv_random_seq(self._h, int(seq), int(n))
 
     def kv(self, layer: int):
         c = self.cfg
@@ -203,28 +213,30 @@ class OracleModel:
         p = lib().orc_weight(self._h, kind, layer, expert)
         return np.ctypeslib.as_array(p, shape=(int(np.prod(shp)),)).reshape(shp).copy()
 
-    def step(self, tok: int, pos: int, dump: bool = False):
+    def step(self, tok: int, pos: int, dump: bool = False, seq: int = 0):
+        """Sequence `seq`'s decode step (a batched step is one call per sequence: they share only weights)."""
         c = self.cfg
         if not dump:
-            return int(lib().orc_step(self._h, int(tok), int(pos), None, None, None))
+            return int(lib().orc_step_seq(self._h, int(seq), int(tok), int(pos), None, None, None))
         x = np.empty((c["L"], c["H"]), np.float32)
         k = max(c["TOPK"], 1)
         ids = np.zeros((c["L"], k), np.int32)
         w = np.zeros((c["L"], k), np.float32)
-        t = int(lib().orc_step(self._h, int(tok), int(pos), x.ctypes.data, ids.ctypes.data, w.ctypes.data))
+        t = int(lib().orc_step_seq(self._h, int(seq), int(tok), int(pos), x.ctypes.data, ids.ctypes.data,
+                                   w.ctypes.data))
         return t, x, ids, w
 
     def materialize_experts(self):
         lib().orc_materialize_experts(self._h)
 
-    def layer_step(self, layer: int, x: np.ndarray, pos: int):
+    def layer_step(self, layer: int, x: np.ndarray, pos: int, seq: int = 0):
         c = self.cfg
         x = np.array(x, np.float32)
         k = max(c["TOPK"], 1)
         ids = np.zeros(k, np.int32)
         w = np.zeros(k, np.float32)
         lg = np.zeros(max(c["E"], 1), np.float32)
-        lib().orc_layer_step(self._h, layer, x, pos, ids.ctypes.data, w.ctypes.data, lg.ctypes.data)
+        lib().orc_layer_step_seq(self._h, int(seq), layer, x, pos, ids.ctypes.data, w.ctypes.data, lg.ctypes.data)
         return x, ids, w, lg
 
 

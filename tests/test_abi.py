@@ -14,7 +14,7 @@ def test_library_exports_every_declared_symbol():
     assert len(names) >= 20
     missing = [n for n in names if not hasattr(L, n)]
     assert not missing
-    assert L.etxmk_abi_version() == 1
+    assert L.etxmk_abi_version() == N.ABI_VERSION == 2
 
 
 def test_sizes_of_real_configurations():
@@ -28,8 +28,8 @@ def test_sizes_of_real_configurations():
     assert 15.0e9 < s8["weights"] < 16.5e9
 
 
-@pytest.mark.parametrize("bad", [dict(HD=64), dict(H=3000), dict(batch=2), dict(block_size=48), dict(max_ctx=10**6),
-                                 dict(TOPK=9), dict(E=0), dict(NKV=3)])
+@pytest.mark.parametrize("bad", [dict(HD=64), dict(H=3000), dict(batch=0), dict(batch=17), dict(block_size=48),
+                                 dict(max_ctx=10**6), dict(TOPK=9), dict(E=0), dict(NKV=3)])
 def test_config_refused(bad):
     d = configs.TINY_MOE.as_dict()
     d.update(bad)
@@ -37,6 +37,20 @@ def test_config_refused(bad):
     with pytest.raises(N.EtxmkError) as e:
         N.sizes(cfg)
     assert e.value.code == N.EINVAL
+
+
+def test_batch_needs_a_batched_kernel():
+    # Qwen3-8B's dense down projection (12288 long) has no batched kernel: refused, not run wrongly
+    with pytest.raises(N.EtxmkError) as e:
+        N.sizes(configs.with_layers(configs.QWEN3_8B, 36, batch=2))
+    assert e.value.code == N.EINVAL and "batched" in str(e.value)
+
+
+def test_batch_sizes_scale_per_sequence():
+    one, four = N.sizes(configs.QWEN3_30B_A3B), N.sizes(configs.with_layers(configs.QWEN3_30B_A3B, 48, batch=4))
+    assert four["weights"] == one["weights"]              # weights are shared by the sequences
+    assert four["kv"] == 4 * one["kv"]                    # one block pool, max_ctx positions per sequence
+    assert four["workspace"] > one["workspace"]
 
 
 def test_unpermute_inverts_the_lane_permutation():
