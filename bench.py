@@ -2,6 +2,7 @@
 """Headline benchmark: Qwen3-30B-A3B-shaped bf16 decode at batch 1 on one MI355X.
 
     python bench.py [--gpus 1] [--steps 32] [--warmup 4] [--ctx 1024] [--no-cpu] [--unfused]
+    python bench.py --batch 16 [--ctx-lo 512 --ctx-hi 4096]      (batched step; not the headline line)
 
 Setup (untimed): seeded random-init weights N(0, 0.02) in HBM, a prompt of `ctx` seeded random token ids fed
 token by token through the decode step (as examples/llm/host.hip:203-213 does), then `warmup` greedy steps.
@@ -51,6 +52,101 @@ def bytes_per_token(cfg, context: int) -> dict:
     kv = cfg.L * (context * kv_pos + kv_pos)
     weights = glob + cfg.L * layer
     return {"weights": weights, "kv": kv, "total": weights + kv}
+
+
+def bytes_per_step(cfg, contexts, union) -> dict:
+    """Algorithmic HBM bytes of one batched step: every non-expert weight once, each layer's distinct routed experts
+    once (union[l], measured), each sequence's KV read over its context plus one position written, one embedding
+    row per sequence (byte_ledger.py:121-178 rules with the expert union of a batch)."""
+    H, HD, NH, NKV, V = cfg.H, cfg.HD, cfg.NH, cfg.NKV, cfg.V
+    bf = 2
+    B = len(contexts)
+    glob = (B * H + H + V * H) * bf
+    layer = (2 * H + 2 * HD) * bf + ((NH + 2 * NKV) * HD * H + H * NH * HD) * bf
+    experts = 0
+    if cfg.moe:
+        layer += cfg.E * H * bf
+        experts = sum(int(u) * 3 * cfg.MI * H * bf for u in union)
+    else:
+        layer += 3 * cfg.I * H * bf
+    kv_pos = 2 * NKV * HD * bf
+    kv = cfg.L * sum((int(c) + 1) * kv_pos for c in contexts)
+    weights = glob + cfg.L * layer + experts
+    return {"weights": weights, "kv": kv, "total": weights + kv}
+
+
+def main_batch(a):
+    """Batched decode (BASELINE.json configs[4] shape with bf16 weights): `batch` sequences with per-sequence contexts
+    drawn uniform in [ctx_lo, ctx_hi] (seeded N(0,1) KV; the reference prefills by decoding), one seeded token each,
+    `warmup` then `steps` batched greedy steps (one persistent launch each)."""
+    import torch
+    from etx.runtime import native as N
+    from etx.models import configs
+    B = a.batch
+    rng = np.random.default_rng(a.seed + 4)
+    ctx = rng.integers(a.ctx_lo, a.ctx_hi + 1, B).astype(np.int32)
+    max_ctx = int(ctx.max()) + a.warmup + a.steps + 2
+    cfg = configs.with_layers(configs.QWEN3_30B_A3B, configs.QWEN3_30B_A3B.L, batch=B, max_ctx=max_ctx)
+    dev = torch.device("cuda:0")
+    t0 = time.time()
+    dec = N.Decoder(cfg, device="cuda:0", workgroups=a.workgroups)
+    dec.init_weights(a.seed, 0.02)
+    first = rng.integers(0, cfg.V, B).astype(np.int32)
+    for b in range(B):
+        dec.fill_kv_seeded(a.seed, int(ctx[b]), seq=b)
+        row = np.zeros(int(ctx[b]) + 1, np.int32)
+        row[-1] = first[b]
+        dec.set_tokens(row, seq=b)
+    dec.sync()
+    log(f"[gpu] batch {B}: weights {dec.sizes['weights'] / 1e9:.2f} GB, KV pool {dec.sizes['kv'] / 1e9:.2f} GB, "
+        f"contexts {list(ctx)} ready in {time.time() - t0:.1f}s")
+    pos = ctx.copy()
+    for _ in range(a.warmup):
+        dec.step_batch(pos)
+        pos += 1
+    dec.sync()
+    stream = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    first_timed = pos.copy()
+    w0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(a.steps):
+        dec.step_batch(pos)
+        pos += 1
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - w0) * 1e3
+    dec.sync()
+    ms = e0.elapsed_time(e1) / a.steps
+    # distinct routed experts per layer, from one more (untimed) step with the routing dumps on
+    dec.enable_dumps(True)
+    dec.step_batch(pos)
+    d = dec.dumps()
+    dec.enable_dumps(False)
+    union = [len(np.unique(d["ids"][l])) for l in range(cfg.L)]
+    mean_ctx = (first_timed + pos - 1) / 2.0
+    by = bytes_per_step(cfg, np.round(mean_ctx).astype(int), union)
+    gbps = by["total"] / (ms * 1e-3) / 1e9
+    log(f"[gpu] {a.steps} batched steps: {ms:.4f} ms/step ({ms / B:.4f} ms/token, {B * 1e3 / ms:.1f} tokens/s), "
+        f"{gbps:.1f} GB/s = {gbps / HBM_PEAK_GBPS:.3f} of 8 TB/s; expert union per layer mean {np.mean(union):.1f}")
+    out = {
+        "metric": f"decode ms/step at batch {B}, Qwen3-30B-A3B shape; tokens/s; achieved HBM GB/s vs peak",
+        "value": round(ms, 4), "unit": "ms/step", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic: seeded random-init bf16 weights N(0,0.02); per-sequence KV of seeded N(0,1) values",
+        "config": {"workload": f"{cfg.name} decode, batch {B}, contexts uniform in [{a.ctx_lo}, {a.ctx_hi}], greedy "
+                               f"(BASELINE.json configs[4] shape with bf16 weights)",
+                   "batch": B, "contexts": [int(c) for c in ctx], "layers": cfg.L, "experts": cfg.E,
+                   "top_k": cfg.TOPK, "vocab": cfg.V, "mode": "fused megakernel", "seed": a.seed},
+        "tokens_per_s": round(B * 1e3 / ms, 2), "ms_per_token": round(ms / B, 4),
+        "host_wall_ms_per_step": round(wall / a.steps, 4), "expert_union_mean": round(float(np.mean(union)), 2),
+        "bytes_per_step": by["total"], "achieved_GBps": round(gbps, 1),
+        "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None, "kernel": "etxmk_fused_b*"},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(out), flush=True)
 
 
 def cpu_baseline(cfg, ctx: int, seed: int) -> dict:
@@ -135,11 +231,16 @@ def main():
                     help="profiling runs: first copy 1 GiB device to device, the known-size reference for HBM counters")
     ap.add_argument("--kv-fill", action="store_true",
                     help="profiling runs: fill the KV cache with seeded N(0,1) instead of prefilling the prompt")
+    ap.add_argument("--batch", type=int, default=1, help="sequences per step (> 1: the batched step, not the headline)")
+    ap.add_argument("--ctx-lo", type=int, default=512)
+    ap.add_argument("--ctx-hi", type=int, default=4096)
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py: this build runs on exactly one GPU (asked for {a.gpus}); multi-GPU sharding is a design "
               f"note only", file=sys.stderr)
         sys.exit(2)
+    if a.batch > 1:
+        return main_batch(a)
 
     import numpy as np
     import torch

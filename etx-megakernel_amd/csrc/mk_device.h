@@ -31,8 +31,9 @@ constexpr int CHUNK = 64;               // attention positions per chunk (one la
 constexpr int HDIM = 128;               // head dim handled by the attention phase
 constexpr int MAX_H = 4096;
 constexpr int MAX_K = 12288;
-constexpr int MAX_CTX = 4096;
-constexpr int MAX_CHUNKS = MAX_CTX / CHUNK;
+constexpr int MAX_CTX = 8192;
+constexpr int MAX_CHUNKS = MAX_CTX / CHUNK;  // at most two per lane in the attention merge
+static_assert(MAX_CHUNKS <= 128, "the attention merge holds two chunks per lane");
 constexpr int MAX_G = 16;               // q heads per kv head
 constexpr int MAX_E = 256;
 constexpr int MAX_TOPK = 8;
@@ -95,7 +96,7 @@ struct AttnTiles {
   u32x4 vt[CHUNK / 8][2][CHUNK];        // V tile: [8-position group][dim half][dim in half], 16 bytes each
   alignas(16) float q[MAX_G][HDIM];     // roped q heads of the kv group
   float knew[HDIM], vnew[HDIM];         // this step's k (roped) and v of the kv group
-  float p[MAX_G][2 * CHUNK];            // exp(s - m_c) of the chunk per head; merge: chunk weights and sums
+  float p[MAX_G][2 * MAX_CHUNKS];       // exp(s - m_c) of the chunk per head; merge: chunk weights, then sums
   float m[MAX_G];
 };
 
@@ -753,8 +754,8 @@ __device__ __forceinline__ void phase_attn(const Params& p, int layer, S& s, Wai
     if (s.last) {
       for (int j = wave; j < G; j += NWAVE) {
         const float* part = apart + (size_t)(g * G + j) * MAX_CHUNKS * PART;
-        // lane cc holds chunk cc's (m, l); the chunk weights go through LDS for the ordered sums.  The first MB
-        // chunks' a[] are loaded together with (m, l) (they do not depend on the maximum): one memory round trip.
+        // lane cc holds chunks cc and cc + 64's (m, l); the chunk weights go through LDS for the ordered sums.  The
+        // first MB chunks' a[] are loaded together with (m, l) (they do not depend on the maximum): one round trip.
         constexpr int MB = 18;
         float av0[MB], av1[MB];
         auto load_a = [&](int c0) {
@@ -765,13 +766,18 @@ __device__ __forceinline__ void phase_attn(const Params& p, int layer, S& s, Wai
             av1[u] = ld_ag(part + (size_t)c * PART + lane + 64);
           }
         };
-        float mloc = -__builtin_huge_valf(), lloc = 0.0f;
+        float mloc = -__builtin_huge_valf(), lloc = 0.0f, mhi = -__builtin_huge_valf(), lhi = 0.0f;
         if (lane < nch) { mloc = ld_ag(part + (size_t)lane * PART + HD); lloc = ld_ag(part + (size_t)lane * PART + HD + 1); }
+        if (lane + 64 < nch) {
+          mhi = ld_ag(part + (size_t)(lane + 64) * PART + HD);
+          lhi = ld_ag(part + (size_t)(lane + 64) * PART + HD + 1);
+        }
         load_a(0);
-        const float M = wave_max(mloc);
-        const float w = lane < nch ? expf_mk(mloc - M) : 0.0f;
-        s.a.p[j][lane] = w;
-        s.a.p[j][64 + lane] = lloc;
+        const float M = wave_max(fmaxf(mloc, mhi));
+        s.a.p[j][lane] = lane < nch ? expf_mk(mloc - M) : 0.0f;
+        s.a.p[j][64 + lane] = lane + 64 < nch ? expf_mk(mhi - M) : 0.0f;
+        s.a.p[j][MAX_CHUNKS + lane] = lloc;
+        s.a.p[j][MAX_CHUNKS + 64 + lane] = lhi;
         float Ls = 0.0f, A0 = 0.0f, A1 = 0.0f;
         for (int c0 = 0; c0 < nch; c0 += MB) {
           if (c0 > 0) load_a(c0);
@@ -779,7 +785,7 @@ __device__ __forceinline__ void phase_attn(const Params& p, int layer, S& s, Wai
           for (int u = 0; u < MB; ++u)
             if (c0 + u < nch) {
               const float wc = s.a.p[j][c0 + u];
-              Ls = __builtin_fmaf(wc, s.a.p[j][64 + c0 + u], Ls);
+              Ls = __builtin_fmaf(wc, s.a.p[j][MAX_CHUNKS + c0 + u], Ls);
               A0 = __builtin_fmaf(wc, av0[u], A0);
               A1 = __builtin_fmaf(wc, av1[u], A1);
             }

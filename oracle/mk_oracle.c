@@ -256,7 +256,7 @@ static void attention_head(const float* q, const uint16_t* kc, const uint16_t* v
   float A[512], a[512];
   float L = 0.0f, M = -INFINITY;
   const int nch = (n + ATT_CHUNK - 1) / ATT_CHUNK;
-  float mc[4096];
+  float mc[256];                                                 /* chunks: n <= 16384 positions */
   for (int c = 0; c < nch; ++c) {
     const int t0 = c * ATT_CHUNK, t1 = t0 + ATT_CHUNK < n ? t0 + ATT_CHUNK : n;
     float m = -INFINITY;

@@ -69,6 +69,8 @@ def run_contexts(cfg, ctx, n_steps, shuffle=False, check_every=1, pool=True):
         dec.step_batch(pos, write_next=True)
         check = s % check_every == 0 or s == n_steps - 1
         d = dec.dumps() if check else None
+        if d is not None and B == 1:                        # single-sequence handles dump [layer][...]
+            d = {k: v[:, None] for k, v in d.items()}
         for b in range(B):
             if check:
                 t, xo, ido, wo = orc.step(toks[b][-1], int(pos[b]), dump=True, seq=b)
@@ -137,3 +139,10 @@ def test_qwen3_30b_a3b_batch4_full_depth(gpu):
     last step's per-layer residuals and routing bit for bit."""
     cfg = configs.with_layers(configs.QWEN3_30B_A3B, 48, batch=4)
     run_contexts(cfg, [600, 811, 1024, 700], n_steps=8, check_every=7, pool=False)
+
+
+@pytest.mark.parametrize("B", [1, 2], ids=["b1", "b2"])
+def test_tiny_contexts_past_4096(gpu, B):
+    """More than 64 chunks of 64 positions: the merge's second chunk per lane (contexts up to 8192)."""
+    cfg = configs.with_layers(configs.TINY_MOE, configs.TINY_MOE.L, batch=B, max_ctx=4700)
+    run_contexts(cfg, [4500, 4100][:B], n_steps=3, check_every=2)
