@@ -37,17 +37,23 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def mat_bytes(cfg, rows: int, cols: int) -> int:
+    """Algorithmic bytes of a rows x cols matrix of the model's weight type: bf16, or fp8 codes plus one fp32 scale
+    per row."""
+    return rows * (cols + 4) if cfg.wdtype else rows * cols * 2
+
+
 def bytes_per_token(cfg, context: int) -> dict:
     """Algorithmic HBM bytes of one decode step at `context` cached positions."""
     H, HD, NH, NKV, V = cfg.H, cfg.HD, cfg.NH, cfg.NKV, cfg.V
     bf = 2
     glob = (H + H + V * H) * bf                     # embedding row, final norm, lm_head
     layer = (2 * H + 2 * HD) * bf                   # ln1, ln2, q/k norm
-    layer += ((NH + 2 * NKV) * HD * H + H * NH * HD) * bf
+    layer += mat_bytes(cfg, (NH + 2 * NKV) * HD, H) + mat_bytes(cfg, H, NH * HD)
     if cfg.moe:
-        layer += (cfg.E * H + cfg.TOPK * 3 * cfg.MI * H) * bf
+        layer += cfg.E * H * bf + cfg.TOPK * (mat_bytes(cfg, 2 * cfg.MI, H) + mat_bytes(cfg, H, cfg.MI))
     else:
-        layer += 3 * cfg.I * H * bf
+        layer += mat_bytes(cfg, 2 * cfg.I, H) + mat_bytes(cfg, H, cfg.I)
     kv_pos = 2 * NKV * HD * bf
     kv = cfg.L * (context * kv_pos + kv_pos)
     weights = glob + cfg.L * layer
@@ -62,13 +68,13 @@ def bytes_per_step(cfg, contexts, union) -> dict:
     bf = 2
     B = len(contexts)
     glob = (B * H + H + V * H) * bf
-    layer = (2 * H + 2 * HD) * bf + ((NH + 2 * NKV) * HD * H + H * NH * HD) * bf
+    layer = (2 * H + 2 * HD) * bf + mat_bytes(cfg, (NH + 2 * NKV) * HD, H) + mat_bytes(cfg, H, NH * HD)
     experts = 0
     if cfg.moe:
         layer += cfg.E * H * bf
-        experts = sum(int(u) * 3 * cfg.MI * H * bf for u in union)
+        experts = sum(int(u) * (mat_bytes(cfg, 2 * cfg.MI, H) + mat_bytes(cfg, H, cfg.MI)) for u in union)
     else:
-        layer += 3 * cfg.I * H * bf
+        layer += mat_bytes(cfg, 2 * cfg.I, H) + mat_bytes(cfg, H, cfg.I)
     kv_pos = 2 * NKV * HD * bf
     kv = cfg.L * sum((int(c) + 1) * kv_pos for c in contexts)
     weights = glob + cfg.L * layer + experts
@@ -86,7 +92,9 @@ def main_batch(a):
     rng = np.random.default_rng(a.seed + 4)
     ctx = rng.integers(a.ctx_lo, a.ctx_hi + 1, B).astype(np.int32)
     max_ctx = int(ctx.max()) + a.warmup + a.steps + 2
-    cfg = configs.with_layers(configs.QWEN3_30B_A3B, configs.QWEN3_30B_A3B.L, batch=B, max_ctx=max_ctx)
+    cfg = configs.with_layers(configs.QWEN3_30B_A3B, configs.QWEN3_30B_A3B.L, batch=B, max_ctx=max_ctx,
+                              wdtype=N.W_FP8 if a.fp8 else N.W_BF16)
+    wname = "fp8 e4m3 (per-row scales; router, embedding, lm_head bf16)" if a.fp8 else "bf16"
     dev = torch.device("cuda:0")
     t0 = time.time()
     dec = N.Decoder(cfg, device="cuda:0", workgroups=a.workgroups)
@@ -133,10 +141,12 @@ def main_batch(a):
     out = {
         "metric": f"decode ms/step at batch {B}, Qwen3-30B-A3B shape; tokens/s; achieved HBM GB/s vs peak",
         "value": round(ms, 4), "unit": "ms/step", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
-        "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
-        "data": "synthetic: seeded random-init bf16 weights N(0,0.02); per-sequence KV of seeded N(0,1) values",
-        "config": {"workload": f"{cfg.name} decode, batch {B}, contexts uniform in [{a.ctx_lo}, {a.ctx_hi}], greedy "
-                               f"(BASELINE.json configs[4] shape with bf16 weights)",
+        "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp8-e4m3 weights x bf16 activations, fp32 accumulation" if a.fp8 else "bf16",
+        "data": f"synthetic: seeded random-init weights N(0,0.02) ({wname}); per-sequence KV of seeded N(0,1) values",
+        "config": {"workload": f"{cfg.name} decode, batch {B}, {wname} weights, contexts uniform in "
+                               f"[{a.ctx_lo}, {a.ctx_hi}], greedy"
+                               + (" (BASELINE.json configs[4])" if a.fp8 else " (configs[4] shape with bf16 weights)"),
                    "batch": B, "contexts": [int(c) for c in ctx], "layers": cfg.L, "experts": cfg.E,
                    "top_k": cfg.TOPK, "vocab": cfg.V, "mode": "fused megakernel", "seed": a.seed},
         "tokens_per_s": round(B * 1e3 / ms, 2), "ms_per_token": round(ms / B, 4),
@@ -234,6 +244,7 @@ def main():
     ap.add_argument("--batch", type=int, default=1, help="sequences per step (> 1: the batched step, not the headline)")
     ap.add_argument("--ctx-lo", type=int, default=512)
     ap.add_argument("--ctx-hi", type=int, default=4096)
+    ap.add_argument("--fp8", action="store_true", help="fp8 e4m3 weights with per-row scales (BASELINE.json configs[4])")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py: this build runs on exactly one GPU (asked for {a.gpus}); multi-GPU sharding is a design "
@@ -248,6 +259,8 @@ def main():
     from etx.models import configs
 
     cfg = configs.QWEN3_30B_A3B
+    if a.fp8:
+        cfg = configs.with_layers(cfg, cfg.L, wdtype=N.W_FP8)
     if a.ctx + a.warmup + a.steps + 1 > cfg.max_ctx:
         raise SystemExit(f"ctx {a.ctx} + warmup + steps exceeds max_ctx {cfg.max_ctx}")
     dev = torch.device("cuda:0")
@@ -318,8 +331,9 @@ def main():
     out = {
         "metric": METRIC, "value": round(ms, 4), "unit": "ms/token", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
         "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic: seeded random-init bf16 weights N(0,0.02); " + ("KV cache of seeded N(0,1) values"
+        "dtype": "fp8-e4m3 weights x bf16 activations, fp32 accumulation" if a.fp8 else "bf16",
+        "data": "synthetic: seeded random-init " + ("fp8 (quantised from bf16 N(0,0.02))" if a.fp8 else "bf16")
+                + " weights N(0,0.02); " + ("KV cache of seeded N(0,1) values"
                 if a.kv_fill else "prompt of seeded uniform token ids prefilled token by token"),
         "config": {"workload": f"{cfg.name} decode, batch 1, context {a.ctx} (+{a.warmup} warmup), greedy "
                                f"(BASELINE.json configs[2])",

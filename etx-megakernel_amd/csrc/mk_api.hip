@@ -14,6 +14,27 @@
 
 #include "etxmk.h"
 #include "mk_batch.h"
+#include "mk_init.h"
+
+namespace mk {
+// the persistent kernels live in their own translation units (mk_fused_*.hip, mk_batch_*.hip)
+MK_FUSED_SHAPES_BF16(MK_FUSED_DECL)
+MK_FUSED_SHAPES_FP8(MK_FUSED_DECL)
+MK_BATCH_SHAPES_BF16(MK_BATCH_DECL)
+MK_BATCH_SHAPES_FP8(MK_BATCH_DECL)
+
+// unfused mode (bf16 weights)
+MK_PHASE_KERNEL(etxmk_p_qkv, phase_qkv_any(p, layer, s, NoWait{}))
+MK_PHASE_KERNEL(etxmk_p_attn, phase_attn<1>(p, layer, s, NoWait{}))
+MK_PHASE_KERNEL(etxmk_p_oproj, phase_oproj_any(p, layer, s, NoWait{}))
+MK_PHASE_KERNEL(etxmk_p_router, phase_router_any(p, layer, s, NoWait{}))
+MK_PHASE_KERNEL(etxmk_p_expert_up, phase_expert_up_any(p, layer, s, NoWait{}))
+MK_PHASE_KERNEL(etxmk_p_expert_down, phase_expert_down_any(p, layer, s, NoWait{}))
+MK_PHASE_KERNEL(etxmk_p_gateup, phase_gateup_any(p, layer, s, NoWait{}))
+MK_PHASE_KERNEL(etxmk_p_down, phase_down_any(p, layer, s, NoWait{}))
+MK_PHASE_KERNEL(etxmk_p_head, phase_head_any(p, s, NoWait{}))
+MK_PHASE_KERNEL(etxmk_p_token, phase_token(p, NoWait{}))
+}  // namespace mk
 
 using namespace mk;
 
@@ -42,8 +63,17 @@ struct TensorSlot {
   int kind, layer;
   int count;                 // tensors of this shape back to back (experts)
   int rows, cols, perm;      // perm: rows stored lane-permuted
+  int fp8;                   // rows in Fp8Row format (codes + scale, cols + 16 bytes) instead of bf16
   uint64_t off;              // byte offset of tensor 0
+  uint64_t row_bytes() const { return fp8 ? (uint64_t)cols + 16 : 2ull * cols; }
+  uint64_t tensor_bytes() const { return (uint64_t)rows * row_bytes(); }
 };
+
+// the matrices held as fp8 when the weight type is ETXMK_W_FP8
+bool fp8_kind(int kind) {
+  return kind == ETXMK_T_WQKV || kind == ETXMK_T_WO || kind == ETXMK_T_W13 || kind == ETXMK_T_W2 ||
+         kind == ETXMK_T_WGU || kind == ETXMK_T_WD;
+}
 
 inline uint64_t stream_id(int kind, int layer, int expert) {
   return ((uint64_t)kind << 48) | ((uint64_t)(layer + 1) << 24) | (uint64_t)expert;
@@ -56,18 +86,33 @@ bool k_in(int k, std::initializer_list<int> ks) {
   return false;
 }
 
-// the batched persistent kernel for this shape with the smallest batch capacity that holds c.batch, or nullptr
+// the single-sequence persistent kernel instantiated for this shape and weight type, or nullptr
+const void* fused_kernel(const etxmk_config& c) {
+  const int km = c.moe ? c.MI : c.I;
+#define MK_PICK(name, h_, ka_, km_, moe_, e_, fp8_)                                                               \
+  if (c.H == h_ && c.NH * c.HD == ka_ && km == km_ && (c.moe != 0) == moe_ && (!moe_ || c.E == e_) &&            \
+      (c.wdtype == ETXMK_W_FP8) == fp8_)                                                                          \
+    return (const void*)name;
+  MK_FUSED_SHAPES_BF16(MK_PICK)
+  MK_FUSED_SHAPES_FP8(MK_PICK)
+#undef MK_PICK
+  return nullptr;
+}
+
+// the batched persistent kernel for this shape and weight type with the smallest batch capacity that holds
+// c.batch, or nullptr
 const void* batch_kernel(const etxmk_config& c) {
   const int km = c.moe ? c.MI : c.I;
   const void* best = nullptr;
   int cap = 0;
-#define MK_PICK_B(name, h_, ka_, km_, moe_, e_, b_)                                                             \
-  if (c.H == h_ && c.NH * c.HD == ka_ && km == km_ && (c.moe != 0) == moe_ && (!moe_ || c.E == e_) && c.batch <= b_ && \
-      (!best || b_ < cap)) {                                                                                      \
+#define MK_PICK_B(name, h_, ka_, km_, moe_, e_, fp8_, b_)                                                         \
+  if (c.H == h_ && c.NH * c.HD == ka_ && km == km_ && (c.moe != 0) == moe_ && (!moe_ || c.E == e_) &&            \
+      (c.wdtype == ETXMK_W_FP8) == fp8_ && c.batch <= b_ && (!best || b_ < cap)) {                                \
     best = (const void*)name;                                                                                     \
     cap = b_;                                                                                                     \
   }
-  MK_BATCH_SHAPES(MK_PICK_B)
+  MK_BATCH_SHAPES_BF16(MK_PICK_B)
+  MK_BATCH_SHAPES_FP8(MK_PICK_B)
 #undef MK_PICK_B
   return best;
 }
@@ -90,6 +135,10 @@ int check_config(const etxmk_config* c) {
   } else {
     if (!k_in(c->I, {MK_K_INTER}) || c->I > MAX_K) return fail(ETXMK_EINVAL, "intermediate %d unsupported", c->I);
   }
+  if (c->wdtype != ETXMK_W_BF16 && c->wdtype != ETXMK_W_FP8) return fail(ETXMK_EINVAL, "weight type %d unknown", c->wdtype);
+  if (c->wdtype == ETXMK_W_FP8 && c->batch == 1 && !fused_kernel(*c))
+    return fail(ETXMK_EINVAL, "no fp8 persistent kernel for H %d, NH*HD %d, %s %d (fp8 runs fused only)", c->H,
+                c->NH * c->HD, c->moe ? "MI" : "I", c->moe ? c->MI : c->I);
   if (c->batch > 1 && !batch_kernel(*c))
     return fail(ETXMK_EINVAL, "no batched persistent kernel for batch %d, H %d, NH*HD %d, %s %d", c->batch, c->H,
                 c->NH * c->HD, c->moe ? "MI" : "I", c->moe ? c->MI : c->I);
@@ -101,8 +150,9 @@ std::vector<TensorSlot> weight_layout(const etxmk_config* c, uint64_t* total) {
   std::vector<TensorSlot> v;
   uint64_t off = 0;
   auto add = [&](int kind, int layer, int count, int rows, int cols, int perm) {
-    v.push_back({kind, layer, count, rows, cols, perm, off});
-    off = align_up(off + (uint64_t)count * rows * cols * 2);
+    TensorSlot t{kind, layer, count, rows, cols, perm, c->wdtype == ETXMK_W_FP8 && fp8_kind(kind) ? 1 : 0, off};
+    v.push_back(t);
+    off = align_up(off + (uint64_t)count * t.tensor_bytes());
   };
   const int NQKV = (c->NH + 2 * c->NKV) * c->HD;
   add(ETXMK_T_EMBED, -1, 1, c->V, c->H, 0);
@@ -196,9 +246,9 @@ struct etxmk_handle {
     return nullptr;
   }
   template <class T> T* wsptr(uint64_t off) const { return (T*)(wsp + off); }
-  const uint16_t* wt(int kind, int layer) const {
+  const uint8_t* wt(int kind, int layer) const {
     const TensorSlot* s = slot(kind, layer);
-    return s ? (const uint16_t*)(w + s->off) : nullptr;
+    return s ? (const uint8_t*)(w + s->off) : nullptr;
   }
   int barriers(int l0, int l1, int head) const { return (c.moe ? 6 : 5) * (l1 - l0) + (head ? 1 : 0); }
 };
@@ -264,10 +314,10 @@ int etxmk_bind(etxmk_handle* h, void* weights, void* kv, void* workspace) {
   const uint64_t kvl = kv_layer_elems(&c);
   for (int l = 0; l < c.L; ++l) {
     LayerW& y = lw[l];
-    y.ln1 = h->wt(ETXMK_T_LN1, l);
-    y.ln2 = h->wt(ETXMK_T_LN2, l);
-    y.qn = h->wt(ETXMK_T_QNORM, l);
-    y.kn = h->wt(ETXMK_T_KNORM, l);
+    y.ln1 = (const uint16_t*)h->wt(ETXMK_T_LN1, l);
+    y.ln2 = (const uint16_t*)h->wt(ETXMK_T_LN2, l);
+    y.qn = (const uint16_t*)h->wt(ETXMK_T_QNORM, l);
+    y.kn = (const uint16_t*)h->wt(ETXMK_T_KNORM, l);
     y.wqkv = h->wt(ETXMK_T_WQKV, l);
     y.wo = h->wt(ETXMK_T_WO, l);
     y.wr = h->wt(ETXMK_T_ROUTER, l);
@@ -315,10 +365,30 @@ int etxmk_tensor_info(etxmk_handle* h, int kind, int layer, int expert, uint64_t
   const TensorSlot* s = h->slot(kind, global ? -1 : layer);
   if (!s) return fail(ETXMK_EINVAL, "no tensor kind %d layer %d", kind, layer);
   if (expert < 0 || expert >= s->count) return fail(ETXMK_EINVAL, "expert %d outside 0..%d", expert, s->count - 1);
-  if (offset) *offset = s->off + (uint64_t)expert * s->rows * s->cols * 2;
+  if (offset) *offset = s->off + (uint64_t)expert * s->tensor_bytes();
   if (rows) *rows = s->rows;
   if (cols) *cols = s->cols;
   if (permuted) *permuted = s->perm;
+  return ETXMK_OK;
+}
+
+int etxmk_tensor_format(etxmk_handle* h, int kind, int layer, int32_t* wdtype, uint64_t* row_bytes) {
+  if (!h) return fail(ETXMK_EINVAL, "NULL handle");
+  const bool global = kind == ETXMK_T_EMBED || kind == ETXMK_T_LMHEAD || kind == ETXMK_T_FINAL_NORM;
+  const TensorSlot* s = h->slot(kind, global ? -1 : layer);
+  if (!s) return fail(ETXMK_EINVAL, "no tensor kind %d layer %d", kind, layer);
+  if (wdtype) *wdtype = s->fp8 ? ETXMK_W_FP8 : ETXMK_W_BF16;
+  if (row_bytes) *row_bytes = s->row_bytes();
+  return ETXMK_OK;
+}
+
+// fp8 rows of n_t tensors (rows x cols) at dst, from the seeded generator (src null) or natural bf16 rows
+static int quantize(uint8_t* dst, const uint16_t* src, uint64_t seed, uint64_t sid0, int n_t, int rows, int cols,
+                    float scale, hipStream_t st) {
+  const size_t nrows = (size_t)n_t * rows, blocks = (nrows + 3) / 4;   // 4 waves per block, one row each
+  hipLaunchKernelGGL(etxmk_quant_rows, dim3((unsigned)(blocks < 65536 ? blocks : 65536)), dim3(256), 0, st, dst, src,
+                     seed, sid0, n_t, rows, cols, scale);
+  HIPCHK(hipGetLastError());
   return ETXMK_OK;
 }
 
@@ -329,6 +399,11 @@ int etxmk_init_weights_seeded(etxmk_handle* h, uint64_t seed, float scale, void*
     uint16_t* dst = (uint16_t*)(h->w + s.off);
     const size_t n = (size_t)s.count * s.rows * s.cols;
     const bool norm = s.kind >= ETXMK_T_LN1;
+    if (s.fp8) {
+      if (int r = quantize(h->w + s.off, nullptr, seed, stream_id(s.kind, s.layer, 0), s.count, s.rows, s.cols, scale, st))
+        return r;
+      continue;
+    }
     if (norm) {
       hipLaunchKernelGGL(etxmk_fill_u16, dim3(64), dim3(256), 0, st, dst, n, (uint16_t)0x3F80);
     } else {
@@ -349,6 +424,8 @@ int etxmk_load_tensor(etxmk_handle* h, int kind, int layer, int expert, const vo
   if (int r = etxmk_tensor_info(h, kind, layer, expert, &off, &rows, &cols, &perm)) return r;
   if (!src) return fail(ETXMK_EINVAL, "src is NULL");
   hipStream_t st = (hipStream_t)stream;
+  const bool global = kind == ETXMK_T_EMBED || kind == ETXMK_T_LMHEAD || kind == ETXMK_T_FINAL_NORM;
+  if (h->slot(kind, global ? -1 : layer)->fp8) return quantize(h->w + off, (const uint16_t*)src, 0, 0, 1, rows, cols, 0.0f, st);
   if (perm) {
     const size_t n = (size_t)rows * cols;
     hipLaunchKernelGGL(etxmk_pack_rows, dim3((unsigned)((n + 255) / 256 < 65536 ? (n + 255) / 256 : 65536)), dim3(256), 0, st,
@@ -493,17 +570,6 @@ int etxmk_barriers_per_step(etxmk_handle* h, int32_t* n) {
   return ETXMK_OK;
 }
 
-// the persistent kernel instantiated for this shape, or nullptr
-static const void* fused_kernel(const etxmk_config& c) {
-  const int km = c.moe ? c.MI : c.I;
-#define MK_PICK(name, h_, ka_, km_, moe_, e_) \
-  if (c.H == h_ && c.NH * c.HD == ka_ && km == km_ && (c.moe != 0) == moe_ && (!moe_ || c.E == e_)) return (const void*)name;
-  MK_FUSED_SHAPES(MK_PICK)
-#undef MK_PICK
-  return nullptr;
-}
-
-// One step: single-sequence handles take `pos`; batched handles take one position per sequence (posv[batch]).
 static int launch(etxmk_handle* h, const int32_t* posv, int pos, int write_next, int l0, int l1, int embed, int head,
                   hipStream_t st) {
   if (!h || !h->wsp) return fail(ETXMK_EUNBOUND, "handle not bound");
@@ -518,6 +584,7 @@ static int launch(etxmk_handle* h, const int32_t* posv, int pos, int write_next,
   if (l0 < 0 || l1 > c.L || l0 >= l1) return fail(ETXMK_EINVAL, "layer range [%d, %d) outside [0, %d)", l0, l1, c.L);
   const int need = 8;                       // the grid barrier spreads arrivals over 8 groups
   if (h->nwg < need) return fail(ETXMK_EINVAL, "grid of %d workgroups is below the %d the grid barrier needs", h->nwg, need);
+  if (!h->fused && c.wdtype == ETXMK_W_FP8) return fail(ETXMK_EINVAL, "fp8 weights run the persistent kernel only");
   if (batched) {
     if (!h->fused) return fail(ETXMK_EINVAL, "batched handles run the persistent kernel only");
     if (!embed || !head) return fail(ETXMK_EINVAL, "batched handles run whole steps");
@@ -531,9 +598,9 @@ static int launch(etxmk_handle* h, const int32_t* posv, int pos, int write_next,
   p.nblocks = nblocks_of(&c);
   p.eps = c.eps;
   p.attn_scale = (float)(1.0 / sqrt((double)c.HD));
-  p.embed = h->wt(ETXMK_T_EMBED, -1);
-  p.lm_head = h->wt(ETXMK_T_LMHEAD, -1);
-  p.final_norm = h->wt(ETXMK_T_FINAL_NORM, -1);
+  p.embed = (const uint16_t*)h->wt(ETXMK_T_EMBED, -1);
+  p.lm_head = (const uint16_t*)h->wt(ETXMK_T_LMHEAD, -1);
+  p.final_norm = (const uint16_t*)h->wt(ETXMK_T_FINAL_NORM, -1);
   p.layers = h->wsptr<const LayerW>(h->ws.layers);
   p.rope_cos = h->wsptr<const float>(h->ws.rcos);
   p.rope_sin = h->wsptr<const float>(h->ws.rsin);
@@ -557,7 +624,8 @@ static int launch(etxmk_handle* h, const int32_t* posv, int pos, int write_next,
   p.spin_ticks = 200000000ull;            // 2 s of the 100 MHz s_memrealtime clock
   {                                        // QKV rows staged in LDS a layer ahead when a workgroup's share fits
     const int rows = (c.NH + 2 * c.NKV) * c.HD, R = (rows + h->nwg - 1) / h->nwg;
-    p.qkv_rows = (!batched && h->fused && c.H % 512 == 0 && (uint64_t)R * c.H * 2 <= (uint64_t)QKVW_BYTES) ? R : 0;
+    p.qkv_rows = (!batched && h->fused && c.wdtype == ETXMK_W_BF16 && c.H % 512 == 0 &&
+                  (uint64_t)R * c.H * 2 <= (uint64_t)QKVW_BYTES) ? R : 0;
   }
   p.B = c.batch;
   p.nbps = nbps_of(&c);

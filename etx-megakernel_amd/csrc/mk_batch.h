@@ -189,24 +189,25 @@ __device__ __forceinline__ void dot_rows_b(const RowRegs<K> (&r)[NR], XP xp, int
 // B x NR dots, which covers the latency of the next group's loads).  The first group is issued before `prologue`
 // (which waits for the inputs).  nvec(g) is the number of input rows of group g, xvec(g, b) the LDS address of
 // its b-th; epi(g, nv, v) consumes v[NR][B].
-template <int K, int NR, int B, class RowF, class NVF, class XF, class EpiF, class Pro>
+template <class WR, int NR, int B, class RowF, class NVF, class XF, class EpiF, class Pro>
 __device__ __forceinline__ bool gemv_run_b(int ngroups, RowF rowf, NVF nvec, XF xvec, EpiF epi, Pro prologue, int nwg,
                                            uint64_t* trace, int s_phase) {
-  static_assert(KS<K>::KB <= 16, "batched GEMV rows are at most 8192 long");
+  static_assert(!WR::LONG, "batched GEMV rows are at most 8192 long");
+  using Regs = typename WR::Regs;
   const int lane = lane_id();
   const int gw = blockIdx.x * NWAVE + wave_u(), nw = nwg * NWAVE;
-  RowRegs<K> RA[NR], RB[NR];
-  auto issue = [&](RowRegs<K>(&R)[NR], int g) {
+  Regs RA[NR], RB[NR];
+  auto issue = [&](Regs(&R)[NR], int g) {
 #pragma unroll
     for (int i = 0; i < NR; ++i) {
-      const uint16_t* rp = rowf(g, i);
-      if (rp) load_row<K>(R[i], rp, lane);
+      const uint8_t* rp = rowf(g, i);
+      if (rp) WR::load(R[i], rp, lane);
     }
   };
-  auto compute = [&](const RowRegs<K>(&R)[NR], int g) {
+  auto compute = [&](const Regs(&R)[NR], int g) {
     const int nv = nvec(g);
     float v[NR][B];
-    dot_rows_b<K, NR, B>(R, [&](int b) { return xvec(g, b); }, nv, lane, v);
+    dot_rows_any<WR, NR, B>(R, [&](int b) { return xvec(g, b); }, nv, lane, v);
     epi(g, nv, v);
   };
   int g = gw;
@@ -227,6 +228,46 @@ __device__ __forceinline__ bool gemv_run_b(int ngroups, RowF rowf, NVF nvec, XF 
   return true;
 }
 
+// fp8 rows (Fp8Row) dotted with up to B input rows: each block's codes are decoded once and used for every input;
+// per (row, input) the order is dot_row8's, then wave_sum and the row's scale
+template <int K, int NR, int B, class XP>
+__device__ __forceinline__ void dot_rows_b8(const RowRegs8<K> (&r)[NR], XP xp, int nv, int lane, float (&v)[NR][B]) {
+  constexpr int NB = KS8<K>::KB + (KS8<K>::T > 0 ? 1 : 0);
+  float acc[NR][B];
+#pragma unroll
+  for (int i = 0; i < NR; ++i)
+#pragma unroll
+    for (int b = 0; b < B; ++b) acc[i][b] = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NB; ++j) {
+    const int n = j < KS8<K>::KB ? 16 : KS8<K>::TM;
+    float wv[NR][16];
+#pragma unroll
+    for (int i = 0; i < NR; ++i) w_of_fp8_block<K>(r[i], j, wv[i]);
+#pragma unroll
+    for (int b = 0; b < B; ++b)
+      if (b < nv) {
+        float xv[16];
+        x_of_fp8_block<K>(xp(b), j, lane, xv);
+#pragma unroll
+        for (int i = 0; i < NR; ++i)
+#pragma unroll
+          for (int e = 0; e < 16; ++e)
+            if (e < n) acc[i][b] = __builtin_fmaf(wv[i][e], xv[e], acc[i][b]);
+      }
+  }
+#pragma unroll
+  for (int i = 0; i < NR; ++i)
+#pragma unroll
+    for (int b = 0; b < B; ++b) v[i][b] = b < nv ? wave_sum(acc[i][b]) * r[i].sc : 0.0f;
+}
+
+template <class WR, int NR, int B, class XP>
+__device__ __forceinline__ void dot_rows_any(const typename WR::Regs (&r)[NR], XP xp, int nv, int lane, float (&v)[NR][B]) {
+  if constexpr (WR::FP8) dot_rows_b8<WR::K, NR, B>(r, xp, nv, lane, v);
+  else dot_rows_b<WR::K, NR, B>(r, xp, nv, lane, v);
+}
+
 // store NR x B values: lane i*B + b stores (i, b) for b < nv
 template <int NR, int B, class F>
 __device__ __forceinline__ void lane_store_b(const float (&v)[NR][B], int nv, F f) {
@@ -240,15 +281,16 @@ __device__ __forceinline__ void lane_store_b(const float (&v)[NR][B], int nv, F 
 
 // ---------------------------------------------------------------- phases (batched)
 // P1: input RMSNorm + QKV GEMV per sequence (ref_numpy.py:111-115)
-template <int KK, int B, class S, class Wait>
+template <class WR, int B, class S, class Wait>
 __device__ __forceinline__ void phase_qkv_b(const Params& p, int layer, S& s, Wait wait) {
+  constexpr int KK = WR::K;
   const LayerW Lw = layer_w(p, layer);
   const bool first = layer == p.l0 && p.do_embed;
   const int rows = (p.NH + 2 * p.NKV) * p.HD, nb = p.B;
-  const uint16_t* W = Lw.wqkv;
-  gemv_run_b<KK, 2, B>(
+  const uint8_t* W = Lw.wqkv;
+  gemv_run_b<WR, 2, B>(
       (rows + 1) / 2,
-      [&](int g, int i) -> const uint16_t* { const int r = 2 * g + i; return r < rows ? W + (size_t)r * KK : nullptr; },
+      [&](int g, int i) -> const uint8_t* { const int r = 2 * g + i; return r < rows ? mrow<WR>(W, r) : nullptr; },
       [&](int) { return nb; }, [&](int, int b) { return (const uint16_t*)(s.n.xs + b * KK); },
       [&](int g, int nv, const float(&v)[2][B]) {
         lane_store_b<2, B>(v, nv, [&](int i, int b, float val) {
@@ -272,15 +314,16 @@ __device__ __forceinline__ void phase_qkv_b(const Params& p, int layer, S& s, Wa
 }
 
 // P3: O projection + residual per sequence (ref_numpy.py:130)
-template <int KK, int B, class S, class Wait>
+template <class WR, int B, class S, class Wait>
 __device__ __forceinline__ void phase_oproj_b(const Params& p, int layer, S& s, Wait wait) {
+  constexpr int KK = WR::K;
   static_assert(B * KK <= S::XCAP, "attention rows exceed the LDS budget");
   const LayerW Lw = layer_w(p, layer);
   const int H = p.H, nb = p.B, nw = p.nwg * NWAVE;
   const bool first = layer == p.l0 && p.do_embed;
-  const uint16_t* W = Lw.wo;
-  gemv_run_b<KK, 1, B>(
-      H, [&](int g, int) -> const uint16_t* { return W + (size_t)g * KK; }, [&](int) { return nb; },
+  const uint8_t* W = Lw.wo;
+  gemv_run_b<WR, 1, B>(
+      H, [&](int g, int) -> const uint8_t* { return mrow<WR>(W, g); }, [&](int) { return nb; },
       [&](int, int b) { return (const uint16_t*)(s.v.xs + b * KK); },
       [&](int g, int nv, const float(&v)[1][B]) {
         const int r = res_slot(g, nw);
@@ -302,11 +345,12 @@ __device__ __forceinline__ void phase_oproj_b(const Params& p, int layer, S& s, 
 // P4: post-attention RMSNorm + router GEMV per sequence (ref_numpy.py:131-134)
 template <int KK, int B, class S, class Wait>
 __device__ __forceinline__ void phase_router_b(const Params& p, int layer, S& s, Wait wait) {
+  using WR = Bf16Row<KK>;                                 // the router stays bf16 in every weight type
   const LayerW Lw = layer_w(p, layer);
   const int E = p.E, nb = p.B;
-  const uint16_t* W = Lw.wr;
-  gemv_run_b<KK, 1, B>(
-      E, [&](int g, int) -> const uint16_t* { return W + (size_t)g * KK; }, [&](int) { return nb; },
+  const uint8_t* W = Lw.wr;
+  gemv_run_b<WR, 1, B>(
+      E, [&](int g, int) -> const uint8_t* { return mrow<WR>(W, g); }, [&](int) { return nb; },
       [&](int, int b) { return (const uint16_t*)(s.n.xs + b * KK); },
       [&](int g, int nv, const float(&v)[1][B]) {
         lane_store_b<1, B>(v, nv, [&](int, int b, float val) { st_ag(p.logits + (size_t)b * E + g, bfr(val)); });
@@ -364,11 +408,12 @@ __device__ __forceinline__ void route_all(const Params& p, S& s) {
 
 // P5: routing, then each distinct expert's gate/up rows against the normed rows of the sequences routed to it,
 // SiLU*up into that pair's h16 row (ref_numpy.py:135-145)
-template <int KK, int B, int EC, class S, class Wait>
+template <class WR, int B, int EC, class S, class Wait>
 __device__ __forceinline__ void phase_expert_up_b(const Params& p, int layer, S& s, Wait wait) {
+  constexpr int KK = WR::K;
   const LayerW Lw = layer_w(p, layer);
   const int MI = p.MI, KT = p.TOPK, nb = p.B;
-  const uint16_t* W = Lw.w13;
+  const uint8_t* W = Lw.w13;
   build_norm_xb<KK, B>(p, false, Lw.ln2, s);              // x is final since the O projection
   if (!wait()) return;
   route_all<B, EC>(p, s);
@@ -382,11 +427,11 @@ __device__ __forceinline__ void phase_expert_up_b(const Params& p, int layer, S&
       for (int t = threadIdx.x; t < nb * p.E; t += NT) st_f(p.dump_logits + (size_t)layer * nb * p.E + t, ld_ag(p.logits + t));
   }
   const int U = s.nexp;
-  gemv_run_b<KK, 2, B>(
+  gemv_run_b<WR, 2, B>(
       U * MI,
-      [&](int g, int i) -> const uint16_t* {
+      [&](int g, int i) -> const uint8_t* {
         const int u = g / MI, j = g - u * MI;
-        return W + ((size_t)s.uexp[u] * 2 * MI + 2 * j + i) * KK;
+        return mrow<WR>(W, (size_t)s.uexp[u] * 2 * MI + 2 * j + i);
       },
       [&](int g) { const int u = g / MI; return s.ustart[u + 1] - s.ustart[u]; },
       [&](int g, int b) { return (const uint16_t*)(s.n.xs + s.pseq[s.ustart[g / MI] + b] * KK); },
@@ -405,22 +450,24 @@ __device__ __forceinline__ void phase_expert_up_b(const Params& p, int layer, S&
 // Each wave owns output rows; for its row it streams the rows of every distinct expert (D at a time, the next
 // batch in flight while the current one is reduced) and dots each with the h rows of that expert's pairs.  The
 // pairs' h rows are staged in LDS in passes of whole experts that fit; lane b carries sequence b's combine chain.
-template <int KK, int B, class S, class Wait>
+template <class WR, int B, class S, class Wait>
 __device__ __forceinline__ void phase_expert_down_b(const Params& p, int layer, S& s, Wait wait) {
+  constexpr int KK = WR::K;
   constexpr int PCAP = S::XCAP / KK;                      // pairs per pass
   static_assert(PCAP >= MAX_B, "one expert's pairs must fit a pass");
-  constexpr int DE = KS<KK>::REGS <= 6 ? 8 : KS<KK>::REGS <= 12 ? 4 : 2;
+  constexpr int DE = WR::REGS <= 7 ? 8 : WR::REGS <= 13 ? 4 : 2;
+  using Regs = typename WR::Regs;
   const LayerW Lw = layer_w(p, layer);
   const int H = p.H, nb = p.B, nw = p.nwg * NWAVE, lane = lane_id();
   const int gw = blockIdx.x * NWAVE + wave_u();
   const int U = s.nexp;                                   // routing kept from P5
-  const uint16_t* W = Lw.w2;
+  const uint8_t* W = Lw.w2;
   const int nrw = gw < H ? (H - 1 - gw) / nw + 1 : 0;    // output rows of this wave
-  RowRegs<KK> R[2][DE];
-  auto issue = [&](RowRegs<KK>(&Rb)[DE], int g, int ub, int u1) {
+  Regs R[2][DE];
+  auto issue = [&](Regs(&Rb)[DE], int g, int ub, int u1) {
 #pragma unroll
     for (int d = 0; d < DE; ++d)
-      if (ub + d < u1) load_row<KK>(Rb[d], W + ((size_t)s.uexp[ub + d] * H + g) * KK, lane);
+      if (ub + d < u1) WR::load(Rb[d], mrow<WR>(W, (size_t)s.uexp[ub + d] * H + g), lane);
   };
   int u0 = 0, u1 = 0;
   auto pass_end = [&](int a) {
@@ -444,14 +491,14 @@ __device__ __forceinline__ void phase_expert_down_b(const Params& p, int layer, 
     __syncthreads();
     const bool last_pass = u1 >= U;
     float acc = 0.0f;
-    auto compute = [&](RowRegs<KK>(&Rb)[DE], int t) {
+    auto compute = [&](Regs(&Rb)[DE], int t) {
       const int g = gw + (t / nbt) * nw, ub = u0 + (t % nbt) * DE, r = res_slot(g, nw);
       if (t % nbt == 0) acc = (!first_pass && lane < nb) ? s.v.acc[lane][r] : 0.0f;
 #pragma unroll
       for (int d = 0; d < DE; ++d)
         if (ub + d < u1)
           for (int pp = s.ustart[ub + d]; pp < s.ustart[ub + d + 1]; ++pp) {
-            const float y = bfr(bfr(dot_row<KK>(Rb[d], s.v.xs + (pp - p0) * KK, lane)) * s.pw[pp]);
+            const float y = bfr(bfr(WR::dot(Rb[d], s.v.xs + (pp - p0) * KK, lane)) * s.pw[pp]);
             if (lane == s.pseq[pp]) acc = bfr(acc + y);
           }
       if (t % nbt == nbt - 1 && lane < nb) {
@@ -478,13 +525,14 @@ __device__ __forceinline__ void phase_expert_down_b(const Params& p, int layer, 
 }
 
 // dense MLP (ref_numpy.py:149-152): gate/up + SiLU*up per sequence into h16, then down + residual
-template <int KK, int B, class S, class Wait>
+template <class WR, int B, class S, class Wait>
 __device__ __forceinline__ void phase_gateup_b(const Params& p, int layer, S& s, Wait wait) {
+  constexpr int KK = WR::K;
   const LayerW Lw = layer_w(p, layer);
   const int I = p.I, nb = p.B;
-  const uint16_t* W = Lw.wgu;
-  gemv_run_b<KK, 2, B>(
-      I, [&](int g, int i) -> const uint16_t* { return W + ((size_t)2 * g + i) * KK; }, [&](int) { return nb; },
+  const uint8_t* W = Lw.wgu;
+  gemv_run_b<WR, 2, B>(
+      I, [&](int g, int i) -> const uint8_t* { return mrow<WR>(W, (size_t)2 * g + i); }, [&](int) { return nb; },
       [&](int, int b) { return (const uint16_t*)(s.n.xs + b * KK); },
       [&](int g, int nv, const float(&v)[2][B]) {
         const int lane = lane_id();
@@ -501,14 +549,15 @@ __device__ __forceinline__ void phase_gateup_b(const Params& p, int layer, S& s,
       p.nwg, p.trace, s.phase);
 }
 
-template <int KK, int B, class S, class Wait>
+template <class WR, int B, class S, class Wait>
 __device__ __forceinline__ void phase_down_b(const Params& p, int layer, S& s, Wait wait) {
+  constexpr int KK = WR::K;
   static_assert(B * KK <= S::XCAP, "intermediate rows exceed the LDS budget");
   const LayerW Lw = layer_w(p, layer);
   const int H = p.H, nb = p.B, nw = p.nwg * NWAVE;
-  const uint16_t* W = Lw.wd;
-  gemv_run_b<KK, 1, B>(
-      H, [&](int g, int) -> const uint16_t* { return W + (size_t)g * KK; }, [&](int) { return nb; },
+  const uint8_t* W = Lw.wd;
+  gemv_run_b<WR, 1, B>(
+      H, [&](int g, int) -> const uint8_t* { return mrow<WR>(W, g); }, [&](int) { return nb; },
       [&](int, int b) { return (const uint16_t*)(s.v.xs + b * KK); },
       [&](int g, int nv, const float(&v)[1][B]) {
         const int r = res_slot(g, nw);
@@ -530,14 +579,15 @@ __device__ __forceinline__ void phase_down_b(const Params& p, int layer, S& s, W
 // P7: final norm + lm_head + greedy argmax per sequence (ref_numpy.py:155-158; vl_tiles.hip:45-89)
 template <int KK, int B, class S, class Wait>
 __device__ __forceinline__ void phase_head_b(const Params& p, S& s, Wait wait) {
+  using WR = Bf16Row<KK>;                                 // lm_head stays bf16 in every weight type
   const int V = p.V, nb = p.B;
-  const uint16_t* W = p.lm_head;
+  const uint8_t* W = (const uint8_t*)p.lm_head;
   uint64_t best[B];
 #pragma unroll
   for (int b = 0; b < B; ++b) best[b] = 0;
-  const bool ran = gemv_run_b<KK, 2, B>(
+  const bool ran = gemv_run_b<WR, 2, B>(
       (V + 1) / 2,
-      [&](int g, int i) -> const uint16_t* { const int r = 2 * g + i; return r < V ? W + (size_t)r * KK : nullptr; },
+      [&](int g, int i) -> const uint8_t* { const int r = 2 * g + i; return r < V ? mrow<WR>(W, r) : nullptr; },
       [&](int) { return nb; }, [&](int, int b) { return (const uint16_t*)(s.n.xs + b * KK); },
       [&](int g, int nv, const float(&v)[2][B]) {
 #pragma unroll
@@ -585,7 +635,7 @@ __device__ __forceinline__ void phase_token_b(const Params& p, Wait wait) {
 }
 
 // ---------------------------------------------------------------- batched persistent kernel
-template <int H, int KA, int KM, bool MOE, int EC, int B>
+template <int H, int KA, int KM, bool MOE, int EC, bool FP8, int B>
 __device__ __forceinline__ void fused_body_b(const Params& p) {
   __shared__ SmemB<B> s;
   if (threadIdx.x == 0) s.abort = 0;
@@ -595,30 +645,30 @@ __device__ __forceinline__ void fused_body_b(const Params& p) {
   if (p.trace && threadIdx.x == 0) *(MK_G uint64_t*)(p.trace + (size_t)blockIdx.x * 3) = __builtin_amdgcn_s_memrealtime();
   s.phase = 0;
   for (int layer = p.l0; layer < p.l1; ++layer) {
-    phase_qkv_b<H, B>(p, layer, s, wait);
+    phase_qkv_b<RowOf<FP8, H>, B>(p, layer, s, wait);
     if (s.abort) return;
     grid_arrive(p, k, s);
     phase_attn<B>(p, layer, s, wait);
     if (s.abort) return;
     grid_arrive(p, k, s);
-    phase_oproj_b<KA, B>(p, layer, s, wait);
+    phase_oproj_b<RowOf<FP8, KA>, B>(p, layer, s, wait);
     if (s.abort) return;
     grid_arrive(p, k, s);
     if constexpr (MOE) {
       phase_router_b<H, B>(p, layer, s, wait);
       if (s.abort) return;
       grid_arrive(p, k, s);
-      phase_expert_up_b<H, B, EC>(p, layer, s, wait);
+      phase_expert_up_b<RowOf<FP8, H>, B, EC>(p, layer, s, wait);
       if (s.abort) return;
       grid_arrive(p, k, s);
-      phase_expert_down_b<KM, B>(p, layer, s, wait);
+      phase_expert_down_b<RowOf<FP8, KM>, B>(p, layer, s, wait);
       if (s.abort) return;
       grid_arrive(p, k, s);
     } else {
-      phase_gateup_b<H, B>(p, layer, s, wait);
+      phase_gateup_b<RowOf<FP8, H>, B>(p, layer, s, wait);
       if (s.abort) return;
       grid_arrive(p, k, s);
-      phase_down_b<KM, B>(p, layer, s, wait);
+      phase_down_b<RowOf<FP8, KM>, B>(p, layer, s, wait);
       if (s.abort) return;
       grid_arrive(p, k, s);
     }
@@ -631,15 +681,23 @@ __device__ __forceinline__ void fused_body_b(const Params& p) {
   }
 }
 
-// batched shapes: name, H, KA, KM, MoE, E, batch capacity (the host picks the smallest capacity >= its batch)
-#define MK_BATCH_SHAPES(X)                                                    \
-  X(etxmk_fused_b4_h2048_a4096_moe768_e128, 2048, 4096, 768, true, 128, 4)   \
-  X(etxmk_fused_b16_h2048_a4096_moe768_e128, 2048, 4096, 768, true, 128, 16) \
-  X(etxmk_fused_b4_h512_a512_moe256_e16, 512, 512, 256, true, 16, 4)         \
-  X(etxmk_fused_b16_h512_a512_moe256_e16, 512, 512, 256, true, 16, 16)       \
-  X(etxmk_fused_b4_h512_a512_mlp1024, 512, 512, 1024, false, 0, 4)
-#define MK_BATCH_KERNEL(name, H, KA, KM, MOE, EC, B) \
-  extern "C" __global__ void __launch_bounds__(NT, 1) name(Params p) { fused_body_b<H, KA, KM, MOE, EC, B>(p); }
-MK_BATCH_SHAPES(MK_BATCH_KERNEL)
+// batched shapes: name, H, KA, KM, MoE, E, fp8 weights, batch capacity (the host picks the smallest capacity that
+// holds its batch); one translation unit per list (mk_batch_bf16.hip, mk_batch_fp8.hip)
+#define MK_BATCH_SHAPES_BF16(X)                                                      \
+  X(etxmk_fused_b4_h2048_a4096_moe768_e128, 2048, 4096, 768, true, 128, false, 4)   \
+  X(etxmk_fused_b16_h2048_a4096_moe768_e128, 2048, 4096, 768, true, 128, false, 16) \
+  X(etxmk_fused_b4_h512_a512_moe256_e16, 512, 512, 256, true, 16, false, 4)         \
+  X(etxmk_fused_b16_h512_a512_moe256_e16, 512, 512, 256, true, 16, false, 16)       \
+  X(etxmk_fused_b4_h512_a512_mlp1024, 512, 512, 1024, false, 0, false, 4)
+#define MK_BATCH_SHAPES_FP8(X)                                                          \
+  X(etxmk_fused_fp8_b4_h2048_a4096_moe768_e128, 2048, 4096, 768, true, 128, true, 4)   \
+  X(etxmk_fused_fp8_b16_h2048_a4096_moe768_e128, 2048, 4096, 768, true, 128, true, 16) \
+  X(etxmk_fused_fp8_b4_h512_a512_moe256_e16, 512, 512, 256, true, 16, true, 4)         \
+  X(etxmk_fused_fp8_b16_h512_a512_moe256_e16, 512, 512, 256, true, 16, true, 16)       \
+  X(etxmk_fused_fp8_b4_h512_a512_mlp1024, 512, 512, 1024, false, 0, true, 4)
+#define MK_BATCH_KERNEL(name, H, KA, KM, MOE, EC, FP8, B) \
+  extern "C" __global__ void __launch_bounds__(NT, 1) name(Params p) { fused_body_b<H, KA, KM, MOE, EC, FP8, B>(p); }
+#define MK_BATCH_DECL(name, H, KA, KM, MOE, EC, FP8, B) \
+  extern "C" __global__ void __launch_bounds__(NT, 1) name(Params p);
 
 }  // namespace mk

@@ -1,0 +1,6 @@
+// The batched persistent kernels with fp8 weights (one translation unit per list, compiled in parallel).
+#include "mk_batch.h"
+
+namespace mk {
+MK_BATCH_SHAPES_FP8(MK_BATCH_KERNEL)
+}  // namespace mk

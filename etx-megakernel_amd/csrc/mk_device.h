@@ -41,9 +41,10 @@ constexpr int PART = HDIM + 2;          // attention partial: a[HD], m, l
 constexpr int QKVW_BYTES = 81920;       // the workgroup's rows of the next layer's QKV matrix, staged in LDS
 constexpr int MAX_B = 16;               // sequences per batched step
 
+// one layer's tensors; matrices are byte addresses of rows in their format (Bf16Row / Fp8Row below)
 struct LayerW {
   const uint16_t *ln1, *ln2, *qn, *kn;
-  const uint16_t *wqkv, *wo, *wr, *w13, *w2, *wgu, *wd;
+  const uint8_t *wqkv, *wo, *wr, *w13, *w2, *wgu, *wd;
   uint16_t *kc, *vc;
 };
 
@@ -386,33 +387,165 @@ __device__ __forceinline__ float dot_row_long(const uint16_t* row, const uint16_
   return wave_sum(acc);
 }
 
+// fp8 rows (etxmk_config.wdtype = ETXMK_W_FP8): K e4m3 codes stored lane-permuted in blocks of 1024 (lane l's 16
+// bytes of a block are the logical elements l, l+64, ..., l+960; a last block of 64m elements gives each lane m),
+// then the row's fp32 scale, rows K + 16 bytes apart.  The input vector keeps its bf16 layout (blocks of 512), so
+// a block's first 8 codes pair with the lane's 8 elements of one 512-block and the next 8 with the following one.
+template <int K>
+struct KS8 {
+  static_assert(K % 256 == 0, "fp8 rows are whole 256-element quarters of a block");
+  static constexpr int KB = K / 1024;
+  static constexpr int T = K % 1024;             // tail block length
+  static constexpr int TM = T / 64;              // codes per lane in the tail (4, 8 or 12)
+  static constexpr int TW = TM / 4;
+  static constexpr int REGS = 4 * KB + TW + 1;   // VGPRs one row occupies in flight (with its scale)
+};
+
+template <int K>
+struct RowRegs8 {
+  u32x4 w[KS8<K>::KB > 0 ? KS8<K>::KB : 1];
+  uint32_t t[KS8<K>::TW > 0 ? KS8<K>::TW : 1];
+  float sc;
+};
+
+template <int K>
+__device__ __forceinline__ void load_row8(RowRegs8<K>& r, const uint8_t* row, int lane) {
+#pragma unroll
+  for (int b = 0; b < KS8<K>::KB; ++b) r.w[b] = ld_nt16(row + 1024 * b + lane * 16);
+#pragma unroll
+  for (int t = 0; t < KS8<K>::TW; ++t) r.t[t] = ld_nt4(row + 1024 * KS8<K>::KB + lane * KS8<K>::TM + 4 * t);
+  r.sc = ld_f((const float*)(row + K));
+}
+
+// the 16 input elements that pair with lane `lane`'s codes of fp8 block j (or its tail), as fp32
+template <int K>
+__device__ __forceinline__ void x_of_fp8_block(const uint16_t* xs, int j, int lane, float (&xv)[16]) {
+  if (j < KS8<K>::KB || KS8<K>::T >= 512) {
+    const u32x4 a = *(const u32x4*)(xs + 1024 * j + lane * 8);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) { xv[2 * e] = bf_lo(a[e]); xv[2 * e + 1] = bf_hi(a[e]); }
+  }
+  if (j < KS8<K>::KB) {
+    const u32x4 b = *(const u32x4*)(xs + 1024 * j + 512 + lane * 8);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) { xv[8 + 2 * e] = bf_lo(b[e]); xv[9 + 2 * e] = bf_hi(b[e]); }
+  } else if constexpr (KS8<K>::T == 768) {                // 512 + a 256 bf16 tail (4 per lane)
+    const uint64_t b = *(const uint64_t*)(xs + 1024 * j + 512 + lane * 4);
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const uint32_t w = (uint32_t)(b >> (32 * e));
+      xv[8 + 2 * e] = bf_lo(w);
+      xv[9 + 2 * e] = bf_hi(w);
+    }
+  } else if constexpr (KS8<K>::T == 256) {                // a 256 bf16 tail (4 per lane)
+    const uint64_t b = *(const uint64_t*)(xs + 1024 * j + lane * 4);
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const uint32_t w = (uint32_t)(b >> (32 * e));
+      xv[2 * e] = bf_lo(w);
+      xv[2 * e + 1] = bf_hi(w);
+    }
+  }
+}
+// the codes of block j (or the tail) decoded to fp32 (hardware OCP e4m3 conversion, exact)
+template <int K>
+__device__ __forceinline__ void w_of_fp8_block(const RowRegs8<K>& r, int j, float (&wv)[16]) {
+  constexpr int NW = KS8<K>::TW;
+  auto dec4 = [&](uint32_t d, int e0) {
+    const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)d, false);
+    const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)d, true);
+    wv[e0] = lo[0]; wv[e0 + 1] = lo[1]; wv[e0 + 2] = hi[0]; wv[e0 + 3] = hi[1];
+  };
+  if (j < KS8<K>::KB) {
+#pragma unroll
+    for (int d = 0; d < 4; ++d) dec4(r.w[j][d], 4 * d);
+  } else {
+#pragma unroll
+    for (int d = 0; d < NW; ++d) dec4(r.t[d], 4 * d);
+  }
+}
+
+// fp8 row dot: lane order as dot_row (blocks ascending, a lane's elements ascending), then wave_sum, then the scale
+template <int K>
+__device__ __forceinline__ float dot_row8(const RowRegs8<K>& r, const uint16_t* xs, int lane) {
+  constexpr int NB = KS8<K>::KB + (KS8<K>::T > 0 ? 1 : 0);
+  float acc = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NB; ++j) {
+    const int n = j < KS8<K>::KB ? 16 : KS8<K>::TM;
+    float wv[16], xv[16];
+    w_of_fp8_block<K>(r, j, wv);
+    x_of_fp8_block<K>(xs, j, lane, xv);
+#pragma unroll
+    for (int e = 0; e < 16; ++e)
+      if (e < n) acc = __builtin_fmaf(wv[e], xv[e], acc);
+  }
+  return wave_sum(acc) * r.sc;
+}
+
+// Row formats of the streamed matrices: the register image of one row in flight, its load and its dot with the
+// input vector in LDS.  The GEMV engine and the phases are written once over these.
+template <int K_>
+struct Bf16Row {
+  static constexpr int K = K_;
+  static constexpr bool FP8 = false;
+  static constexpr bool LONG = KS<K>::KB > 16;   // streamed in segments (dot_row_long), not held in registers
+  static constexpr size_t STRIDE = 2 * (size_t)K;
+  static constexpr int REGS = KS<K>::REGS;
+  using Regs = RowRegs<K>;
+  __device__ static void load(Regs& r, const uint8_t* row, int lane) { load_row<K>(r, (const uint16_t*)row, lane); }
+  __device__ static float dot(const Regs& r, const uint16_t* xs, int lane) { return dot_row<K>(r, xs, lane); }
+  __device__ static float dot_long(const uint8_t* row, const uint16_t* xs, int lane) {
+    if constexpr (LONG) return dot_row_long<K>((const uint16_t*)row, xs, lane);
+    else return 0.0f;
+  }
+};
+template <int K_>
+struct Fp8Row {
+  static constexpr int K = K_;
+  static constexpr bool FP8 = true;
+  static constexpr bool LONG = false;
+  static_assert(K <= 8192, "fp8 rows are held in registers");
+  static constexpr size_t STRIDE = (size_t)K + 16;
+  static constexpr int REGS = KS8<K>::REGS;
+  using Regs = RowRegs8<K>;
+  __device__ static void load(Regs& r, const uint8_t* row, int lane) { load_row8<K>(r, row, lane); }
+  __device__ static float dot(const Regs& r, const uint16_t* xs, int lane) { return dot_row8<K>(r, xs, lane); }
+  __device__ static float dot_long(const uint8_t*, const uint16_t*, int) { return 0.0f; }
+};
+template <bool FP8, int K>
+using RowOf = typename std::conditional<FP8, Fp8Row<K>, Bf16Row<K>>::type;
+// row r of a matrix stored in format WR
+template <class WR>
+__device__ __forceinline__ const uint8_t* mrow(const uint8_t* base, size_t r) { return base + r * WR::STRIDE; }
+
 // Groups of NR rows are dealt round-robin to the grid's waves (group g to global wave g mod nw).  A wave loads up
 // to D of its groups at once (about 96 VGPRs of weights), then reduces them; the first batch is issued before
 // `prologue` runs, so the weight stream overlaps the grid-barrier wait and the input-vector build that the
 // prologue does.  Every thread calls prologue() exactly once (it may synchronise the workgroup); it returns false
 // to abandon the phase.  rowf(g, i) gives row i of group g (nullptr when absent), xf(i) its LDS input vector,
 // epi(g, v) consumes the NR dot products (every lane holds them).  All group logic is wave-uniform.
-template <int K, int NR, class RowF, class XF, class EpiF, class Pro>
+template <class WR, int NR, class RowF, class XF, class EpiF, class Pro>
 __device__ __forceinline__ bool gemv_run(int ngroups, RowF rowf, XF xf, EpiF epi, Pro prologue, int nwg,
                                          uint64_t* trace = nullptr, int s_phase = 0) {
   const int lane = lane_id();
   const int gw = blockIdx.x * NWAVE + wave_u(), nw = nwg * NWAVE;
-  if constexpr (KS<K>::KB > 16) {
+  if constexpr (WR::LONG) {
     if (!prologue()) return false;
     for (int g = gw; g < ngroups; g += nw) {
       float v[NR];
 #pragma unroll
       for (int i = 0; i < NR; ++i) {
-        const uint16_t* rp = rowf(g, i);
-        v[i] = rp ? dot_row_long<K>(rp, xf(i), lane) : 0.0f;
+        const uint8_t* rp = rowf(g, i);
+        v[i] = rp ? WR::dot_long(rp, xf(i), lane) : 0.0f;
       }
       epi(g, v);
     }
     return true;
   } else {
-    constexpr int RPG = NR * KS<K>::REGS;
+    constexpr int RPG = NR * WR::REGS;
     constexpr int D = (96 / RPG) < 1 ? 1 : (96 / RPG) > 8 ? 8 : (96 / RPG);
-    RowRegs<K> R[D][NR];
+    typename WR::Regs R[D][NR];
     auto issue = [&](int g0) {
 #pragma unroll
       for (int d = 0; d < D; ++d) {
@@ -420,8 +553,8 @@ __device__ __forceinline__ bool gemv_run(int ngroups, RowF rowf, XF xf, EpiF epi
         if (g < ngroups) {
 #pragma unroll
           for (int i = 0; i < NR; ++i) {
-            const uint16_t* rp = rowf(g, i);
-            if (rp) load_row<K>(R[d][i], rp, lane);
+            const uint8_t* rp = rowf(g, i);
+            if (rp) WR::load(R[d][i], rp, lane);
           }
         }
       }
@@ -439,8 +572,8 @@ __device__ __forceinline__ bool gemv_run(int ngroups, RowF rowf, XF xf, EpiF epi
           float v[NR];
 #pragma unroll
           for (int i = 0; i < NR; ++i) {
-            const uint16_t* rp = rowf(g, i);
-            v[i] = rp ? dot_row<K>(R[d][i], xf(i), lane) : 0.0f;
+            const uint8_t* rp = rowf(g, i);
+            v[i] = rp ? WR::dot(R[d][i], xf(i), lane) : 0.0f;
           }
           epi(g, v);
         }
@@ -496,7 +629,7 @@ __device__ __forceinline__ void qkv_to_lds(const Params& p, int layer, Smem& s) 
   const int rows = (p.NH + 2 * p.NKV) * p.HD, R = p.qkv_rows, r0 = (int)blockIdx.x * R;
   const int lane = lane_id();
   for (int i = wave_u(); i < R && r0 + i < rows; i += NWAVE) {
-    const uint16_t* src = Lw.wqkv + (size_t)(r0 + i) * KK + 8 * lane;
+    const uint16_t* src = (const uint16_t*)Lw.wqkv + (size_t)(r0 + i) * KK + 8 * lane;
 #pragma unroll
     for (int b = 0; b < KK / 512; ++b)
       __builtin_amdgcn_global_load_lds((const MK_G void*)(src + 512 * b),
@@ -534,16 +667,17 @@ __device__ __forceinline__ void phase_qkv_lds(const Params& p, int layer, Smem& 
 }
 
 // P1: input RMSNorm + fused QKV GEMV (ref_numpy.py:111-115)
-template <int KK, class Wait>
+template <class WR, class Wait>
 __device__ __forceinline__ void phase_qkv(const Params& p, int layer, Smem& s, Wait wait) {
+  constexpr int KK = WR::K;
   const LayerW Lw = layer_w(p, layer);
   const bool first = layer == p.l0 && p.do_embed;
   const int rows = (p.NH + 2 * p.NKV) * p.HD;
   float* qkv = p.qkv;
-  const uint16_t* W = Lw.wqkv;
-  gemv_run<KK, 2>(
+  const uint8_t* W = Lw.wqkv;
+  gemv_run<WR, 2>(
       (rows + 1) / 2,
-      [&](int g, int i) -> const uint16_t* { const int r = 2 * g + i; return r < rows ? W + (size_t)r * KK : nullptr; },
+      [&](int g, int i) -> const uint8_t* { const int r = 2 * g + i; return r < rows ? mrow<WR>(W, r) : nullptr; },
       [&](int) { return (const uint16_t*)s.g.xs; },
       [&](int g, const float(&v)[2]) {
         lane_store<2>(v, [&](int i, float val) { const int r = 2 * g + i; if (r < rows) st_ag(qkv + r, bfr(val)); });
@@ -812,16 +946,17 @@ __device__ __forceinline__ void phase_attn(const Params& p, int layer, S& s, Wai
 // the prologue together with o, so the epilogue does not wait on memory.  HQ > 0 (persistent kernel): the next
 // layer's QKV rows of this workgroup start streaming into LDS right behind the O rows; the attention and router
 // phases around it leave the memory system room for them.
-template <int KK, class Wait, int HQ = 0>
+template <class WR, class Wait, int HQ = 0>
 __device__ __forceinline__ void phase_oproj(const Params& p, int layer, Smem& s, Wait wait) {
+  constexpr int KK = WR::K;
   const LayerW Lw = layer_w(p, layer);
   const int H = p.H;
   const bool first = layer == p.l0 && p.do_embed;
   float* x = p.x;
-  const uint16_t* W = Lw.wo;
-  gemv_run<KK, 1>(
+  const uint8_t* W = Lw.wo;
+  gemv_run<WR, 1>(
       H,
-      [&](int g, int) -> const uint16_t* { return W + (size_t)g * KK; },
+      [&](int g, int) -> const uint8_t* { return mrow<WR>(W, g); },
       [&](int) { return (const uint16_t*)s.g.xs; },
       [&](int g, const float(&v)[1]) {
         if (lane_id() == 0) st_ag(x + g, bfr(s.g.xf[g] + bfr(v[0])));
@@ -841,13 +976,14 @@ __device__ __forceinline__ void phase_oproj(const Params& p, int layer, Smem& s,
 // P4: post-attention RMSNorm + router GEMV (ref_numpy.py:131-134)
 template <int KK, class Wait>
 __device__ __forceinline__ void phase_router(const Params& p, int layer, Smem& s, Wait wait) {
+  using WR = Bf16Row<KK>;                                 // the router stays bf16 in every weight type
   const LayerW Lw = layer_w(p, layer);
   const int E = p.E;
   float* lg = p.logits;
-  const uint16_t* W = Lw.wr;
-  gemv_run<KK, 1>(
+  const uint8_t* W = Lw.wr;
+  gemv_run<WR, 1>(
       E,
-      [&](int g, int) -> const uint16_t* { return W + (size_t)g * KK; },
+      [&](int g, int) -> const uint8_t* { return mrow<WR>(W, g); },
       [&](int) { return (const uint16_t*)s.g.xs; },
       [&](int g, const float(&v)[1]) { if (lane_id() == 0) st_ag(lg + g, bfr(v[0])); },
       [&]() {
@@ -941,12 +1077,13 @@ __device__ __forceinline__ void route_topk(const Params& p, Smem& s) {
 
 // P5: experts gate/up + SiLU*up for the top-k slots (ref_numpy.py:142-145).  The normed input depends only on x
 // (final since the O projection), so it is built before the wait; the routing needs this phase's inputs.
-template <int KK, class Wait, int EC = 0>
+template <class WR, class Wait, int EC = 0>
 __device__ __forceinline__ void phase_expert_up(const Params& p, int layer, Smem& s, Wait wait) {
+  constexpr int KK = WR::K;
   const LayerW Lw = layer_w(p, layer);
   const int MI = p.MI, KT = p.TOPK;
   float* hb = p.hbuf;
-  const uint16_t* W = Lw.w13;
+  const uint8_t* W = Lw.w13;
   build_norm_x<KK>(p, p.x, nullptr, Lw.ln2, s);
   if (!wait()) return;
   route_topk<EC>(p, s);
@@ -957,11 +1094,11 @@ __device__ __forceinline__ void phase_expert_up(const Params& p, int layer, Smem
     if (p.dump_logits)
       for (int e = t; e < p.E; e += 64) st_f(p.dump_logits + (size_t)layer * p.E + e, ld_ag(p.logits + e));
   }
-  gemv_run<KK, 2>(
+  gemv_run<WR, 2>(
       KT * MI,
-      [&](int g, int i) -> const uint16_t* {
+      [&](int g, int i) -> const uint8_t* {
         const int slot = g / MI, jj = g - slot * MI;
-        return W + ((size_t)s.ids[wave_u()][slot] * 2 * MI + 2 * jj + i) * KK;
+        return mrow<WR>(W, (size_t)s.ids[wave_u()][slot] * 2 * MI + 2 * jj + i);
       },
       [&](int) { return (const uint16_t*)s.g.xs; },
       [&](int g, const float(&v)[2]) {
@@ -972,16 +1109,17 @@ __device__ __forceinline__ void phase_expert_up(const Params& p, int layer, Smem
 
 // P6: expert down, routing weight, combine in ascending expert id, residual (ref_numpy.py:146-148).  The routing
 // comes from the router logits, final since two barriers ago, so the weights stream before the wait.
-template <int KK, class Wait, bool ROUTED = false>
+template <class WR, class Wait, bool ROUTED = false>
 __device__ __forceinline__ void phase_expert_down(const Params& p, int layer, Smem& s, Wait wait) {
+  constexpr int KK = WR::K;
   const LayerW Lw = layer_w(p, layer);
   const int H = p.H, KT = p.TOPK;
   if constexpr (!ROUTED) route_topk(p, s);                 // the persistent kernel keeps expert_up's routing in LDS
   float* x = p.x;
-  const uint16_t* W = Lw.w2;
-  gemv_run<KK, MAX_TOPK>(
+  const uint8_t* W = Lw.w2;
+  gemv_run<WR, MAX_TOPK>(
       H,
-      [&](int g, int i) -> const uint16_t* { return i < KT ? W + ((size_t)s.ids[wave_u()][i] * H + g) * KK : nullptr; },
+      [&](int g, int i) -> const uint8_t* { return i < KT ? mrow<WR>(W, (size_t)s.ids[wave_u()][i] * H + g) : nullptr; },
       [&](int i) { return (const uint16_t*)(s.g.xs + (size_t)i * KK); },
       [&](int g, const float(&v)[MAX_TOPK]) {
         if (lane_id() == 0) {
@@ -1010,14 +1148,15 @@ __device__ __forceinline__ void phase_expert_down(const Params& p, int layer, Sm
 }
 
 // dense MLP (ref_numpy.py:149-152): P4' gate/up + SiLU*up, P5' down + residual
-template <int KK, class Wait>
+template <class WR, class Wait>
 __device__ __forceinline__ void phase_gateup(const Params& p, int layer, Smem& s, Wait wait) {
+  constexpr int KK = WR::K;
   const LayerW Lw = layer_w(p, layer);
   float* hb = p.hbuf;
-  const uint16_t* W = Lw.wgu;
-  gemv_run<KK, 2>(
+  const uint8_t* W = Lw.wgu;
+  gemv_run<WR, 2>(
       p.I,
-      [&](int g, int i) -> const uint16_t* { return W + ((size_t)2 * g + i) * KK; },
+      [&](int g, int i) -> const uint8_t* { return mrow<WR>(W, (size_t)2 * g + i); },
       [&](int) { return (const uint16_t*)s.g.xs; },
       [&](int g, const float(&v)[2]) {
         if (lane_id() == 0) st_ag(hb + g, bfr(bfr(silu(bfr(v[0]))) * bfr(v[1])));
@@ -1030,14 +1169,15 @@ __device__ __forceinline__ void phase_gateup(const Params& p, int layer, Smem& s
       p.nwg, p.trace, s.phase);
 }
 
-template <int KK, class Wait>
+template <class WR, class Wait>
 __device__ __forceinline__ void phase_down(const Params& p, int layer, Smem& s, Wait wait) {
+  constexpr int KK = WR::K;
   const LayerW Lw = layer_w(p, layer);
   float* x = p.x;
-  const uint16_t* W = Lw.wd;
-  gemv_run<KK, 1>(
+  const uint8_t* W = Lw.wd;
+  gemv_run<WR, 1>(
       p.H,
-      [&](int g, int) -> const uint16_t* { return W + (size_t)g * KK; },
+      [&](int g, int) -> const uint8_t* { return mrow<WR>(W, g); },
       [&](int) { return (const uint16_t*)s.g.xs; },
       [&](int g, const float(&v)[1]) {
         if (lane_id() == 0) st_ag(x + g, bfr(s.g.xf[g] + bfr(v[0])));
@@ -1062,13 +1202,14 @@ __device__ __forceinline__ uint64_t argmax_key(float v, int idx) {
 
 template <int KK, class Wait>
 __device__ __forceinline__ void phase_head(const Params& p, Smem& s, Wait wait) {
+  using WR = Bf16Row<KK>;                                 // lm_head stays bf16 in every weight type
   const int V = p.V;
-  const uint16_t* W = p.lm_head;
+  const uint8_t* W = (const uint8_t*)p.lm_head;
   uint64_t best = 0;
   bool ran = false;
-  ran = gemv_run<KK, 2>(
+  ran = gemv_run<WR, 2>(
       (V + 1) / 2,
-      [&](int g, int i) -> const uint16_t* { const int r = 2 * g + i; return r < V ? W + (size_t)r * KK : nullptr; },
+      [&](int g, int i) -> const uint8_t* { const int r = 2 * g + i; return r < V ? mrow<WR>(W, r) : nullptr; },
       [&](int) { return (const uint16_t*)s.g.xs; },
       [&](int g, const float(&v)[2]) {
 #pragma unroll
@@ -1109,11 +1250,11 @@ __device__ __forceinline__ void phase_token(const Params& p, Wait wait) {
 // runtime row-length dispatch (unfused per-phase kernels)
 template <class Wait>
 __device__ __forceinline__ void phase_qkv_any(const Params& p, int layer, Smem& s, Wait wait) {
-  dispatch_k<MK_K_HIDDEN>(p.H, [&](auto kc_) { phase_qkv<decltype(kc_)::value>(p, layer, s, wait); });
+  dispatch_k<MK_K_HIDDEN>(p.H, [&](auto kc_) { phase_qkv<Bf16Row<decltype(kc_)::value>>(p, layer, s, wait); });
 }
 template <class Wait>
 __device__ __forceinline__ void phase_oproj_any(const Params& p, int layer, Smem& s, Wait wait) {
-  dispatch_k<MK_K_ATTN>(p.NH * p.HD, [&](auto kc_) { phase_oproj<decltype(kc_)::value>(p, layer, s, wait); });
+  dispatch_k<MK_K_ATTN>(p.NH * p.HD, [&](auto kc_) { phase_oproj<Bf16Row<decltype(kc_)::value>>(p, layer, s, wait); });
 }
 template <class Wait>
 __device__ __forceinline__ void phase_router_any(const Params& p, int layer, Smem& s, Wait wait) {
@@ -1121,19 +1262,19 @@ __device__ __forceinline__ void phase_router_any(const Params& p, int layer, Sme
 }
 template <class Wait>
 __device__ __forceinline__ void phase_expert_up_any(const Params& p, int layer, Smem& s, Wait wait) {
-  dispatch_k<MK_K_HIDDEN>(p.H, [&](auto kc_) { phase_expert_up<decltype(kc_)::value>(p, layer, s, wait); });
+  dispatch_k<MK_K_HIDDEN>(p.H, [&](auto kc_) { phase_expert_up<Bf16Row<decltype(kc_)::value>>(p, layer, s, wait); });
 }
 template <class Wait>
 __device__ __forceinline__ void phase_expert_down_any(const Params& p, int layer, Smem& s, Wait wait) {
-  dispatch_k<MK_K_MOE>(p.MI, [&](auto kc_) { phase_expert_down<decltype(kc_)::value>(p, layer, s, wait); });
+  dispatch_k<MK_K_MOE>(p.MI, [&](auto kc_) { phase_expert_down<Bf16Row<decltype(kc_)::value>>(p, layer, s, wait); });
 }
 template <class Wait>
 __device__ __forceinline__ void phase_gateup_any(const Params& p, int layer, Smem& s, Wait wait) {
-  dispatch_k<MK_K_HIDDEN>(p.H, [&](auto kc_) { phase_gateup<decltype(kc_)::value>(p, layer, s, wait); });
+  dispatch_k<MK_K_HIDDEN>(p.H, [&](auto kc_) { phase_gateup<Bf16Row<decltype(kc_)::value>>(p, layer, s, wait); });
 }
 template <class Wait>
 __device__ __forceinline__ void phase_down_any(const Params& p, int layer, Smem& s, Wait wait) {
-  dispatch_k<MK_K_INTER>(p.I, [&](auto kc_) { phase_down<decltype(kc_)::value>(p, layer, s, wait); });
+  dispatch_k<MK_K_INTER>(p.I, [&](auto kc_) { phase_down<Bf16Row<decltype(kc_)::value>>(p, layer, s, wait); });
 }
 template <class Wait>
 __device__ __forceinline__ void phase_head_any(const Params& p, Smem& s, Wait wait) {
@@ -1143,9 +1284,10 @@ __device__ __forceinline__ void phase_head_any(const Params& p, Smem& s, Wait wa
 // ---------------------------------------------------------------- kernels
 enum Phase { PH_QKV = 0, PH_ATTN, PH_OPROJ, PH_ROUTER, PH_EXPUP, PH_EXPDN, PH_GATEUP, PH_DOWN, PH_HEAD, PH_TOKEN };
 
-// The persistent kernel, instantiated per model shape: hidden size H, attention width KA = NH*HD, and the MLP
-// row length KM (the expert intermediate for MoE, the dense intermediate otherwise).
-template <int H, int KA, int KM, bool MOE, int EC>
+// The persistent kernel, instantiated per model shape: hidden size H, attention width KA = NH*HD, the MLP row
+// length KM (the expert intermediate for MoE, the dense intermediate otherwise) and the weight type (FP8: the
+// QKV, O and MLP matrices in Fp8Row format).
+template <int H, int KA, int KM, bool MOE, int EC, bool FP8>
 __device__ __forceinline__ void fused_body(const Params& p) {
   __shared__ Smem s;
   if (threadIdx.x == 0) s.abort = 0;
@@ -1157,31 +1299,35 @@ __device__ __forceinline__ void fused_body(const Params& p) {
   if (p.trace && threadIdx.x == 0) *(MK_G uint64_t*)(p.trace + (size_t)blockIdx.x * 3) = __builtin_amdgcn_s_memrealtime();
   s.phase = 0;
   for (int layer = p.l0; layer < p.l1; ++layer) {
-    if (p.qkv_rows > 0 && layer > p.l0) phase_qkv_lds<H>(p, layer, s, wait);
-    else phase_qkv<H>(p, layer, s, wait);
+    if constexpr (!FP8) {
+      if (p.qkv_rows > 0 && layer > p.l0) phase_qkv_lds<H>(p, layer, s, wait);
+      else phase_qkv<Bf16Row<H>>(p, layer, s, wait);
+    } else {
+      phase_qkv<Fp8Row<H>>(p, layer, s, wait);
+    }
     if (s.abort) return;
     grid_arrive(p, k, s);
     phase_attn<1>(p, layer, s, wait);
     if (s.abort) return;
     grid_arrive(p, k, s);
-    phase_oproj<KA, decltype(wait), (H % 512 == 0 ? H : 0)>(p, layer, s, wait);
+    phase_oproj<RowOf<FP8, KA>, decltype(wait), (!FP8 && H % 512 == 0 ? H : 0)>(p, layer, s, wait);
     if (s.abort) return;
     grid_arrive(p, k, s);
     if constexpr (MOE) {
       phase_router<H>(p, layer, s, wait);
       if (s.abort) return;
       grid_arrive(p, k, s);
-      phase_expert_up<H, decltype(wait), EC>(p, layer, s, wait);
+      phase_expert_up<RowOf<FP8, H>, decltype(wait), EC>(p, layer, s, wait);
       if (s.abort) return;
       grid_arrive(p, k, s);
-      phase_expert_down<KM, decltype(wait), true>(p, layer, s, wait);
+      phase_expert_down<RowOf<FP8, KM>, decltype(wait), true>(p, layer, s, wait);
       if (s.abort) return;
       grid_arrive(p, k, s);
     } else {
-      phase_gateup<H>(p, layer, s, wait);
+      phase_gateup<RowOf<FP8, H>>(p, layer, s, wait);
       if (s.abort) return;
       grid_arrive(p, k, s);
-      phase_down<KM>(p, layer, s, wait);
+      phase_down<RowOf<FP8, KM>>(p, layer, s, wait);
       if (s.abort) return;
       grid_arrive(p, k, s);
     }
@@ -1194,17 +1340,24 @@ __device__ __forceinline__ void fused_body(const Params& p) {
   }
 }
 
-// shapes with a persistent kernel: name, H, KA, KM, MoE, E (the host picks by the same fields)
-#define MK_FUSED_SHAPES(X)                                             \
-  X(etxmk_fused_h2048_a4096_moe768_e128, 2048, 4096, 768, true, 128)  \
-  X(etxmk_fused_h4096_a4096_mlp12288, 4096, 4096, 12288, false, 0)    \
-  X(etxmk_fused_h512_a512_moe256_e16, 512, 512, 256, true, 16)        \
-  X(etxmk_fused_h512_a512_mlp1024, 512, 512, 1024, false, 0)
-#define MK_FUSED_KERNEL(name, H, KA, KM, MOE, EC) \
-  extern "C" __global__ void __launch_bounds__(NT, 1) name(Params p) { fused_body<H, KA, KM, MOE, EC>(p); }
-MK_FUSED_SHAPES(MK_FUSED_KERNEL)
+// Shapes with a persistent kernel: name, H, KA, KM, MoE, E, fp8 weights (the host picks by the same fields).  Each
+// list is instantiated by its own translation unit (mk_fused_bf16.hip, mk_fused_fp8.hip), so they compile in
+// parallel; the host declares them all (MK_FUSED_DECL).
+#define MK_FUSED_SHAPES_BF16(X)                                                \
+  X(etxmk_fused_h2048_a4096_moe768_e128, 2048, 4096, 768, true, 128, false)   \
+  X(etxmk_fused_h4096_a4096_mlp12288, 4096, 4096, 12288, false, 0, false)     \
+  X(etxmk_fused_h512_a512_moe256_e16, 512, 512, 256, true, 16, false)         \
+  X(etxmk_fused_h512_a512_mlp1024, 512, 512, 1024, false, 0, false)
+#define MK_FUSED_SHAPES_FP8(X)                                                 \
+  X(etxmk_fused_fp8_h2048_a4096_moe768_e128, 2048, 4096, 768, true, 128, true) \
+  X(etxmk_fused_fp8_h512_a512_moe256_e16, 512, 512, 256, true, 16, true)       \
+  X(etxmk_fused_fp8_h512_a512_mlp1024, 512, 512, 1024, false, 0, true)
+#define MK_FUSED_KERNEL(name, H, KA, KM, MOE, EC, FP8) \
+  extern "C" __global__ void __launch_bounds__(NT, 1) name(Params p) { fused_body<H, KA, KM, MOE, EC, FP8>(p); }
+#define MK_FUSED_DECL(name, H, KA, KM, MOE, EC, FP8) extern "C" __global__ void __launch_bounds__(NT, 1) name(Params p);
 
-// unfused mode: one kernel per phase, same device functions (named per phase so profiles separate them)
+// unfused mode: one kernel per phase, same device functions (named per phase so profiles separate them; bf16
+// weights; instantiated by the host translation unit)
 struct NoWait {
   __device__ bool operator()() const { return true; }
 };
@@ -1215,62 +1368,5 @@ struct NoWait {
     __syncthreads();                                                              \
     CALL;                                                                         \
   }
-MK_PHASE_KERNEL(etxmk_p_qkv, phase_qkv_any(p, layer, s, NoWait{}))
-MK_PHASE_KERNEL(etxmk_p_attn, phase_attn<1>(p, layer, s, NoWait{}))
-MK_PHASE_KERNEL(etxmk_p_oproj, phase_oproj_any(p, layer, s, NoWait{}))
-MK_PHASE_KERNEL(etxmk_p_router, phase_router_any(p, layer, s, NoWait{}))
-MK_PHASE_KERNEL(etxmk_p_expert_up, phase_expert_up_any(p, layer, s, NoWait{}))
-MK_PHASE_KERNEL(etxmk_p_expert_down, phase_expert_down_any(p, layer, s, NoWait{}))
-MK_PHASE_KERNEL(etxmk_p_gateup, phase_gateup_any(p, layer, s, NoWait{}))
-MK_PHASE_KERNEL(etxmk_p_down, phase_down_any(p, layer, s, NoWait{}))
-MK_PHASE_KERNEL(etxmk_p_head, phase_head_any(p, s, NoWait{}))
-MK_PHASE_KERNEL(etxmk_p_token, phase_token(p, NoWait{}))
-
-// ---------------------------------------------------------------- seeded initialisation / packing
-// n_t consecutive tensors of rows x cols (experts of one layer); element (r, k) of tensor e is number r*cols+k
-// of stream sid0 + e; stored at its lane-permuted position when perm != 0.
-extern "C" __global__ void etxmk_gen_weights(uint16_t* dst, uint64_t seed, uint64_t sid0, int n_t, int rows, int cols,
-                                             int perm, float scale) {
-  const size_t per = (size_t)rows * cols;
-  const size_t total8 = per * n_t / 8;
-  for (size_t q8 = (size_t)blockIdx.x * blockDim.x + threadIdx.x; q8 < total8; q8 += (size_t)gridDim.x * blockDim.x) {
-    const size_t q = q8 * 8;
-    const int e = (int)(q / per);
-    const size_t rem = q - (size_t)e * per;
-    const int r = (int)(rem / cols), p0 = (int)(rem - (size_t)r * cols);
-    const uint64_t key = stream_key(seed, sid0 + (uint64_t)e);
-    uint16_t out[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int k = perm ? perm_logical(p0 + u, cols) : p0 + u;
-      out[u] = f2bf(scale * normal_at(key, (uint64_t)r * cols + k));
-    }
-    *(u32x4*)(dst + q) = *(const u32x4*)out;
-  }
-}
-
-extern "C" __global__ void etxmk_fill_u16(uint16_t* dst, size_t n, uint16_t v) {
-  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) dst[i] = v;
-}
-
-extern "C" __global__ void etxmk_pack_rows(uint16_t* dst, const uint16_t* src, int rows, int cols) {
-  const size_t total = (size_t)rows * cols;
-  for (size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x; q < total; q += (size_t)gridDim.x * blockDim.x) {
-    const int r = (int)(q / cols), p = (int)(q - (size_t)r * cols);
-    dst[q] = src[(size_t)r * cols + perm_logical(p, cols)];
-  }
-}
-
-// KV positions [0, npos): element (t, h, d) is number (t*NKV + h)*HD + d of the layer's K / V stream
-extern "C" __global__ void etxmk_gen_kv(uint16_t* kc, uint16_t* vc, const int32_t* btab, uint64_t kkey, uint64_t vkey,
-                                        int npos, int NKV, int HD, int BS) {
-  const size_t total = (size_t)npos * NKV * HD;
-  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
-    const int d = (int)(i % HD), h = (int)((i / HD) % NKV), t = (int)(i / ((size_t)HD * NKV));
-    const int blk = btab[t / BS], off = t % BS;
-    kc[((((size_t)blk * NKV + h) * (HD / 8) + d / 8) * BS + off) * 8 + d % 8] = f2bf(normal_at(kkey, i));
-    vc[(((size_t)blk * NKV + h) * HD + d) * BS + off] = f2bf(normal_at(vkey, i));
-  }
-}
 
 }  // namespace mk

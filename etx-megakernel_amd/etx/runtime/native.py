@@ -38,7 +38,10 @@ class DeviceAbort(EtxmkError):
 class EtxmkConfig(C.Structure):
     _fields_ = [(n, C.c_int32) for n in ("H", "NH", "NKV", "HD", "I", "E", "TOPK", "MI", "L", "V",
                                           "moe", "qk_norm", "norm_topk", "block_size", "max_ctx", "batch")] + \
-               [("eps", C.c_float), ("theta", C.c_float)]
+               [("eps", C.c_float), ("theta", C.c_float), ("wdtype", C.c_int32)]
+
+
+W_BF16, W_FP8 = 0, 1          # weight types of etxmk_config.wdtype
 
 
 @dataclass(frozen=True)
@@ -62,6 +65,7 @@ class ModelConfig:
     batch: int = 1
     eps: float = 1e-6
     theta: float = 1e6
+    wdtype: int = W_BF16          # W_FP8: QKV / O / MLP matrices as e4m3 with per-row scales
     name: str = field(default="custom", compare=False)
 
     def as_struct(self) -> EtxmkConfig:
@@ -109,6 +113,7 @@ def load(path: Path | None = None):
         "etxmk_destroy": [vp],
         "etxmk_bind": [vp, vp, vp, vp],
         "etxmk_tensor_info": [vp, i32, i32, i32, C.POINTER(u64), C.POINTER(i32), C.POINTER(i32), C.POINTER(i32)],
+        "etxmk_tensor_format": [vp, i32, i32, C.POINTER(i32), C.POINTER(u64)],
         "etxmk_init_weights_seeded": [vp, u64, C.c_float, vp],
         "etxmk_load_tensor": [vp, i32, i32, i32, vp, vp],
         "etxmk_set_block_table": [vp, C.POINTER(i32), i32, vp],
@@ -161,12 +166,13 @@ def sizes(cfg: ModelConfig) -> dict:
     return out
 
 
-def unpermute_rows(stored: np.ndarray) -> np.ndarray:
-    """Natural row order from the lane-permuted storage (blocks of 512; lane l holds l, l+64, ...)."""
+def unpermute_rows(stored: np.ndarray, block: int = 512) -> np.ndarray:
+    """Natural row order from the lane-permuted storage (blocks of 512 for bf16 rows, 1024 for fp8 codes; lane l
+    holds l, l+64, ...)."""
     rows, K = stored.shape
     out = np.empty_like(stored)
-    for base in range(0, K, 512):
-        S = min(512, K - base)
+    for base in range(0, K, block):
+        S = min(block, K - base)
         m = S // 64
         blk = stored[:, base:base + S].reshape(rows, 64, m)           # [row][lane][e]
         out[:, base:base + S] = blk.transpose(0, 2, 1).reshape(rows, S)  # element l + 64 e
@@ -222,8 +228,25 @@ class Decoder:
         _check(self.L, self.L.etxmk_tensor_info(self.h, kind, layer, expert, C.byref(off), C.byref(r), C.byref(c), C.byref(p)))
         return int(off.value), int(r.value), int(c.value), bool(p.value)
 
+    def tensor_format(self, kind: int, layer: int = -1):
+        """(weight type W_BF16 / W_FP8, bytes per row) of a tensor kind."""
+        wt, rb = C.c_int32(), C.c_uint64()
+        _check(self.L, self.L.etxmk_tensor_format(self.h, kind, layer, C.byref(wt), C.byref(rb)))
+        return int(wt.value), int(rb.value)
+
+    def tensor_fp8(self, kind: int, layer: int = -1, expert: int = 0):
+        """Host copy of an fp8 tensor: (e4m3 codes [rows][cols] uint8 in natural order, scales [rows] fp32)."""
+        wt, rb = self.tensor_format(kind, layer)
+        if wt != W_FP8:
+            raise ValueError(f"tensor kind {kind} is not held as fp8")
+        off, r, c, _ = self.tensor_info(kind, layer, expert)
+        raw = self.weights[off:off + r * rb].cpu().numpy().reshape(r, rb)
+        return unpermute_rows(raw[:, :c].copy(), 1024), raw[:, c:c + 4].copy().view(np.float32).reshape(r)
+
     def tensor(self, kind: int, layer: int = -1, expert: int = 0, natural: bool = True) -> np.ndarray:
-        """Host copy of one tensor as uint16 bf16 bits [rows][cols] (natural row order unless natural=False)."""
+        """Host copy of one bf16 tensor as uint16 bits [rows][cols] (natural row order unless natural=False)."""
+        if self.tensor_format(kind, layer)[0] != W_BF16:
+            raise ValueError(f"tensor kind {kind} is held as fp8: use tensor_fp8")
         off, r, c, perm = self.tensor_info(kind, layer, expert)
         t = self.weights[off:off + r * c * 2].view(self.torch.int16).cpu().numpy().view(np.uint16).reshape(r, c)
         return unpermute_rows(t) if (perm and natural) else t

@@ -52,7 +52,16 @@ typedef struct etxmk_config {
   int32_t H, NH, NKV, HD, I, E, TOPK, MI, L, V;
   int32_t moe, qk_norm, norm_topk, block_size, max_ctx, batch;
   float eps, theta;
+  int32_t wdtype;               /* ETXMK_W_BF16, or ETXMK_W_FP8 */
 } etxmk_config;
+
+/* Weight types.  ETXMK_W_FP8: the QKV, O, expert (gate/up, down) and dense MLP matrices are stored as OCP e4m3
+ * (round to nearest even, saturated at +-448) with one fp32 scale per output row, s = amax(row) / 448, quantised
+ * from bf16 by the library; a matvec row is (sum_k e4m3_k * x_k) * s in the bf16 path's fixed order and rounding
+ * points.  Embedding, router, norms and lm_head stay bf16.  Reference: the fp8 fixture quantisation of
+ * examples/glm53/cpu_check.py:93-98 (per tensor there; per output channel here). */
+#define ETXMK_W_BF16 0
+#define ETXMK_W_FP8 1
 
 typedef struct etxmk_handle etxmk_handle;
 
@@ -82,12 +91,18 @@ int etxmk_bind(etxmk_handle* h, void* weights, void* kv, void* workspace);
 int etxmk_tensor_info(etxmk_handle* h, int kind, int layer, int expert, uint64_t* offset, int32_t* rows,
                       int32_t* cols, int32_t* permuted);
 
+/* Storage of a tensor kind: ETXMK_W_BF16 rows (2 * cols bytes, lane-permuted in blocks of 512 when permuted) or
+ * ETXMK_W_FP8 rows (cols e4m3 codes lane-permuted in blocks of 1024, then the row's fp32 scale and 12 zero
+ * bytes: cols + 16 bytes).  Reference: the per-tensor dtype kind and scale offset of examples/glm53/stage.py:100-124
+ * (block scales there; one scale per row here). */
+int etxmk_tensor_format(etxmk_handle* h, int kind, int layer, int32_t* wdtype, uint64_t* row_bytes);
+
 /* Fill every weight from the seeded generator (bf16(scale * N(0,1)); norm weights 1.0).
  * Reference: random-init weights have no counterpart; the shapes are those of prep.py:88-146. */
 int etxmk_init_weights_seeded(etxmk_handle* h, uint64_t seed, float scale, void* stream);
 
-/* Copy one tensor in natural row-major layout (device pointer) into the arena, permuting its rows.
- * Reference: the weight load of examples/llm/host.hip:70-121. */
+/* Copy one tensor in natural row-major bf16 layout (device pointer) into the arena, permuting its rows (and
+ * quantising them when the tensor is held as fp8).  Reference: the weight load of examples/llm/host.hip:70-121. */
 int etxmk_load_tensor(etxmk_handle* h, int kind, int layer, int expert, const void* src, void* stream);
 
 /* Paged-KV block tables, [batch][ceil(max_ctx / block_size)] flattened: entry b * nbps + i is the physical

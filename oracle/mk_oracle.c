@@ -20,6 +20,12 @@
  *                    mathematically the softmax of ref_numpy.py:122-129.
  *   softmax sums     over experts: the dot64 accumulator pattern with plain adds.
  *   exp              mk_expf below: Cody-Waite reduction by ln2 and a degree-7 Taylor polynomial.
+ *   fp8 weights      (wdtype 1) the QKV, O, expert and dense MLP matrices are held as OCP
+ *                    e4m3 with one fp32 scale per output row, quantised from the seeded bf16 rows: s = amax / 448,
+ *                    q = e4m3(w / s) rounded to nearest even and saturated at +-448.  A matvec row is
+ *                    dot64(e4m3 values, x) * s, followed by the bf16 path's rounding points.  wdtype 2 (oracle
+ *                    only) dequantises instead, w' = bfr(e4m3(q) * s), into the bf16 dot: the HF-style reference
+ *                    the reference's fp8 fixtures build (examples/glm53/cpu_check.py:93-98), for the 5e-2 gate.
  *
  * The seeded weight generator (splitmix64 counter stream + Box-Muller with polynomial log/sin/cos, all
  * in IEEE basic operations) is specified here independently of the device code that must reproduce it.
@@ -196,6 +202,65 @@ static inline float sum64(const float* v, int n) {
   return butterfly64(acc);
 }
 EXPORT float orc_dot64(const uint16_t* w, const float* x, int K) { return dot64(w, x, K); }
+
+/* ------------------------------------------------------------------ fp8 e4m3 (OCP "fn": no infinities, max 448) */
+/* code s.eeee.mmm: e = 0 subnormal m * 2^-9, else (1 + m/8) * 2^(e-7); 0x7F / 0xFF are NaN (never produced here) */
+static inline float e4m3_to_f32(uint8_t c) {
+  const int e = (c >> 3) & 15, mt = c & 7;
+  const float v = e == 0 ? ldexpf((float)mt, -9) : ldexpf(1.0f + (float)mt / 8.0f, e - 7);
+  return (c & 0x80) ? -v : v;
+}
+/* round to nearest even, saturating: |f| >= 448 (or inf) -> 448; below 2^-6 the subnormal grid of 2^-9 */
+static inline uint8_t f32_to_e4m3(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  const uint8_t sign = (uint8_t)((u >> 24) & 0x80);
+  const uint32_t a = u & 0x7FFFFFFFu;
+  float af;
+  memcpy(&af, &a, 4);
+  if (af != af) return (uint8_t)(sign | 0x7E);              /* NaN input: never produced by quantize_rows */
+  if (af >= 448.0f) return (uint8_t)(sign | 0x7E);
+  if (af < 0.015625f) return (uint8_t)(sign | (uint8_t)rintf(af * 512.0f));   /* exact scaling, then RNE */
+  int e = (int)(a >> 23) - 127;                              /* -6 .. 8 */
+  uint32_t qm = (a >> 20) & 7, rem = a & 0xFFFFFu;
+  if (rem > 0x80000u || (rem == 0x80000u && (qm & 1))) ++qm;
+  if (qm == 8) { qm = 0; ++e; }
+  if (e > 8 || (e == 8 && qm > 6)) return (uint8_t)(sign | 0x7E);
+  return (uint8_t)(sign | (uint8_t)((e + 7) << 3) | (uint8_t)qm);
+}
+EXPORT float orc_e4m3_to_f32(uint8_t c) { return e4m3_to_f32(c); }
+EXPORT uint8_t orc_f32_to_e4m3(float f) { return f32_to_e4m3(f); }
+
+/* per-row quantisation of R rows of K bf16 values */
+static void quantize_rows(const uint16_t* w, size_t R, int K, uint8_t* q, float* sc) {
+#pragma omp parallel for schedule(static)
+  for (size_t r = 0; r < R; ++r) {
+    float amax = 0.0f;
+    for (int k = 0; k < K; ++k) { const float v = fabsf(bf2f(w[r * K + k])); if (v > amax) amax = v; }
+    const float s = amax > 0.0f ? amax / 448.0f : 1.0f;
+    sc[r] = s;
+    for (int k = 0; k < K; ++k) q[r * K + k] = f32_to_e4m3(bf2f(w[r * K + k]) / s);
+  }
+}
+EXPORT void orc_quantize_rows(const uint16_t* w, int64_t R, int K, uint8_t* q, float* sc) { quantize_rows(w, (size_t)R, K, q, sc); }
+
+/* canonical dot over e4m3 values (exact in fp32) */
+static inline float dot64_q(const uint8_t* q, const float* x, int K) {
+  float acc[64];
+  for (int l = 0; l < 64; ++l) acc[l] = 0.0f;
+  for (int k0 = 0; k0 < K; k0 += 64)
+    for (int l = 0; l < 64; ++l) acc[l] = fmaf(e4m3_to_f32(q[k0 + l]), x[k0 + l], acc[l]);
+  return butterfly64(acc);
+}
+/* canonical dot over dequantised bf16 weights bfr(e4m3 * s) (wdtype 2) */
+static inline float dot64_deq(const uint8_t* q, float s, const float* x, int K) {
+  float acc[64];
+  for (int l = 0; l < 64; ++l) acc[l] = 0.0f;
+  for (int k0 = 0; k0 < K; k0 += 64)
+    for (int l = 0; l < 64; ++l) acc[l] = fmaf(bfr(e4m3_to_f32(q[k0 + l]) * s), x[k0 + l], acc[l]);
+  return butterfly64(acc);
+}
+EXPORT float orc_dot64_q(const uint8_t* q, const float* x, int K) { return dot64_q(q, x, K); }
 EXPORT float orc_sum64(const float* v, int n) { return sum64(v, n); }
 
 /* ------------------------------------------------------------------ model pieces */
@@ -320,6 +385,7 @@ typedef struct {
   int32_t H, NH, NKV, HD, I, E, TOPK, MI, L, V;
   int32_t moe, qk_norm, norm_topk, block_size, max_ctx, batch;
   float eps, theta;
+  int32_t wdtype;                 /* 0 bf16 weights; 1 fp8 e4m3 + per-row scales; 2 fp8 dequantised to bf16 */
 } orc_config;
 
 /* tensor streams of the seeded generator: kind << 48 | (layer + 1) << 24 | expert */
@@ -330,9 +396,17 @@ static inline uint64_t sid(int kind, int layer, int expert) {
 }
 EXPORT uint64_t orc_stream_id(int kind, int layer, int expert) { return sid(kind, layer, expert); }
 
+/* a weight matrix: bf16 rows (w), or e4m3 rows (q) with one fp32 scale per row (s) */
 typedef struct {
-  uint16_t *wqkv, *wo, *wr, *wgu, *wd;
-  uint16_t **w13, **w2;           /* per expert, generated on first use */
+  uint16_t* w;
+  uint8_t* q;
+  float* s;
+} orc_mat;
+
+typedef struct {
+  orc_mat wqkv, wo, wgu, wd;
+  uint16_t* wr;                   /* the router stays bf16 */
+  orc_mat *w13, *w2;              /* per expert, generated on first use */
   uint16_t *kc, *vc;
 } orc_layer;
 
@@ -352,6 +426,25 @@ static uint16_t* gen_tensor(uint64_t seed, uint64_t stream, size_t n, float scal
   if (p) orc_gen_normal_bf16(seed, stream, 0, n, scale, p);
   return p;
 }
+/* a seeded R x K matrix, quantised (and its bf16 rows dropped) when the model's weights are fp8 */
+static orc_mat gen_mat(uint64_t seed, uint64_t stream, size_t R, int K, float scale, int wdtype) {
+  orc_mat m = {gen_tensor(seed, stream, R * (size_t)K, scale), NULL, NULL};
+  if (wdtype && m.w) {
+    m.q = (uint8_t*)malloc(R * (size_t)K);
+    m.s = (float*)malloc(R * sizeof(float));
+    quantize_rows(m.w, R, K, m.q, m.s);
+    free(m.w);
+    m.w = NULL;
+  }
+  return m;
+}
+static void free_mat(orc_mat* m) { free(m->w); free(m->q); free(m->s); }
+/* row r of a matrix dotted with x (the matvec value before its bf16 rounding) */
+static inline float mat_dot(const orc_mat* m, int wdtype, size_t r, const float* x, int K) {
+  if (wdtype == 0) return dot64(m->w + r * K, x, K);
+  if (wdtype == 1) return dot64_q(m->q + r * K, x, K) * m->s[r];
+  return dot64_deq(m->q + r * K, m->s[r], x, K);
+}
 
 EXPORT void* orc_model_create(const orc_config* cfg, uint64_t seed, float wscale) {
   orc_model* m = (orc_model*)calloc(1, sizeof(orc_model));
@@ -369,15 +462,15 @@ EXPORT void* orc_model_create(const orc_config* cfg, uint64_t seed, float wscale
   const size_t kvn = (size_t)m->nblocks * c->block_size * c->NKV * c->HD;
   for (int l = 0; l < c->L; ++l) {
     orc_layer* y = &m->ly[l];
-    y->wqkv = gen_tensor(seed, sid(S_WQKV, l, 0), (size_t)NQKV * c->H, wscale);
-    y->wo = gen_tensor(seed, sid(S_WO, l, 0), (size_t)c->H * c->NH * c->HD, wscale);
+    y->wqkv = gen_mat(seed, sid(S_WQKV, l, 0), (size_t)NQKV, c->H, wscale, c->wdtype);
+    y->wo = gen_mat(seed, sid(S_WO, l, 0), (size_t)c->H, c->NH * c->HD, wscale, c->wdtype);
     if (c->moe) {
       y->wr = gen_tensor(seed, sid(S_ROUTER, l, 0), (size_t)c->E * c->H, wscale);
-      y->w13 = (uint16_t**)calloc((size_t)c->E, sizeof(uint16_t*));
-      y->w2 = (uint16_t**)calloc((size_t)c->E, sizeof(uint16_t*));
+      y->w13 = (orc_mat*)calloc((size_t)c->E, sizeof(orc_mat));
+      y->w2 = (orc_mat*)calloc((size_t)c->E, sizeof(orc_mat));
     } else {
-      y->wgu = gen_tensor(seed, sid(S_WGU, l, 0), (size_t)2 * c->I * c->H, wscale);
-      y->wd = gen_tensor(seed, sid(S_WD, l, 0), (size_t)c->H * c->I, wscale);
+      y->wgu = gen_mat(seed, sid(S_WGU, l, 0), (size_t)2 * c->I, c->H, wscale, c->wdtype);
+      y->wd = gen_mat(seed, sid(S_WD, l, 0), (size_t)c->H, c->I, wscale, c->wdtype);
     }
     y->kc = (uint16_t*)calloc(kvn, sizeof(uint16_t));
     y->vc = (uint16_t*)calloc(kvn, sizeof(uint16_t));
@@ -394,8 +487,8 @@ EXPORT void orc_model_destroy(void* h) {
   if (!m) return;
   for (int l = 0; l < m->c.L; ++l) {
     orc_layer* y = &m->ly[l];
-    free(y->wqkv); free(y->wo); free(y->wr); free(y->wgu); free(y->wd); free(y->kc); free(y->vc);
-    if (y->w13) for (int e = 0; e < m->c.E; ++e) { free(y->w13[e]); free(y->w2[e]); }
+    free_mat(&y->wqkv); free_mat(&y->wo); free(y->wr); free_mat(&y->wgu); free_mat(&y->wd); free(y->kc); free(y->vc);
+    if (y->w13) for (int e = 0; e < m->c.E; ++e) { free_mat(&y->w13[e]); free_mat(&y->w2[e]); }
     free(y->w13); free(y->w2);
   }
   free(m->ly); free(m->embed); free(m->lm_head); free(m->btab); free(m->rcos); free(m->rsin); free(m);
@@ -437,10 +530,15 @@ EXPORT void orc_fill_kv_random(void* h, int n) { orc_fill_kv_random_seq(h, 0, n)
 static void ensure_expert(orc_model* m, int l, int e) {
   const orc_config* c = &m->c;
   orc_layer* y = &m->ly[l];
-  if (!y->w13[e]) y->w13[e] = gen_tensor(m->seed, sid(S_W13, l, e), (size_t)2 * c->MI * c->H, m->scale);
-  if (!y->w2[e]) y->w2[e] = gen_tensor(m->seed, sid(S_W2, l, e), (size_t)c->H * c->MI, m->scale);
+  if (!y->w13[e].w && !y->w13[e].q) y->w13[e] = gen_mat(m->seed, sid(S_W13, l, e), (size_t)2 * c->MI, c->H, m->scale, c->wdtype);
+  if (!y->w2[e].w && !y->w2[e].q) y->w2[e] = gen_mat(m->seed, sid(S_W2, l, e), (size_t)c->H, c->MI, m->scale, c->wdtype);
 }
 
+/* GEMV rows [0, R) of a weight matrix into out, rounding each to bf16 */
+static void gemv_mat(const orc_mat* W, int wdtype, int R, int K, const float* x, float* out) {
+#pragma omp parallel for schedule(static)
+  for (int r = 0; r < R; ++r) out[r] = bfr(mat_dot(W, wdtype, (size_t)r, x, K));
+}
 /* GEMV rows [0, R) into out, rounding each to bf16 */
 static void gemv_bf(const uint16_t* W, int R, int K, const float* x, float* out) {
 #pragma omp parallel for schedule(static)
@@ -459,7 +557,8 @@ static void layer_step(orc_model* m, int l, float* x, int pos, const int32_t* bt
   float* qkv = (float*)malloc(sizeof(float) * (size_t)NQKV);
   float* o = (float*)malloc(sizeof(float) * (size_t)NH * HD);
   rmsnorm(x, NULL, H, c->eps, xs);                                 /* input_layernorm (weight 1.0) */
-  gemv_bf(y->wqkv, NQKV, H, xs, qkv);                               /* :112-115 */
+  const int wt = c->wdtype;
+  gemv_mat(&y->wqkv, wt, NQKV, H, xs, qkv);                         /* :112-115 */
   const float* cs = m->rcos + (size_t)pos * (HD / 2);
   const float* sn = m->rsin + (size_t)pos * (HD / 2);
   float tmp[512];
@@ -478,7 +577,7 @@ static void layer_step(orc_model* m, int l, float* x, int pos, const int32_t* bt
   for (int hh = 0; hh < NH; ++hh)                                   /* :122-129 */
     attention_head(qkv + (size_t)hh * HD, y->kc, y->vc, bt, pos + 1, hh / G, NKV, HD, BS, o + (size_t)hh * HD);
   float* t = (float*)malloc(sizeof(float) * (size_t)(H > c->I ? H : c->I) * 2 + 64);
-  gemv_bf(y->wo, H, NH * HD, o, t);                                 /* :130 */
+  gemv_mat(&y->wo, wt, H, NH * HD, o, t);                           /* :130 */
   for (int i = 0; i < H; ++i) x[i] = bfr(x[i] + t[i]);
   rmsnorm(x, NULL, H, c->eps, xs);                                 /* :131 post_attention_layernorm */
   if (c->moe) {
@@ -498,17 +597,17 @@ static void layer_step(orc_model* m, int l, float* x, int pos, const int32_t* bt
     float* hbuf = (float*)malloc(sizeof(float) * (size_t)K * MI);
     float* ys = (float*)malloc(sizeof(float) * (size_t)K * H);
     for (int k = 0; k < K; ++k) {                                    /* :142-146 */
-      const uint16_t* W13 = y->w13[ids[k]];
+      const orc_mat* W13 = &y->w13[ids[k]];
       float* hk = hbuf + (size_t)k * MI;
 #pragma omp parallel for schedule(static)
       for (int j = 0; j < MI; ++j) {
-        const float g = bfr(dot64(W13 + (size_t)(2 * j) * H, xs, H));
-        const float u = bfr(dot64(W13 + (size_t)(2 * j + 1) * H, xs, H));
+        const float g = bfr(mat_dot(W13, wt, (size_t)(2 * j), xs, H));
+        const float u = bfr(mat_dot(W13, wt, (size_t)(2 * j + 1), xs, H));
         hk[j] = bfr(bfr(silu(g)) * u);
       }
-      const uint16_t* W2 = y->w2[ids[k]];
+      const orc_mat* W2 = &y->w2[ids[k]];
 #pragma omp parallel for schedule(static)
-      for (int i = 0; i < H; ++i) ys[(size_t)k * H + i] = bfr(bfr(dot64(W2 + (size_t)i * MI, hk, MI)) * wts[k]);
+      for (int i = 0; i < H; ++i) ys[(size_t)k * H + i] = bfr(bfr(mat_dot(W2, wt, (size_t)i, hk, MI)) * wts[k]);
     }
     for (int i = 0; i < H; ++i) {                                    /* :146-148 */
       float acc = 0.0f;
@@ -521,11 +620,11 @@ static void layer_step(orc_model* m, int l, float* x, int pos, const int32_t* bt
     float* hb = (float*)malloc(sizeof(float) * (size_t)I);
 #pragma omp parallel for schedule(static)
     for (int j = 0; j < I; ++j) {
-      const float g = bfr(dot64(y->wgu + (size_t)(2 * j) * H, xs, H));
-      const float u = bfr(dot64(y->wgu + (size_t)(2 * j + 1) * H, xs, H));
+      const float g = bfr(mat_dot(&y->wgu, wt, (size_t)(2 * j), xs, H));
+      const float u = bfr(mat_dot(&y->wgu, wt, (size_t)(2 * j + 1), xs, H));
       hb[j] = bfr(bfr(silu(g)) * u);
     }
-    gemv_bf(y->wd, H, I, hb, t);
+    gemv_mat(&y->wd, wt, H, I, hb, t);
     for (int i = 0; i < H; ++i) x[i] = bfr(x[i] + t[i]);
     free(hb);
   }
@@ -578,20 +677,34 @@ EXPORT void orc_materialize_experts(void* h) {
     for (int e = 0; e < m->c.E; ++e) ensure_expert(m, l, e);
 }
 
-/* raw weight access for tests (natural layout); expert tensors are generated on first use */
+static const orc_mat* mat_of(orc_model* m, int kind, int l, int e) {
+  switch (kind) {
+    case S_WQKV: return &m->ly[l].wqkv;
+    case S_WO: return &m->ly[l].wo;
+    case S_W13: ensure_expert(m, l, e); return &m->ly[l].w13[e];
+    case S_W2: ensure_expert(m, l, e); return &m->ly[l].w2[e];
+    case S_WGU: return &m->ly[l].wgu;
+    case S_WD: return &m->ly[l].wd;
+    default: return NULL;
+  }
+}
+/* raw weight access for tests (natural layout); expert tensors are generated on first use.  bf16 rows (NULL for
+ * a matrix held as fp8), or the e4m3 rows and per-row scales of an fp8 matrix (NULL otherwise). */
 EXPORT const uint16_t* orc_weight(void* h, int kind, int l, int e) {
   orc_model* m = (orc_model*)h;
   switch (kind) {
     case S_EMBED: return m->embed;
     case S_LMHEAD: return m->lm_head;
-    case S_WQKV: return m->ly[l].wqkv;
-    case S_WO: return m->ly[l].wo;
     case S_ROUTER: return m->ly[l].wr;
-    case S_W13: ensure_expert(m, l, e); return m->ly[l].w13[e];
-    case S_W2: ensure_expert(m, l, e); return m->ly[l].w2[e];
-    case S_WGU: return m->ly[l].wgu;
-    case S_WD: return m->ly[l].wd;
-    default: return NULL;
+    default: { const orc_mat* w = mat_of(m, kind, l, e); return w ? w->w : NULL; }
   }
+}
+EXPORT const uint8_t* orc_weight_q(void* h, int kind, int l, int e) {
+  const orc_mat* w = mat_of((orc_model*)h, kind, l, e);
+  return w ? w->q : NULL;
+}
+EXPORT const float* orc_weight_scale(void* h, int kind, int l, int e) {
+  const orc_mat* w = mat_of((orc_model*)h, kind, l, e);
+  return w ? w->s : NULL;
 }
 EXPORT int orc_num_threads(void) { return omp_get_max_threads(); }

@@ -24,7 +24,10 @@ S_EMBED, S_LMHEAD, S_WQKV, S_WO, S_ROUTER, S_W13, S_W2, S_WGU, S_WD, S_KINIT, S_
 class OrcConfig(C.Structure):
     _fields_ = [(n, C.c_int32) for n in ("H", "NH", "NKV", "HD", "I", "E", "TOPK", "MI", "L", "V",
                                           "moe", "qk_norm", "norm_topk", "block_size", "max_ctx", "batch")] + \
-               [("eps", C.c_float), ("theta", C.c_float)]
+               [("eps", C.c_float), ("theta", C.c_float), ("wdtype", C.c_int32)]
+
+# weight types: bf16; fp8 e4m3 rows with per-row fp32 scales; (oracle only) fp8 dequantised into bf16 before the dot
+W_BF16, W_FP8, W_FP8_DEQ = 0, 1, 2
 
 
 def build(force: bool = False) -> Path:
@@ -42,7 +45,8 @@ def lib():
         if not LIB.exists():
             build()
         L = C.CDLL(str(LIB))
-        u16p, f32p, i32p = (np.ctypeslib.ndpointer(t, flags="C_CONTIGUOUS") for t in (np.uint16, np.float32, np.int32))
+        u16p, f32p, i32p, u8p = (np.ctypeslib.ndpointer(t, flags="C_CONTIGUOUS")
+                                 for t in (np.uint16, np.float32, np.int32, np.uint8))
         sig = {
             "orc_splitmix64": (C.c_uint64, [C.c_uint64, C.c_uint64]),
             "orc_stream_key": (C.c_uint64, [C.c_uint64, C.c_uint64]),
@@ -55,6 +59,12 @@ def lib():
             "orc_gen_normal_f32": (None, [C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint64, f32p]),
             "orc_gen_tokens": (None, [C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint32, i32p]),
             "orc_dot64": (C.c_float, [u16p, f32p, C.c_int]),
+            "orc_dot64_q": (C.c_float, [u8p, f32p, C.c_int]),
+            "orc_e4m3_to_f32": (C.c_float, [C.c_uint8]),
+            "orc_f32_to_e4m3": (C.c_uint8, [C.c_float]),
+            "orc_quantize_rows": (None, [u16p, C.c_int64, C.c_int, u8p, f32p]),
+            "orc_weight_q": (C.POINTER(C.c_uint8), [C.c_void_p, C.c_int, C.c_int, C.c_int]),
+            "orc_weight_scale": (C.POINTER(C.c_float), [C.c_void_p, C.c_int, C.c_int, C.c_int]),
             "orc_sum64": (C.c_float, [f32p, C.c_int]),
             "orc_rmsnorm": (None, [f32p, C.c_void_p, C.c_int, C.c_float, f32p]),
             "orc_rope_tables": (None, [C.c_float, C.c_int, C.c_int, f32p, f32p]),
@@ -167,7 +177,7 @@ class OracleModel:
 
     def __init__(self, cfg: dict, seed: int, wscale: float = 0.02):
         self.cfg = dict(cfg)
-        c = OrcConfig(**{k: cfg[k] for k, _ in OrcConfig._fields_})
+        c = OrcConfig(**{k: cfg.get(k, 0) if k == "wdtype" else cfg[k] for k, _ in OrcConfig._fields_})
         self._h = lib().orc_model_create(C.byref(c), seed, wscale)
         if not self._h:
             raise MemoryError("oracle model allocation failed")
@@ -212,6 +222,20 @@ class OracleModel:
         shp = shape or shapes[kind]
         p = lib().orc_weight(self._h, kind, layer, expert)
         return np.ctypeslib.as_array(p, shape=(int(np.prod(shp)),)).reshape(shp).copy()
+
+    def weight_fp8(self, kind: int, layer: int = -1, expert: int = 0):
+        """(e4m3 codes [rows][cols] uint8, per-row scales [rows] fp32) of a matrix the model holds as fp8."""
+        c = self.cfg
+        H, NQKV = c["H"], (c["NH"] + 2 * c["NKV"]) * c["HD"]
+        shapes = {S_WQKV: (NQKV, H), S_WO: (H, c["NH"] * c["HD"]), S_W13: (2 * c["MI"], H), S_W2: (H, c["MI"]),
+                  S_WGU: (2 * c["I"], H), S_WD: (H, c["I"])}
+        R, K = shapes[kind]
+        q = lib().orc_weight_q(self._h, kind, layer, expert)
+        sc = lib().orc_weight_scale(self._h, kind, layer, expert)
+        if not q or not sc:
+            raise ValueError(f"tensor kind {kind} is not held as fp8")
+        return (np.ctypeslib.as_array(q, shape=(R * K,)).reshape(R, K).copy(),
+                np.ctypeslib.as_array(sc, shape=(R,)).copy())
 
     def step(self, tok: int, pos: int, dump: bool = False, seq: int = 0):
         """Sequence `seq`'s decode step (a batched step is one call per sequence: they share only weights)."""

@@ -65,3 +65,27 @@ def test_unpermute_inverts_the_lane_permutation():
                 lane, e = divmod(p, m)
                 stored[:, base + p] = nat[:, base + lane + 64 * e]
         assert np.array_equal(N.unpermute_rows(stored), nat)
+
+
+def test_fp8_weights_shrink_the_arena():
+    bf, f8 = configs.QWEN3_30B_A3B, configs.with_layers(configs.QWEN3_30B_A3B, 48, wdtype=N.W_FP8)
+    c = bf
+    sb, s8 = N.sizes(bf)["weights"], N.sizes(f8)["weights"]
+    fp8_elems = c.L * ((c.NH + 2 * c.NKV) * c.HD * c.H + c.H * c.NH * c.HD + c.E * 3 * c.MI * c.H)
+    fp8_rows = c.L * ((c.NH + 2 * c.NKV) * c.HD + c.H + c.E * (2 * c.MI + c.H))
+    # every fp8 element saves one byte; every fp8 row gains its 16-byte scale slot (up to 256-byte padding per tensor)
+    assert abs((sb - s8) - (fp8_elems - 16 * fp8_rows)) < 256 * 8 * c.L
+
+
+@pytest.mark.parametrize("bad", [dict(wdtype=2), dict(wdtype=-1)])
+def test_unknown_weight_type_refused(bad):
+    with pytest.raises(N.EtxmkError) as e:
+        N.sizes(N.ModelConfig(**dict(configs.TINY_MOE.as_dict(), **bad)))
+    assert e.value.code == N.EINVAL
+
+
+def test_fp8_needs_a_persistent_kernel():
+    # Qwen3-8B's dense rows (12288) have no fp8 kernel: refused, not run wrongly
+    with pytest.raises(N.EtxmkError) as e:
+        N.sizes(configs.with_layers(configs.QWEN3_8B, 36, wdtype=N.W_FP8))
+    assert e.value.code == N.EINVAL and "fp8" in str(e.value)

@@ -46,7 +46,9 @@ def check_pool(cfg, dec, orc):
 def run_contexts(cfg, ctx, n_steps, shuffle=False, check_every=1, pool=True):
     """Sequence b holds ctx[b] cached positions (seeded KV), reads one seeded token at position ctx[b], then decodes
     greedily for n_steps positions; every step is one batched launch."""
+    import time
     B = cfg.batch
+    t0 = time.time()
     say(f"[gpu] batch {B} {cfg.name}: contexts {list(ctx)}, {n_steps} steps, shuffled={shuffle}")
     dec = N.Decoder(cfg)
     dec.init_weights(SEED, 0.02)
@@ -62,6 +64,8 @@ def run_contexts(cfg, ctx, n_steps, shuffle=False, check_every=1, pool=True):
         row = np.zeros(int(ctx[b]) + 1, np.int32)
         row[-1] = first[b]
         dec.set_tokens(row, seq=b)
+        if cfg.L > 2:
+            say(f"[gpu]   sequence {b}: {int(ctx[b])} cached positions filled ({time.time() - t0:.0f}s)")
     dec.enable_dumps(True)
     toks = [[int(first[b])] for b in range(B)]
     pos = np.asarray(ctx, np.int32).copy()
@@ -78,6 +82,8 @@ def run_contexts(cfg, ctx, n_steps, shuffle=False, check_every=1, pool=True):
             else:
                 t = orc.step(toks[b][-1], int(pos[b]), seq=b)
             toks[b].append(t)
+            if cfg.L > 2:
+                say(f"[gpu]   step {s} sequence {b}: oracle token {t} ({time.time() - t0:.0f}s)")
         pos += 1
     dec.sync()
     for b in range(B):
