@@ -130,8 +130,19 @@ def main_batch(a):
     # distinct routed experts per layer, from one more (untimed) step with the routing dumps on
     dec.enable_dumps(True)
     dec.step_batch(pos)
+    pos += 1
     d = dec.dumps()
     dec.enable_dumps(False)
+    phase_us = None
+    if a.trace:
+        dec.enable_trace(True)
+        dec.step_batch(pos)
+        pos += 1
+        t = dec.trace()
+        dec.enable_trace(False)
+        if a.trace_out:
+            np.save(a.trace_out, t)
+        phase_us = trace_summary(t, cfg)
     union = [len(np.unique(d["ids"][l])) for l in range(cfg.L)]
     mean_ctx = (first_timed + pos - 1) / 2.0
     by = bytes_per_step(cfg, np.round(mean_ctx).astype(int), union)
@@ -156,6 +167,8 @@ def main_batch(a):
                      "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None, "kernel": "etxmk_fused_b*"},
         "cpu_baseline": None,
     }
+    if phase_us:
+        out["phase_us"] = phase_us
     print(json.dumps(out), flush=True)
 
 
