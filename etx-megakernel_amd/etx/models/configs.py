@@ -9,7 +9,7 @@ from __future__ import annotations
 import json
 from pathlib import Path
 
-from etx.runtime.native import ModelConfig
+from etx.runtime.native import ARCH_DSV2, ModelConfig
 
 QWEN3_8B = ModelConfig(name="qwen3-8b", H=4096, NH=32, NKV=8, HD=128, L=36, V=151936, I=12288,
                        moe=0, qk_norm=1, eps=1e-6, theta=1e6, max_ctx=1088)
@@ -23,7 +23,25 @@ TINY_MOE = ModelConfig(name="tiny-moe", H=512, NH=4, NKV=2, HD=128, L=2, V=4096,
 TINY_DENSE = ModelConfig(name="tiny-dense", H=512, NH=4, NKV=2, HD=128, L=2, V=4096, I=1024,
                          moe=0, qk_norm=1, max_ctx=256)
 
-CONFIGS = {c.name: c for c in (QWEN3_8B, QWEN3_30B_A3B, QWEN3_8B_LAYER, TINY_MOE, TINY_DENSE)}
+# DeepSeek-V2-Lite (the shapes of its HF config, which the reference's MLA host uses):
+# MLA with kv_lora 512, qk_nope 128, qk_rope 64, v_head 128 and no q LoRA; layer 0 dense (10944), then 64 routed
+# experts top-6 (softmax, not renormalised, scaling 1.0) plus 2 shared, each 1408 wide; yarn RoPE factor 40 over
+# 4096 positions (beta 32 / 1, mscale 0.707 for both).  HD is the query head dim (qk_nope + qk_rope).
+DEEPSEEK_V2_LITE = ModelConfig(name="deepseek-v2-lite", H=2048, NH=16, NKV=1, HD=192, L=27, V=102400, E=64, TOPK=6,
+                               MI=1408, moe=1, qk_norm=0, norm_topk=0, eps=1e-6, theta=1e4, max_ctx=2112,
+                               arch=ARCH_DSV2, kv_lora=512, qk_nope=128, qk_rope=64, v_head=128, n_shared=2,
+                               first_dense=1, dense_I=10944, routed_scale=1.0, rope_factor=40.0, rope_mscale=0.707,
+                               rope_mscale_all=0.707, beta_fast=32.0, beta_slow=1.0, rope_orig_max=4096)
+# a tiny MLA decoder for the oracle checks: the real head dims, fewer heads and experts, a 960-wide dense layer 0
+# (its rows are padded to 1024 on the device)
+TINY_MLA = ModelConfig(name="tiny-mla", H=512, NH=4, NKV=1, HD=192, L=3, V=4096, E=16, TOPK=6, MI=256, moe=1,
+                       qk_norm=0, norm_topk=0, eps=1e-6, theta=1e4, max_ctx=256, arch=ARCH_DSV2, kv_lora=512,
+                       qk_nope=128, qk_rope=64, v_head=128, n_shared=2, first_dense=1, dense_I=960, routed_scale=1.0,
+                       rope_factor=40.0, rope_mscale=0.707, rope_mscale_all=0.707, beta_fast=32.0, beta_slow=1.0,
+                       rope_orig_max=4096)
+
+CONFIGS = {c.name: c for c in (QWEN3_8B, QWEN3_30B_A3B, QWEN3_8B_LAYER, TINY_MOE, TINY_DENSE, DEEPSEEK_V2_LITE,
+                               TINY_MLA)}
 
 
 def with_layers(cfg: ModelConfig, L: int, **kw) -> ModelConfig:

@@ -38,10 +38,15 @@ class DeviceAbort(EtxmkError):
 class EtxmkConfig(C.Structure):
     _fields_ = [(n, C.c_int32) for n in ("H", "NH", "NKV", "HD", "I", "E", "TOPK", "MI", "L", "V",
                                           "moe", "qk_norm", "norm_topk", "block_size", "max_ctx", "batch")] + \
-               [("eps", C.c_float), ("theta", C.c_float), ("wdtype", C.c_int32)]
+               [("eps", C.c_float), ("theta", C.c_float), ("wdtype", C.c_int32), ("arch", C.c_int32)] + \
+               [(n, C.c_int32) for n in ("kv_lora", "qk_nope", "qk_rope", "v_head", "n_shared", "first_dense",
+                                         "dense_I")] + \
+               [(n, C.c_float) for n in ("routed_scale", "rope_factor", "rope_mscale", "rope_mscale_all", "beta_fast",
+                                         "beta_slow")] + [("rope_orig_max", C.c_int32)]
 
 
 W_BF16, W_FP8 = 0, 1          # weight types of etxmk_config.wdtype
+ARCH_QWEN3, ARCH_DSV2 = 0, 1  # etxmk_config.arch
 
 
 @dataclass(frozen=True)
@@ -66,6 +71,22 @@ class ModelConfig:
     eps: float = 1e-6
     theta: float = 1e6
     wdtype: int = W_BF16          # W_FP8: QKV / O / MLP matrices as e4m3 with per-row scales
+    # DeepSeek-V2 (arch = ARCH_DSV2): multi-head latent attention, shared experts, leading dense layers, yarn RoPE
+    arch: int = ARCH_QWEN3
+    kv_lora: int = 0
+    qk_nope: int = 0
+    qk_rope: int = 0
+    v_head: int = 0
+    n_shared: int = 0
+    first_dense: int = 0
+    dense_I: int = 0
+    routed_scale: float = 1.0
+    rope_factor: float = 1.0
+    rope_mscale: float = 1.0
+    rope_mscale_all: float = 1.0
+    beta_fast: float = 32.0
+    beta_slow: float = 1.0
+    rope_orig_max: int = 4096
     name: str = field(default="custom", compare=False)
 
     def as_struct(self) -> EtxmkConfig:
@@ -78,6 +99,9 @@ class ModelConfig:
 
     @property
     def nqkv(self) -> int:
+        """Rows of the fused input projection: Q, K, V heads, or (DeepSeek-V2) q_proj and kv_a_proj_with_mqa."""
+        if self.arch == ARCH_DSV2:
+            return self.NH * (self.qk_nope + self.qk_rope) + self.kv_lora + self.qk_rope
         return (self.NH + 2 * self.NKV) * self.HD
 
 

@@ -53,6 +53,14 @@ typedef struct etxmk_config {
   int32_t moe, qk_norm, norm_topk, block_size, max_ctx, batch;
   float eps, theta;
   int32_t wdtype;               /* ETXMK_W_BF16, or ETXMK_W_FP8 */
+  /* ETXMK_ARCH_DSV2 (DeepSeek-V2): multi-head latent attention (kv_lora, qk_nope, qk_rope,
+   * v_head; HD = qk_nope + qk_rope; NKV unused), n_shared shared experts of width MI, first_dense leading dense
+   * layers of width dense_I, routing weights times routed_scale, yarn RoPE (theta, rope_* and beta_*) */
+  int32_t arch;
+  int32_t kv_lora, qk_nope, qk_rope, v_head;
+  int32_t n_shared, first_dense, dense_I;
+  float routed_scale, rope_factor, rope_mscale, rope_mscale_all, beta_fast, beta_slow;
+  int32_t rope_orig_max;
 } etxmk_config;
 
 /* Weight types.  ETXMK_W_FP8: the QKV, O, expert (gate/up, down) and dense MLP matrices are stored as OCP e4m3
@@ -62,6 +70,10 @@ typedef struct etxmk_config {
  * examples/glm53/cpu_check.py:93-98 (per tensor there; per output channel here). */
 #define ETXMK_W_BF16 0
 #define ETXMK_W_FP8 1
+
+/* Architectures: Qwen3 (GQA, QK-norm) and DeepSeek-V2 (MLA) */
+#define ETXMK_ARCH_QWEN3 0
+#define ETXMK_ARCH_DSV2 1
 
 typedef struct etxmk_handle etxmk_handle;
 

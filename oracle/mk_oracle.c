@@ -20,6 +20,12 @@
  *                    mathematically the softmax of ref_numpy.py:122-129.
  *   softmax sums     over experts: the dot64 accumulator pattern with plain adds.
  *   exp              mk_expf below: Cody-Waite reduction by ln2 and a degree-7 Taylor polynomial.
+ *   DeepSeek-V2      (arch 1) the absorbed multi-head latent attention, yarn RoPE with the
+ *                    DeepSeek interleave, fp32 router with unnormalised top-k, shared experts and leading dense layers
+ *                    of the reference's MLA decode specification
+ *                    (examples/dsv2lite/results/2026-10-14-k1/b_alld4r0l1kvs_stamps/fleet_src/host/reference_decode.py,
+ *                    a third-party snapshot the reference keeps: :78-118 yarn, :120-136 RoPE, :210-256 attention,
+ *                    :259-291 MLP and MoE, :294-302 layer), with the fixed orders of mla_layer_step below.
  *   fp8 weights      (wdtype 1) the QKV, O, expert and dense MLP matrices are held as OCP
  *                    e4m3 with one fp32 scale per output row, quantised from the seeded bf16 rows: s = amax / 448,
  *                    q = e4m3(w / s) rounded to nearest even and saturated at +-448.  A matvec row is
@@ -386,11 +392,16 @@ typedef struct {
   int32_t moe, qk_norm, norm_topk, block_size, max_ctx, batch;
   float eps, theta;
   int32_t wdtype;                 /* 0 bf16 weights; 1 fp8 e4m3 + per-row scales; 2 fp8 dequantised to bf16 */
+  int32_t arch;                   /* 0 Qwen3; 1 DeepSeek-V2 (MLA, shared experts, leading dense layers) */
+  int32_t kv_lora, qk_nope, qk_rope, v_head;
+  int32_t n_shared, first_dense, dense_I;
+  float routed_scale, rope_factor, rope_mscale, rope_mscale_all, beta_fast, beta_slow;
+  int32_t rope_orig_max;
 } orc_config;
 
 /* tensor streams of the seeded generator: kind << 48 | (layer + 1) << 24 | expert */
 enum { S_EMBED = 1, S_LMHEAD = 2, S_WQKV = 3, S_WO = 4, S_ROUTER = 5, S_W13 = 6, S_W2 = 7, S_WGU = 8, S_WD = 9,
-       S_KINIT = 10, S_VINIT = 11, S_XIN = 12, S_PROMPT = 13 };
+       S_KINIT = 10, S_VINIT = 11, S_XIN = 12, S_PROMPT = 13, S_WKVB = 14, S_WSGU = 15, S_WSD = 16 };
 static inline uint64_t sid(int kind, int layer, int expert) {
   return ((uint64_t)kind << 48) | ((uint64_t)(layer + 1) << 24) | (uint64_t)expert;
 }
@@ -404,10 +415,12 @@ typedef struct {
 } orc_mat;
 
 typedef struct {
-  orc_mat wqkv, wo, wgu, wd;
+  orc_mat wqkv, wo, wgu, wd;      /* DeepSeek-V2: wqkv = [q_proj; kv_a_proj_with_mqa] */
   uint16_t* wr;                   /* the router stays bf16 */
   orc_mat *w13, *w2;              /* per expert, generated on first use */
-  uint16_t *kc, *vc;
+  uint16_t* wkvb;                 /* DeepSeek-V2 kv_b_proj [NH * (qk_nope + v_head)][kv_lora] */
+  orc_mat wsgu, wsd;              /* DeepSeek-V2 shared experts: gate/up interleaved, down */
+  uint16_t *kc, *vc;              /* DeepSeek-V2: kc is the latent cache [blk][(kv_lora + qk_rope)/8][BS][8] */
 } orc_layer;
 
 typedef struct {
@@ -417,8 +430,9 @@ typedef struct {
   orc_layer* ly;
   int32_t* btab;                  /* [batch][nbps]: sequence b's logical block i -> physical block */
   int nblocks, nbps, batch;
-  float *rcos, *rsin;
+  float *rcos, *rsin;             /* DeepSeek-V2: fp32 yarn tables [max_ctx][qk_rope / 2] */
   float scale;
+  float attn_scale;
 } orc_model;
 
 static uint16_t* gen_tensor(uint64_t seed, uint64_t stream, size_t n, float scale) {
@@ -446,10 +460,13 @@ static inline float mat_dot(const orc_mat* m, int wdtype, size_t r, const float*
   return dot64_deq(m->q + r * K, m->s[r], x, K);
 }
 
+static void* mla_model_create(orc_model* m);
+
 EXPORT void* orc_model_create(const orc_config* cfg, uint64_t seed, float wscale) {
   orc_model* m = (orc_model*)calloc(1, sizeof(orc_model));
   m->c = *cfg; m->seed = seed; m->scale = wscale;
   const orc_config* c = &m->c;
+  if (c->arch == 1) return mla_model_create(m);
   const int NQKV = (c->NH + 2 * c->NKV) * c->HD;
   m->embed = gen_tensor(seed, sid(S_EMBED, -1, 0), (size_t)c->V * c->H, wscale);
   m->lm_head = gen_tensor(seed, sid(S_LMHEAD, -1, 0), (size_t)c->V * c->H, wscale);
@@ -488,6 +505,7 @@ EXPORT void orc_model_destroy(void* h) {
   for (int l = 0; l < m->c.L; ++l) {
     orc_layer* y = &m->ly[l];
     free_mat(&y->wqkv); free_mat(&y->wo); free(y->wr); free_mat(&y->wgu); free_mat(&y->wd); free(y->kc); free(y->vc);
+    free(y->wkvb); free_mat(&y->wsgu); free_mat(&y->wsd);
     if (y->w13) for (int e = 0; e < m->c.E; ++e) { free_mat(&y->w13[e]); free_mat(&y->w2[e]); }
     free(y->w13); free(y->w2);
   }
@@ -508,8 +526,10 @@ EXPORT const uint16_t* orc_vcache(void* h, int layer) { return ((orc_model*)h)->
 /* fill positions [0, n) of sequence `seq`'s cache in every layer with bf16 N(0,1) (the single-layer
  * configuration; the batched workloads' contexts): element (t, h, d) is number (t*NKV + h)*HD + d of the
  * layer's K / V stream for that sequence */
+EXPORT void orc_fill_latent_random_seq(void* h, int seq, int n);
 EXPORT void orc_fill_kv_random_seq(void* h, int seq, int n) {
   orc_model* m = (orc_model*)h; const orc_config* c = &m->c;
+  if (c->arch == 1) { orc_fill_latent_random_seq(h, seq, n); return; }
   const int NKV = c->NKV, HD = c->HD, BS = c->block_size;
   const int32_t* bt = m->btab + (size_t)seq * m->nbps;
   for (int l = 0; l < c->L; ++l) {
@@ -526,6 +546,8 @@ EXPORT void orc_fill_kv_random_seq(void* h, int seq, int n) {
   }
 }
 EXPORT void orc_fill_kv_random(void* h, int n) { orc_fill_kv_random_seq(h, 0, n); }
+
+static int mla_cache_dim(const orc_config* c) { return c->kv_lora + c->qk_rope; }
 
 static void ensure_expert(orc_model* m, int l, int e) {
   const orc_config* c = &m->c;
@@ -634,6 +656,9 @@ static void layer_step(orc_model* m, int l, float* x, int pos, const int32_t* bt
 /* ref_numpy.py:105-158 Ref.step for sequence `seq` of the batch: token at position pos -> greedy next token.
  * The sequences of a batch share the weights and nothing else, so a batched step is this, once per sequence.
  * dump_x [L][H] residual after each layer; dump_ids/dump_wts [L][TOPK]; each may be NULL. */
+static void mla_layer_step(orc_model* m, int l, float* x, int pos, const int32_t* bt, int32_t* ids_out, float* wts_out,
+                           float* logits_out);
+
 EXPORT int32_t orc_step_seq(void* h, int seq, int32_t tok, int pos, float* dump_x, int32_t* dump_ids, float* dump_wts) {
   orc_model* m = (orc_model*)h; const orc_config* c = &m->c;
   const int H = c->H;
@@ -641,8 +666,8 @@ EXPORT int32_t orc_step_seq(void* h, int seq, int32_t tok, int pos, float* dump_
   float* x = (float*)malloc(sizeof(float) * (size_t)H);
   for (int i = 0; i < H; ++i) x[i] = bf2f(m->embed[(size_t)tok * H + i]);
   for (int l = 0; l < c->L; ++l) {
-    layer_step(m, l, x, pos, bt, dump_ids ? dump_ids + (size_t)l * c->TOPK : NULL,
-               dump_wts ? dump_wts + (size_t)l * c->TOPK : NULL, NULL);
+    (c->arch == 1 ? mla_layer_step : layer_step)(m, l, x, pos, bt, dump_ids ? dump_ids + (size_t)l * c->TOPK : NULL,
+                                                   dump_wts ? dump_wts + (size_t)l * c->TOPK : NULL, NULL);
     if (dump_x) memcpy(dump_x + (size_t)l * H, x, sizeof(float) * (size_t)H);
   }
   float* xs = (float*)malloc(sizeof(float) * (size_t)H);
@@ -663,7 +688,8 @@ EXPORT int32_t orc_step(void* h, int32_t tok, int pos, float* dump_x, int32_t* d
 EXPORT void orc_layer_step_seq(void* h, int seq, int l, float* x, int pos, int32_t* ids_out, float* wts_out,
                                float* logits_out) {
   orc_model* m = (orc_model*)h;
-  layer_step(m, l, x, pos, m->btab + (size_t)seq * m->nbps, ids_out, wts_out, logits_out);
+  (m->c.arch == 1 ? mla_layer_step : layer_step)(m, l, x, pos, m->btab + (size_t)seq * m->nbps, ids_out, wts_out,
+                                                 logits_out);
 }
 EXPORT void orc_layer_step(void* h, int l, float* x, int pos, int32_t* ids_out, float* wts_out, float* logits_out) {
   orc_layer_step_seq(h, 0, l, x, pos, ids_out, wts_out, logits_out);
@@ -685,6 +711,8 @@ static const orc_mat* mat_of(orc_model* m, int kind, int l, int e) {
     case S_W2: ensure_expert(m, l, e); return &m->ly[l].w2[e];
     case S_WGU: return &m->ly[l].wgu;
     case S_WD: return &m->ly[l].wd;
+    case S_WSGU: return &m->ly[l].wsgu;
+    case S_WSD: return &m->ly[l].wsd;
     default: return NULL;
   }
 }
@@ -696,6 +724,7 @@ EXPORT const uint16_t* orc_weight(void* h, int kind, int l, int e) {
     case S_EMBED: return m->embed;
     case S_LMHEAD: return m->lm_head;
     case S_ROUTER: return m->ly[l].wr;
+    case S_WKVB: return m->ly[l].wkvb;
     default: { const orc_mat* w = mat_of(m, kind, l, e); return w ? w->w : NULL; }
   }
 }
@@ -708,3 +737,289 @@ EXPORT const float* orc_weight_scale(void* h, int kind, int l, int e) {
   return w ? w->s : NULL;
 }
 EXPORT int orc_num_threads(void) { return omp_get_max_threads(); }
+
+/* ================================================================== DeepSeek-V2 (arch 1) */
+/* yarn_get_mscale (reference_decode.py:78-83) */
+static double yarn_mscale(double scale, double mscale) { return scale <= 1.0 ? 1.0 : 0.1 * mscale * log(scale) + 1.0; }
+
+/* DeepseekV2YarnRotaryEmbedding tables (reference_decode.py:85-118) in the float32 steps the reference's numpy takes:
+ * correction range in float64, ramp / mask / frequencies / products in float32, then cos and sin (libm) times the
+ * mscale ratio (1.0 when mscale == mscale_all_dim).  Only the first half is stored (emb = cat(freqs, freqs)). */
+EXPORT void orc_yarn_tables(const orc_config* c, int ctx, float* cs, float* sn) {
+  const int dim = c->qk_rope, half = dim / 2;
+  const double base = c->theta, two_pi = 2.0 * 3.141592653589793;
+  const double lowd = (dim * log(c->rope_orig_max / (c->beta_fast * two_pi))) / (2.0 * log(base));
+  const double highd = (dim * log(c->rope_orig_max / (c->beta_slow * two_pi))) / (2.0 * log(base));
+  int low = (int)floor(lowd), high = (int)ceil(highd);
+  if (low < 0) low = 0;
+  if (high > dim - 1) high = dim - 1;
+  const float span = low == high ? (float)((double)high + 0.001 - (double)low) : (float)(high - low);
+  const float ms = (float)(yarn_mscale(c->rope_factor, c->rope_mscale) / yarn_mscale(c->rope_factor, c->rope_mscale_all));
+  float inv[256];
+  for (int i = 0; i < half; ++i) {
+    const float e = (float)(2 * i) / (float)dim;
+    const float pw = powf((float)base, e);
+    const float extra = 1.0f / pw, inter = 1.0f / ((float)c->rope_factor * pw);
+    float ramp = ((float)i - (float)low) / span;
+    ramp = ramp < 0.0f ? 0.0f : ramp > 1.0f ? 1.0f : ramp;
+    const float mask = 1.0f - ramp;
+    inv[i] = inter * (1.0f - mask) + extra * mask;
+  }
+  for (int t = 0; t < ctx; ++t)
+    for (int i = 0; i < half; ++i) {
+      const float f = (float)t * inv[i];
+      cs[(size_t)t * half + i] = cosf(f) * ms;
+      sn[(size_t)t * half + i] = sinf(f) * ms;
+    }
+}
+
+/* DeepSeek-V2 RoPE (reference_decode.py:120-136): de-interleave (x0, x2, ..., x1, x3, ...), then rotate_half:
+ * out[i] = x[2i] c_i - x[2i+1] s_i, out[i + d/2] = x[2i+1] c_i + x[2i] s_i, each product and sum in fp32; bfr after */
+static void rope_ds(const float* x, int d, const float* cs, const float* sn, float* out) {
+  const int half = d / 2;
+  for (int i = 0; i < half; ++i) {
+    const float a = x[2 * i], b = x[2 * i + 1];
+    out[i] = bfr(a * cs[i] + (-b) * sn[i]);
+    out[i + half] = bfr(b * cs[i] + a * sn[i]);
+  }
+}
+EXPORT void orc_rope_ds(const float* x, int d, const float* cs, const float* sn, float* out) { rope_ds(x, d, cs, sn, out); }
+
+static void* mla_model_create(orc_model* m) {
+  const orc_config* c = &m->c;
+  const uint64_t seed = m->seed;
+  const float ws = m->scale;
+  const int NH = c->NH, QD = c->qk_nope + c->qk_rope, KVL = c->kv_lora, CD = mla_cache_dim(c);
+  const int NQA = NH * QD + KVL + c->qk_rope;
+  m->embed = gen_tensor(seed, sid(S_EMBED, -1, 0), (size_t)c->V * c->H, ws);
+  m->lm_head = gen_tensor(seed, sid(S_LMHEAD, -1, 0), (size_t)c->V * c->H, ws);
+  m->batch = c->batch > 1 ? c->batch : 1;
+  m->nbps = (c->max_ctx + c->block_size - 1) / c->block_size;
+  m->nblocks = m->batch * m->nbps;
+  m->btab = (int32_t*)malloc(sizeof(int32_t) * (size_t)m->nblocks);
+  for (int i = 0; i < m->nblocks; ++i) m->btab[i] = i;
+  m->ly = (orc_layer*)calloc((size_t)c->L, sizeof(orc_layer));
+  for (int l = 0; l < c->L; ++l) {
+    orc_layer* y = &m->ly[l];
+    y->wqkv = gen_mat(seed, sid(S_WQKV, l, 0), (size_t)NQA, c->H, ws, c->wdtype);
+    y->wo = gen_mat(seed, sid(S_WO, l, 0), (size_t)c->H, NH * c->v_head, ws, c->wdtype);
+    y->wkvb = gen_tensor(seed, sid(S_WKVB, l, 0), (size_t)NH * (c->qk_nope + c->v_head) * KVL, ws);
+    if (l < c->first_dense) {
+      y->wgu = gen_mat(seed, sid(S_WGU, l, 0), (size_t)2 * c->dense_I, c->H, ws, c->wdtype);
+      y->wd = gen_mat(seed, sid(S_WD, l, 0), (size_t)c->H, c->dense_I, ws, c->wdtype);
+    } else {
+      y->wr = gen_tensor(seed, sid(S_ROUTER, l, 0), (size_t)c->E * c->H, ws);
+      y->w13 = (orc_mat*)calloc((size_t)c->E, sizeof(orc_mat));
+      y->w2 = (orc_mat*)calloc((size_t)c->E, sizeof(orc_mat));
+      y->wsgu = gen_mat(seed, sid(S_WSGU, l, 0), (size_t)2 * c->n_shared * c->MI, c->H, ws, c->wdtype);
+      y->wsd = gen_mat(seed, sid(S_WSD, l, 0), (size_t)c->H, c->n_shared * c->MI, ws, c->wdtype);
+    }
+    y->kc = (uint16_t*)calloc((size_t)m->nblocks * c->block_size * CD, sizeof(uint16_t));
+  }
+  const int half = c->qk_rope / 2;
+  m->rcos = (float*)malloc(sizeof(float) * (size_t)c->max_ctx * half);
+  m->rsin = (float*)malloc(sizeof(float) * (size_t)c->max_ctx * half);
+  orc_yarn_tables(c, c->max_ctx, m->rcos, m->rsin);
+  /* softmax_scale (reference_decode.py:198-206): q_head_dim^-0.5 * mscale_all^2, applied as fp32 */
+  const double mm = yarn_mscale(c->rope_factor, c->rope_mscale_all);
+  m->attn_scale = (float)(pow((double)QD, -0.5) * mm * mm);
+  return m;
+}
+EXPORT float orc_attn_scale(void* h) { return ((orc_model*)h)->attn_scale; }
+
+/* canonical dot of a row zero-padded to a multiple of 128 elements (the device stores such rows padded): one more
+ * fma(0, 0, acc) per lane when K % 128 == 64 */
+static inline float dot64_pad(const orc_mat* m, int wdtype, size_t r, const float* x, int K) {
+  if (K % 128 == 0) return mat_dot(m, wdtype, r, x, K);
+  float acc[64];
+  for (int l = 0; l < 64; ++l) acc[l] = 0.0f;
+  for (int k0 = 0; k0 < K; k0 += 64)
+    for (int l = 0; l < 64; ++l) {
+      const float w = wdtype == 0 ? bf2f(m->w[r * K + k0 + l]) : e4m3_to_f32(m->q[r * K + k0 + l]);
+      acc[l] = fmaf(w, x[k0 + l], acc[l]);
+    }
+  for (int l = 0; l < 64; ++l) acc[l] = fmaf(0.0f, 0.0f, acc[l]);
+  const float d = butterfly64(acc);
+  return wdtype == 0 ? d : d * m->s[r];
+}
+
+/* one MLA head over positions 0..n-1 of the latent cache (reference_decode.py:250-253 in chunked form):
+ * s_t = ((q_c . c_t over kv_lora, ascending fma) + (q_pe . kpe_t over qk_rope, ascending fma)) * scale; chunks of 64
+ * with m_c, p = expf(s - m_c), l_c and a_c[i] = sum_t p_t c_t[i] as ascending fma chains; merge as attention_head;
+ * o_c = A / L in fp32 (not rounded: the reference keeps o_c fp32 into W_UV) */
+static void mla_head(const float* q_c, const float* q_pe, const uint16_t* kc, const int32_t* bt, int n, int KVL, int R,
+                     int BS, float scale, float* o_c) {
+  const int CD = KVL + R;
+  float A[1024], a[1024], mc[256];
+  float L = 0.0f, M = -INFINITY;
+  const int nch = (n + ATT_CHUNK - 1) / ATT_CHUNK;
+  float* sc = (float*)malloc(sizeof(float) * (size_t)n);
+  for (int t = 0; t < n; ++t) {
+    const int blk = bt[t / BS], off = t % BS;
+    float s1 = 0.0f, s2 = 0.0f;
+    for (int i = 0; i < KVL; ++i) s1 = fmaf(q_c[i], bf2f(kc[kv_k_index(blk, off, 0, i, 1, CD, BS)]), s1);
+    for (int j = 0; j < R; ++j) s2 = fmaf(q_pe[j], bf2f(kc[kv_k_index(blk, off, 0, KVL + j, 1, CD, BS)]), s2);
+    sc[t] = (s1 + s2) * scale;
+  }
+  for (int c = 0; c < nch; ++c) {
+    float m = -INFINITY;
+    for (int t = c * ATT_CHUNK; t < n && t < (c + 1) * ATT_CHUNK; ++t) if (sc[t] > m) m = sc[t];
+    mc[c] = m;
+    if (m > M) M = m;
+  }
+  for (int i = 0; i < KVL; ++i) A[i] = 0.0f;
+  for (int c = 0; c < nch; ++c) {
+    float l = 0.0f;
+    for (int i = 0; i < KVL; ++i) a[i] = 0.0f;
+    for (int t = c * ATT_CHUNK; t < n && t < (c + 1) * ATT_CHUNK; ++t) {
+      const int blk = bt[t / BS], off = t % BS;
+      const float p = mk_expf(sc[t] - mc[c]);
+      l = l + p;
+      for (int i = 0; i < KVL; ++i) a[i] = fmaf(p, bf2f(kc[kv_k_index(blk, off, 0, i, 1, CD, BS)]), a[i]);
+    }
+    const float w = mk_expf(mc[c] - M);
+    L = fmaf(w, l, L);
+    for (int i = 0; i < KVL; ++i) A[i] = fmaf(w, a[i], A[i]);
+  }
+  for (int i = 0; i < KVL; ++i) o_c[i] = A[i] / L;
+  free(sc);
+}
+
+/* the router of DeepSeek-V2 (reference_decode.py:271-278): fp32 softmax of the fp32 logits, top-k by probability
+ * (ties to the lower id), weights = probability * routed_scale (or renormalised when norm_topk), kept in fp32 */
+static void route_ds(const float* logits, int E, int K, int renorm, float rscale, int32_t* ids, float* wts) {
+  float M = -INFINITY;
+  for (int e = 0; e < E; ++e) if (logits[e] > M) M = logits[e];
+  float p[1024];
+  for (int e = 0; e < E; ++e) p[e] = mk_expf(logits[e] - M);
+  const float S = sum64(p, E);
+  for (int e = 0; e < E; ++e) p[e] = p[e] / S;
+  unsigned char taken[1024] = {0};
+  float sel = 0.0f, wv[64];
+  for (int k = 0; k < K; ++k) {
+    int bi = -1; float bv = -1.0f;
+    for (int e = 0; e < E; ++e) if (!taken[e] && p[e] > bv) { bv = p[e]; bi = e; }
+    taken[bi] = 1; ids[k] = bi; wv[k] = bv; sel = sel + bv;
+  }
+  for (int k = 0; k < K; ++k) wts[k] = renorm ? wv[k] / (sel + 1e-20f) : wv[k] * rscale;
+}
+EXPORT void orc_route_ds(const float* logits, int E, int K, int renorm, float rscale, int32_t* ids, float* wts) {
+  route_ds(logits, E, K, renorm, rscale, ids, wts);
+}
+
+/* one DeepSeek-V2 decoder layer (reference_decode.py:294-302) at position pos on residual x (in place) */
+static void mla_layer_step(orc_model* m, int l, float* x, int pos, const int32_t* bt, int32_t* ids_out, float* wts_out,
+                           float* logits_out) {
+  const orc_config* c = &m->c;
+  orc_layer* y = &m->ly[l];
+  const int H = c->H, NH = c->NH, NOPE = c->qk_nope, R = c->qk_rope, VH = c->v_head, KVL = c->kv_lora, BS = c->block_size;
+  const int QD = NOPE + R, NQA = NH * QD + KVL + R, CD = KVL + R, wt = c->wdtype;
+  const int W = H > c->dense_I ? H : c->dense_I;
+  float* xs = (float*)malloc(sizeof(float) * (size_t)(W + 128));
+  float* qa = (float*)malloc(sizeof(float) * (size_t)NQA);
+  float* out = (float*)malloc(sizeof(float) * (size_t)NH * VH);
+  float* t = (float*)malloc(sizeof(float) * (size_t)H);
+  rmsnorm(x, NULL, H, c->eps, xs);                                  /* :222 input_layernorm (weight 1.0) */
+  gemv_mat(&y->wqkv, wt, NQA, H, xs, qa);                           /* :225, :229 q_proj, kv_a_proj (bf16) */
+  const float* cs = m->rcos + (size_t)pos * (R / 2);
+  const float* sn = m->rsin + (size_t)pos * (R / 2);
+  float cnew[1024], kpe[256];
+  rmsnorm(qa + NH * QD, NULL, KVL, c->eps, cnew);                   /* :231 kv_a_layernorm (weight 1.0) */
+  rope_ds(qa + NH * QD + KVL, R, cs, sn, kpe);                      /* :234 */
+  const int blk = bt[pos / BS], off = pos % BS;                     /* :236-237 append the latent row */
+  for (int i = 0; i < KVL; ++i) y->kc[kv_k_index(blk, off, 0, i, 1, CD, BS)] = f2bf(cnew[i]);
+  for (int j = 0; j < R; ++j) y->kc[kv_k_index(blk, off, 0, KVL + j, 1, CD, BS)] = f2bf(kpe[j]);
+#pragma omp parallel for schedule(static)
+  for (int h = 0; h < NH; ++h) {                                    /* :245-254 per head, absorbed */
+    const float* q = qa + (size_t)h * QD;
+    float qpe[256], q_c[1024], o_c[1024];
+    rope_ds(q + NOPE, R, cs, sn, qpe);                               /* :235 */
+    /* q_c[i] = sum_d q_nope[d] * W_UK[h][d][i]: the canonical dot of column i of W_UK (kv_b rows h*(NOPE+VH)+d) */
+    const uint16_t* wuk = y->wkvb + (size_t)h * (NOPE + VH) * KVL;
+    for (int i = 0; i < KVL; ++i) {
+      uint16_t colb[512];
+      for (int d = 0; d < NOPE; ++d) colb[d] = wuk[(size_t)d * KVL + i];
+      q_c[i] = dot64(colb, q, NOPE);
+    }
+    mla_head(q_c, qpe, y->kc, bt, pos + 1, KVL, R, BS, m->attn_scale, o_c);
+    const uint16_t* wuv = wuk + (size_t)NOPE * KVL;                  /* :254 out[h] = W_UV o_c, bf16 at :256 */
+    for (int d = 0; d < VH; ++d) out[(size_t)h * VH + d] = bfr(dot64(wuv + (size_t)d * KVL, o_c, KVL));
+  }
+  gemv_mat(&y->wo, wt, H, NH * VH, out, t);                         /* :256 o_proj, bf16 */
+  for (int i = 0; i < H; ++i) x[i] = bfr(x[i] + t[i]);              /* :300 residual */
+  rmsnorm(x, NULL, H, c->eps, xs);                                  /* :301 post_attention_layernorm */
+  if (l < c->first_dense) {                                         /* :290-291 dense MLP */
+    const int I = c->dense_I, IP = (I + 127) / 128 * 128;
+    float* hb = (float*)calloc((size_t)IP, sizeof(float));
+#pragma omp parallel for schedule(static)
+    for (int j = 0; j < I; ++j) {
+      const float g = bfr(mat_dot(&y->wgu, wt, (size_t)(2 * j), xs, H));
+      const float u = bfr(mat_dot(&y->wgu, wt, (size_t)(2 * j + 1), xs, H));
+      hb[j] = bfr(bfr(silu(g)) * u);
+    }
+#pragma omp parallel for schedule(static)
+    for (int i = 0; i < H; ++i) t[i] = bfr(dot64_pad(&y->wd, wt, (size_t)i, hb, I));
+    for (int i = 0; i < H; ++i) x[i] = bfr(x[i] + t[i]);
+    free(hb);
+  } else {                                                          /* :268-287 MoE */
+    const int E = c->E, K = c->TOPK, MI = c->MI, SI = c->n_shared * MI;
+    float logits[1024];
+#pragma omp parallel for schedule(static)
+    for (int e = 0; e < E; ++e) logits[e] = dot64(y->wr + (size_t)e * H, xs, H);   /* :271 fp32 router, not rounded */
+    if (logits_out) memcpy(logits_out, logits, sizeof(float) * (size_t)E);
+    int32_t ids[64]; float wts[64];
+    route_ds(logits, E, K, c->norm_topk, c->routed_scale, ids, wts);
+    if (ids_out) memcpy(ids_out, ids, sizeof(int32_t) * (size_t)K);
+    if (wts_out) memcpy(wts_out, wts, sizeof(float) * (size_t)K);
+    for (int k = 0; k < K; ++k) ensure_expert(m, l, ids[k]);
+    int order[64];                                                  /* y summed in ascending expert id */
+    for (int k = 0; k < K; ++k) order[k] = k;
+    for (int a = 1; a < K; ++a)
+      for (int b = a; b > 0 && ids[order[b]] < ids[order[b - 1]]; --b) { int q = order[b]; order[b] = order[b - 1]; order[b - 1] = q; }
+    float* hk = (float*)malloc(sizeof(float) * (size_t)(SI > MI ? SI : MI));
+    float* ys = (float*)malloc(sizeof(float) * (size_t)K * H);
+    for (int k = 0; k < K; ++k) {                                   /* :281-284, mlp_unit :259-265 */
+      const orc_mat* W13 = &y->w13[ids[k]];
+#pragma omp parallel for schedule(static)
+      for (int j = 0; j < MI; ++j) {
+        const float g = bfr(mat_dot(W13, wt, (size_t)(2 * j), xs, H));
+        const float u = bfr(mat_dot(W13, wt, (size_t)(2 * j + 1), xs, H));
+        hk[j] = bfr(bfr(silu(g)) * u);
+      }
+      const orc_mat* W2 = &y->w2[ids[k]];
+#pragma omp parallel for schedule(static)
+      for (int i = 0; i < H; ++i) ys[(size_t)k * H + i] = bfr(wts[k] * bfr(dot64_pad(W2, wt, (size_t)i, hk, MI)));
+    }
+#pragma omp parallel for schedule(static)
+    for (int j = 0; j < SI; ++j) {                                  /* :286 shared experts */
+      const float g = bfr(mat_dot(&y->wsgu, wt, (size_t)(2 * j), xs, H));
+      const float u = bfr(mat_dot(&y->wsgu, wt, (size_t)(2 * j + 1), xs, H));
+      hk[j] = bfr(bfr(silu(g)) * u);
+    }
+#pragma omp parallel for schedule(static)
+    for (int i = 0; i < H; ++i) {
+      float acc = 0.0f;                                             /* :280-284 fp32 sum of the rounded terms */
+      for (int k = 0; k < K; ++k) acc = acc + ys[(size_t)order[k] * H + i];
+      const float sh = bfr(dot64_pad(&y->wsd, wt, (size_t)i, hk, SI));
+      t[i] = bfr(bfr(acc) + sh);                                    /* :287 */
+    }
+    for (int i = 0; i < H; ++i) x[i] = bfr(x[i] + t[i]);            /* :302 */
+    free(hk); free(ys);
+  }
+  free(xs); free(qa); free(out); free(t);
+}
+
+/* fill positions [0, n) of sequence seq's latent cache in every layer with bf16 N(0,1): element (t, i) is number
+ * t*CD + i of the layer's stream (kind 10) for that sequence */
+EXPORT void orc_fill_latent_random_seq(void* h, int seq, int n) {
+  orc_model* m = (orc_model*)h; const orc_config* c = &m->c;
+  const int CD = mla_cache_dim(c), BS = c->block_size;
+  const int32_t* bt = m->btab + (size_t)seq * m->nbps;
+  for (int l = 0; l < c->L; ++l) {
+    const uint64_t kk = stream_key(m->seed, sid(S_KINIT, l, seq));
+#pragma omp parallel for schedule(static)
+    for (int t = 0; t < n; ++t)
+      for (int i = 0; i < CD; ++i)
+        m->ly[l].kc[kv_k_index(bt[t / BS], t % BS, 0, i, 1, CD, BS)] = f2bf(mk_normal(kk, (uint64_t)t * CD + i));
+  }
+}

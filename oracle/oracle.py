@@ -24,7 +24,14 @@ S_EMBED, S_LMHEAD, S_WQKV, S_WO, S_ROUTER, S_W13, S_W2, S_WGU, S_WD, S_KINIT, S_
 class OrcConfig(C.Structure):
     _fields_ = [(n, C.c_int32) for n in ("H", "NH", "NKV", "HD", "I", "E", "TOPK", "MI", "L", "V",
                                           "moe", "qk_norm", "norm_topk", "block_size", "max_ctx", "batch")] + \
-               [("eps", C.c_float), ("theta", C.c_float), ("wdtype", C.c_int32)]
+               [("eps", C.c_float), ("theta", C.c_float), ("wdtype", C.c_int32), ("arch", C.c_int32)] + \
+               [(n, C.c_int32) for n in ("kv_lora", "qk_nope", "qk_rope", "v_head", "n_shared", "first_dense",
+                                         "dense_I")] + \
+               [(n, C.c_float) for n in ("routed_scale", "rope_factor", "rope_mscale", "rope_mscale_all", "beta_fast",
+                                         "beta_slow")] + [("rope_orig_max", C.c_int32)]
+
+ARCH_QWEN3, ARCH_DSV2 = 0, 1
+S_WKVB, S_WSGU, S_WSD = 14, 15, 16
 
 # weight types: bf16; fp8 e4m3 rows with per-row fp32 scales; (oracle only) fp8 dequantised into bf16 before the dot
 W_BF16, W_FP8, W_FP8_DEQ = 0, 1, 2
@@ -64,6 +71,10 @@ def lib():
             "orc_f32_to_e4m3": (C.c_uint8, [C.c_float]),
             "orc_quantize_rows": (None, [u16p, C.c_int64, C.c_int, u8p, f32p]),
             "orc_weight_q": (C.POINTER(C.c_uint8), [C.c_void_p, C.c_int, C.c_int, C.c_int]),
+            "orc_yarn_tables": (None, [C.c_void_p, C.c_int, f32p, f32p]),
+            "orc_rope_ds": (None, [f32p, C.c_int, f32p, f32p, f32p]),
+            "orc_attn_scale": (C.c_float, [C.c_void_p]),
+            "orc_route_ds": (None, [f32p, C.c_int, C.c_int, C.c_int, C.c_float, i32p, f32p]),
             "orc_weight_scale": (C.POINTER(C.c_float), [C.c_void_p, C.c_int, C.c_int, C.c_int]),
             "orc_sum64": (C.c_float, [f32p, C.c_int]),
             "orc_rmsnorm": (None, [f32p, C.c_void_p, C.c_int, C.c_float, f32p]),
@@ -177,7 +188,7 @@ class OracleModel:
 
     def __init__(self, cfg: dict, seed: int, wscale: float = 0.02):
         self.cfg = dict(cfg)
-        c = OrcConfig(**{k: cfg.get(k, 0) if k == "wdtype" else cfg[k] for k, _ in OrcConfig._fields_})
+        c = OrcConfig(**{k: cfg.get(k, 0) for k, _ in OrcConfig._fields_})
         self._h = lib().orc_model_create(C.byref(c), seed, wscale)
         if not self._h:
             raise MemoryError("oracle model allocation failed")
@@ -207,7 +218,11 @@ class OracleModel:
         lib().orc_fill_kv_random_seq(self._h, int(seq), int(n))
 
     def kv(self, layer: int):
+        """(K, V) of one layer's paged pool, flat; DeepSeek-V2: (latent cache [blk][CD/8][BS][8], None)."""
         c = self.cfg
+        if c.get("arch", 0) == ARCH_DSV2:
+            n = self.num_blocks * c["block_size"] * (c["kv_lora"] + c["qk_rope"])
+            return np.ctypeslib.as_array(lib().orc_kcache(self._h, layer), shape=(n,)).copy(), None
         n = self.num_blocks * c["block_size"] * c["NKV"] * c["HD"]
         k = np.ctypeslib.as_array(lib().orc_kcache(self._h, layer), shape=(n,)).copy()
         v = np.ctypeslib.as_array(lib().orc_vcache(self._h, layer), shape=(n,)).copy()
@@ -219,9 +234,19 @@ class OracleModel:
         shapes = {S_EMBED: (c["V"], H), S_LMHEAD: (c["V"], H), S_WQKV: (NQKV, H), S_WO: (H, c["NH"] * c["HD"]),
                   S_ROUTER: (c["E"], H), S_W13: (2 * c["MI"], H), S_W2: (H, c["MI"]),
                   S_WGU: (2 * c["I"], H), S_WD: (H, c["I"])}
+        if c.get("arch", 0) == ARCH_DSV2:
+            NH, QD, KVL, R = c["NH"], c["qk_nope"] + c["qk_rope"], c["kv_lora"], c["qk_rope"]
+            SI = c["n_shared"] * c["MI"]
+            shapes.update({S_WQKV: (NH * QD + KVL + R, H), S_WO: (H, NH * c["v_head"]),
+                           S_WKVB: (NH * (c["qk_nope"] + c["v_head"]), KVL), S_WSGU: (2 * SI, H), S_WSD: (H, SI),
+                           S_WGU: (2 * c["dense_I"], H), S_WD: (H, c["dense_I"])})
         shp = shape or shapes[kind]
         p = lib().orc_weight(self._h, kind, layer, expert)
         return np.ctypeslib.as_array(p, shape=(int(np.prod(shp)),)).reshape(shp).copy()
+
+    @property
+    def attn_scale(self) -> float:
+        return float(lib().orc_attn_scale(self._h))
 
     def weight_fp8(self, kind: int, layer: int = -1, expert: int = 0):
         """(e4m3 codes [rows][cols] uint8, per-row scales [rows] fp32) of a matrix the model holds as fp8."""
@@ -262,6 +287,22 @@ class OracleModel:
         lg = np.zeros(max(c["E"], 1), np.float32)
         lib().orc_layer_step_seq(self._h, int(seq), layer, x, pos, ids.ctypes.data, w.ctypes.data, lg.ctypes.data)
         return x, ids, w, lg
+
+
+def yarn_tables(cfg: dict, ctx: int):
+    """The oracle's fp32 yarn cos / sin tables [ctx][qk_rope / 2] of a DeepSeek-V2 configuration."""
+    c = OrcConfig(**{k: cfg.get(k, 0) for k, _ in OrcConfig._fields_})
+    half = cfg["qk_rope"] // 2
+    cs, sn = np.zeros(ctx * half, np.float32), np.zeros(ctx * half, np.float32)
+    lib().orc_yarn_tables(C.addressof(c), ctx, cs, sn)
+    return cs.reshape(ctx, half), sn.reshape(ctx, half)
+
+
+def rope_ds(x: np.ndarray, cs: np.ndarray, sn: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.zeros_like(x)
+    lib().orc_rope_ds(x, len(x), np.ascontiguousarray(cs, np.float32), np.ascontiguousarray(sn, np.float32), out)
+    return out
 
 
 def num_threads() -> int:
