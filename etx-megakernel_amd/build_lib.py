@@ -24,7 +24,8 @@ FLAGS = [
     "-Wno-unused-command-line-argument",
 ]
 # translation units: the host side (C ABI, unfused and initialisation kernels) and one per persistent-kernel list
-UNITS = ["mk_api.hip", "mk_fused_bf16.hip", "mk_fused_fp8.hip", "mk_batch_bf16.hip", "mk_batch_fp8.hip"]
+UNITS = ["mk_api.hip", "mk_fused_bf16.hip", "mk_fused_fp8.hip", "mk_batch_bf16.hip", "mk_batch_fp8.hip",
+         "mk_mla.hip"]
 
 
 def build(verbose: bool = False) -> Path:

@@ -13,8 +13,8 @@
 #include <vector>
 
 #include "etxmk.h"
-#include "mk_batch.h"
 #include "mk_init.h"
+#include "mk_mla.h"
 
 namespace mk {
 // the persistent kernels live in their own translation units (mk_fused_*.hip, mk_batch_*.hip)
@@ -22,6 +22,7 @@ MK_FUSED_SHAPES_BF16(MK_FUSED_DECL)
 MK_FUSED_SHAPES_FP8(MK_FUSED_DECL)
 MK_BATCH_SHAPES_BF16(MK_BATCH_DECL)
 MK_BATCH_SHAPES_FP8(MK_BATCH_DECL)
+MK_DS_SHAPES(MK_DS_DECL)
 
 // unfused mode (bf16 weights)
 MK_PHASE_KERNEL(etxmk_p_qkv, phase_qkv_any(p, layer, s, NoWait{}))
@@ -65,6 +66,9 @@ struct TensorSlot {
   int rows, cols, perm;      // perm: rows stored lane-permuted
   int fp8;                   // rows in Fp8Row format (codes + scale, cols + 16 bytes) instead of bf16
   uint64_t off;              // byte offset of tensor 0
+  int lcols = 0;             // logical row length when the stored rows are padded (0: cols)
+  int split = 0;             // DeepSeek-V2 kv_b_proj: stored as W_UK^T then W_UV (etxmk_pack_kvb)
+  int logical_cols() const { return lcols ? lcols : cols; }
   uint64_t row_bytes() const { return fp8 ? (uint64_t)cols + 16 : 2ull * cols; }
   uint64_t tensor_bytes() const { return (uint64_t)rows * row_bytes(); }
 };
@@ -84,6 +88,26 @@ bool k_in(int k, std::initializer_list<int> ks) {
   for (int v : ks)
     if (k == v) return true;
   return false;
+}
+
+bool is_ds(const etxmk_config& c) { return c.arch == ETXMK_ARCH_DSV2; }
+// DeepSeek-V2 derived sizes: fused q_proj + kv_a rows, shared width, dense width rounded up to whole 512 blocks
+int ds_nqa(const etxmk_config& c) { return c.NH * (c.qk_nope + c.qk_rope) + c.kv_lora + c.qk_rope; }
+int ds_si(const etxmk_config& c) { return c.n_shared * c.MI; }
+int ds_ip(const etxmk_config& c) { return (c.dense_I + 511) / 512 * 512; }
+int ds_nhg(const etxmk_config& c) { return c.NH < MLA_G ? 1 : c.NH / MLA_G; }
+// rows of the fused QKV matrix
+int nqkv_of(const etxmk_config& c) { return is_ds(c) ? ds_nqa(c) : (c.NH + 2 * c.NKV) * c.HD; }
+
+// the DeepSeek-V2 persistent kernel for this shape, or nullptr
+const void* ds_kernel(const etxmk_config& c) {
+#define MK_PICK_DS(name, h_, ka_, km_, ksh_, e_, ip_, b_)                                                          \
+  if (c.H == h_ && c.NH * c.v_head == ka_ && c.MI == km_ && ds_si(c) == ksh_ && c.E == e_ &&                     \
+      (c.first_dense == 0 || ds_ip(c) == ip_) && c.batch <= b_)                                                   \
+    return (const void*)name;
+  MK_DS_SHAPES(MK_PICK_DS)
+#undef MK_PICK_DS
+  return nullptr;
 }
 
 // the single-sequence persistent kernel instantiated for this shape and weight type, or nullptr
@@ -117,9 +141,36 @@ const void* batch_kernel(const etxmk_config& c) {
   return best;
 }
 
+// DeepSeek-V2 (multi-head latent attention): the kernel is built for DeepSeek-V2's head dimensions, bf16 weights,
+// block sizes whose 16-position groups share a block, and up to MAX_B_DS sequences
+int check_ds(const etxmk_config* c) {
+  if (c->kv_lora != MLA_KVL || c->qk_nope != MLA_NOPE || c->qk_rope != MLA_R || c->v_head != MLA_VH)
+    return fail(ETXMK_EINVAL, "MLA dims (kv_lora %d, qk_nope %d, qk_rope %d, v_head %d) unsupported (built for %d/%d/%d/%d)",
+                c->kv_lora, c->qk_nope, c->qk_rope, c->v_head, MLA_KVL, MLA_NOPE, MLA_R, MLA_VH);
+  if (c->HD != MLA_QD) return fail(ETXMK_EINVAL, "head_dim %d must be qk_nope + qk_rope = %d", c->HD, MLA_QD);
+  if (c->NH > MLA_MAX_NH || (c->NH > MLA_G && c->NH % MLA_G)) return fail(ETXMK_EINVAL, "%d heads unsupported", c->NH);
+  if (!c->moe || c->E <= 0 || c->E > MAX_E || c->E % 4 || c->TOPK <= 0 || c->TOPK > MAX_TOPK || c->TOPK > c->E)
+    return fail(ETXMK_EINVAL, "experts %d / top-k %d unsupported", c->E, c->TOPK);
+  if (c->n_shared < 1 || c->first_dense < 0 || c->first_dense > c->L || (c->first_dense > 0 && c->dense_I <= 0))
+    return fail(ETXMK_EINVAL, "shared experts %d / dense layers %d of width %d unsupported", c->n_shared, c->first_dense, c->dense_I);
+  if (c->block_size != 16 && c->block_size != 32 && c->block_size != 64)
+    return fail(ETXMK_EINVAL, "block size %d unsupported (16, 32 or 64)", c->block_size);
+  if (c->max_ctx <= 0 || c->max_ctx > MAX_CTX) return fail(ETXMK_EINVAL, "max_ctx %d outside 1..%d", c->max_ctx, MAX_CTX);
+  if (c->batch < 1 || c->batch > MAX_B_DS) return fail(ETXMK_EINVAL, "batch %d outside 1..%d", c->batch, MAX_B_DS);
+  if (c->wdtype != ETXMK_W_BF16) return fail(ETXMK_EINVAL, "DeepSeek-V2 runs bf16 weights only");
+  if (c->rope_factor <= 0.0f || c->rope_orig_max <= 0 || c->beta_fast <= 0.0f || c->beta_slow <= 0.0f)
+    return fail(ETXMK_EINVAL, "yarn RoPE parameters must be positive");
+  if (!ds_kernel(*c))
+    return fail(ETXMK_EINVAL, "no DeepSeek-V2 kernel for H %d, NH %d, MI %d, shared %d, E %d, dense I %d", c->H, c->NH,
+                c->MI, ds_si(*c), c->E, c->dense_I);
+  return ETXMK_OK;
+}
+
 int check_config(const etxmk_config* c) {
   if (!c) return fail(ETXMK_EINVAL, "config is NULL");
   if (c->H <= 0 || c->NH <= 0 || c->NKV <= 0 || c->L <= 0 || c->V <= 0) return fail(ETXMK_EINVAL, "non-positive dimension");
+  if (c->arch != ETXMK_ARCH_QWEN3 && c->arch != ETXMK_ARCH_DSV2) return fail(ETXMK_EINVAL, "architecture %d unknown", c->arch);
+  if (c->arch == ETXMK_ARCH_DSV2) return check_ds(c);
   if (c->HD != HDIM) return fail(ETXMK_EINVAL, "head_dim %d unsupported (the attention phase is built for %d)", c->HD, HDIM);
   if (c->NH % c->NKV) return fail(ETXMK_EINVAL, "NH %d not a multiple of NKV %d", c->NH, c->NKV);
   if (c->NH / c->NKV > MAX_G) return fail(ETXMK_EINVAL, "%d q heads per kv head (at most %d)", c->NH / c->NKV, MAX_G);
@@ -149,11 +200,41 @@ int check_config(const etxmk_config* c) {
 std::vector<TensorSlot> weight_layout(const etxmk_config* c, uint64_t* total) {
   std::vector<TensorSlot> v;
   uint64_t off = 0;
-  auto add = [&](int kind, int layer, int count, int rows, int cols, int perm) {
+  auto add = [&](int kind, int layer, int count, int rows, int cols, int perm, int lcols = 0, int split = 0) {
     TensorSlot t{kind, layer, count, rows, cols, perm, c->wdtype == ETXMK_W_FP8 && fp8_kind(kind) ? 1 : 0, off};
+    t.lcols = lcols;
+    t.split = split;
     v.push_back(t);
     off = align_up(off + (uint64_t)count * t.tensor_bytes());
   };
+  if (c->arch == ETXMK_ARCH_DSV2) {
+    // DeepSeek-V2: kv_a_layernorm in the KNORM slot; WQKV = [q_proj; kv_a_proj_with_mqa]; WKVB = kv_b_proj; the
+    // dense layers' down rows padded to whole 512 blocks
+    add(ETXMK_T_EMBED, -1, 1, c->V, c->H, 0);
+    add(ETXMK_T_LMHEAD, -1, 1, c->V, c->H, 1);
+    add(ETXMK_T_FINAL_NORM, -1, 1, 1, c->H, 0);
+    const int SI = ds_si(*c), IP = ds_ip(*c);
+    for (int l = 0; l < c->L; ++l) {
+      add(ETXMK_T_LN1, l, 1, 1, c->H, 0);
+      add(ETXMK_T_LN2, l, 1, 1, c->H, 0);
+      add(ETXMK_T_KNORM, l, 1, 1, c->kv_lora, 0);
+      add(ETXMK_T_WQKV, l, 1, ds_nqa(*c), c->H, 1);
+      add(ETXMK_T_WKVB, l, 1, c->NH * (c->qk_nope + c->v_head), c->kv_lora, 1, 0, 1);
+      add(ETXMK_T_WO, l, 1, c->H, c->NH * c->v_head, 1);
+      if (l < c->first_dense) {
+        add(ETXMK_T_WGU, l, 1, 2 * c->dense_I, c->H, 1);
+        add(ETXMK_T_WD, l, 1, c->H, IP, 1, c->dense_I);
+      } else {
+        add(ETXMK_T_ROUTER, l, 1, c->E, c->H, 1);
+        add(ETXMK_T_W13, l, c->E, 2 * c->MI, c->H, 1);
+        add(ETXMK_T_W2, l, c->E, c->H, c->MI, 1);
+        add(ETXMK_T_WSGU, l, 1, 2 * SI, c->H, 1);
+        add(ETXMK_T_WSD, l, 1, c->H, SI, 1);
+      }
+    }
+    *total = off;
+    return v;
+  }
   const int NQKV = (c->NH + 2 * c->NKV) * c->HD;
   add(ETXMK_T_EMBED, -1, 1, c->V, c->H, 0);
   add(ETXMK_T_LMHEAD, -1, 1, c->V, c->H, 1);
@@ -182,41 +263,91 @@ std::vector<TensorSlot> weight_layout(const etxmk_config* c, uint64_t* total) {
 int nbps_of(const etxmk_config* c) { return (c->max_ctx + c->block_size - 1) / c->block_size; }
 int nblocks_of(const etxmk_config* c) { return c->batch * nbps_of(c); }
 
-uint64_t kv_layer_elems(const etxmk_config* c) { return (uint64_t)nblocks_of(c) * c->block_size * c->NKV * c->HD; }
+// per layer: K and V pools of this many elements each (DeepSeek-V2: one latent pool)
+uint64_t kv_layer_elems(const etxmk_config* c) {
+  if (c->arch == ETXMK_ARCH_DSV2) return (uint64_t)nblocks_of(c) * c->block_size * MLA_CD;
+  return (uint64_t)nblocks_of(c) * c->block_size * c->NKV * c->HD;
+}
+int kv_pools(const etxmk_config* c) { return c->arch == ETXMK_ARCH_DSV2 ? 1 : 2; }
 
 struct WsLayout {
   uint64_t x, x16, qkv, o, o16, logits, hbuf, h16, apart, acnt, amax, bar, abort_w, tokens, out_tokens, btab, rcos, rsin,
-      layers, total;
+      layers, h16d, qc, cnew, oc, h16s, total;
 };
 
 WsLayout ws_layout(const etxmk_config* c) {
   WsLayout w{};
   uint64_t off = 0;
   auto take = [&](uint64_t bytes) { const uint64_t o = off; off = align_up(off + bytes); return o; };
-  const int NQKV = (c->NH + 2 * c->NKV) * c->HD;
+  const bool ds = c->arch == ETXMK_ARCH_DSV2;
+  const int NQKV = nqkv_of(*c), KA = ds ? c->NH * c->v_head : c->NH * c->HD;
   const uint64_t B = (uint64_t)c->batch;
   w.x = take(4ull * c->H * B);
   w.x16 = take(2ull * c->H * B);
   w.qkv = take(4ull * NQKV * B);
-  w.o = take(4ull * c->NH * c->HD * B);
-  w.o16 = take(2ull * c->NH * c->HD * B);
+  w.o = take(4ull * KA * B);
+  w.o16 = take(2ull * KA * B);
   w.logits = take(4ull * (c->E > 0 ? c->E : 1) * B);
   const int hb = c->moe ? c->TOPK * c->MI : c->I;
   w.hbuf = take(4ull * (hb > 0 ? hb : 1) * B);
   w.h16 = take(2ull * (hb > 0 ? hb : 1) * B);
-  w.apart = take(4ull * c->NH * MAX_CHUNKS * PART * B);
-  w.acnt = take(4ull * 64 * c->NKV * B); // one 256-byte line per (sequence, kv head)
+  w.apart = take(4ull * c->NH * MAX_CHUNKS * (ds ? MLA_PART : PART) * B);
+  w.acnt = take(4ull * 64 * (ds ? ds_nhg(*c) : c->NKV) * B); // one 256-byte line per (sequence, kv head / head group)
   w.amax = take(256ull * B);             // one 256-byte line per sequence
   w.bar = take(4 * 64 * 17);          // 8 group counters, 1 global counter, 8 release flags; 256 B apart
   w.abort_w = take(4);
   w.tokens = take(4ull * (c->max_ctx + 1) * B);
   w.out_tokens = take(4ull * (c->max_ctx + 1) * B);
   w.btab = take(4ull * nblocks_of(c));
-  w.rcos = take(4ull * c->max_ctx * (c->HD / 2));
-  w.rsin = take(4ull * c->max_ctx * (c->HD / 2));
+  const int rhalf = ds ? c->qk_rope / 2 : c->HD / 2;
+  w.rcos = take(4ull * c->max_ctx * rhalf);
+  w.rsin = take(4ull * c->max_ctx * rhalf);
   w.layers = take(sizeof(LayerW) * (uint64_t)c->L);
+  if (ds) {
+    w.h16d = take(2ull * (c->first_dense > 0 ? ds_ip(*c) : 8) * B);
+    w.qc = take(4ull * c->NH * c->kv_lora * B);
+    w.cnew = take(4ull * MLA_CD * B);
+    w.oc = take(4ull * c->NH * c->kv_lora * B);
+    w.h16s = take(2ull * ds_si(*c) * B);
+  } else {
+    w.h16d = w.h16;
+  }
   w.total = off;
   return w;
+}
+
+uint64_t acnt_bytes(const etxmk_config& c) { return 4ull * 64 * (is_ds(c) ? ds_nhg(c) : c.NKV) * c.batch; }
+
+// DeepseekV2YarnRotaryEmbedding tables (reference_decode.py:85-118) in the steps the reference's numpy takes in
+// float32: the correction range in double, the ramp, mask and inverse frequencies in float, then cos and sin of
+// t * inv times the ratio of the two yarn mscales (first half only: emb = cat(freqs, freqs)); kept in fp32
+void yarn_tables(const etxmk_config& c, float* cs, float* sn) {
+  const int dim = c.qk_rope, half = dim / 2;
+  const double base = c.theta, two_pi = 2.0 * 3.141592653589793;
+  auto mscale = [](double scale, double m) { return scale <= 1.0 ? 1.0 : 0.1 * m * log(scale) + 1.0; };
+  const double lowd = (dim * log(c.rope_orig_max / (c.beta_fast * two_pi))) / (2.0 * log(base));
+  const double highd = (dim * log(c.rope_orig_max / (c.beta_slow * two_pi))) / (2.0 * log(base));
+  int low = (int)floor(lowd), high = (int)ceil(highd);
+  if (low < 0) low = 0;
+  if (high > dim - 1) high = dim - 1;
+  const float span = low == high ? (float)((double)high + 0.001 - (double)low) : (float)(high - low);
+  const float ms = (float)(mscale(c.rope_factor, c.rope_mscale) / mscale(c.rope_factor, c.rope_mscale_all));
+  std::vector<float> inv(half);
+  for (int i = 0; i < half; ++i) {
+    const float e = (float)(2 * i) / (float)dim;
+    const float pw = powf((float)base, e);
+    const float extra = 1.0f / pw, inter = 1.0f / ((float)c.rope_factor * pw);
+    float ramp = ((float)i - (float)low) / span;
+    ramp = ramp < 0.0f ? 0.0f : ramp > 1.0f ? 1.0f : ramp;
+    const float mask = 1.0f - ramp;
+    inv[i] = inter * (1.0f - mask) + extra * mask;
+  }
+  for (int t = 0; t < c.max_ctx; ++t)
+    for (int i = 0; i < half; ++i) {
+      const float f = (float)t * inv[i];
+      cs[(size_t)t * half + i] = cosf(f) * ms;
+      sn[(size_t)t * half + i] = sinf(f) * ms;
+    }
 }
 
 }  // namespace
@@ -250,7 +381,14 @@ struct etxmk_handle {
     const TensorSlot* s = slot(kind, layer);
     return s ? (const uint8_t*)(w + s->off) : nullptr;
   }
-  int barriers(int l0, int l1, int head) const { return (c.moe ? 6 : 5) * (l1 - l0) + (head ? 1 : 0); }
+  int barriers(int l0, int l1, int head) const {
+    if (c.arch == ETXMK_ARCH_DSV2) {                       // 5 attention phases, then 2 dense or 3 MoE phases
+      int n = 0;
+      for (int l = l0; l < l1; ++l) n += l < c.first_dense ? 7 : 8;
+      return n + (head ? 1 : 0);
+    }
+    return (c.moe ? 6 : 5) * (l1 - l0) + (head ? 1 : 0);
+  }
 };
 
 extern "C" {
@@ -268,7 +406,7 @@ int etxmk_weight_bytes(const etxmk_config* cfg, uint64_t* bytes) {
 int etxmk_kv_bytes(const etxmk_config* cfg, uint64_t* bytes) {
   if (int r = check_config(cfg)) return r;
   if (!bytes) return fail(ETXMK_EINVAL, "bytes is NULL");
-  *bytes = 2ull * 2ull * kv_layer_elems(cfg) * (uint64_t)cfg->L;
+  *bytes = 2ull * kv_pools(cfg) * kv_layer_elems(cfg) * (uint64_t)cfg->L;
   return ETXMK_OK;
 }
 
@@ -312,6 +450,7 @@ int etxmk_bind(etxmk_handle* h, void* weights, void* kv, void* workspace) {
   // per-layer pointer table
   std::vector<LayerW> lw(c.L);
   const uint64_t kvl = kv_layer_elems(&c);
+  const bool ds = is_ds(c);
   for (int l = 0; l < c.L; ++l) {
     LayerW& y = lw[l];
     y.ln1 = (const uint16_t*)h->wt(ETXMK_T_LN1, l);
@@ -325,20 +464,31 @@ int etxmk_bind(etxmk_handle* h, void* weights, void* kv, void* workspace) {
     y.w2 = h->wt(ETXMK_T_W2, l);
     y.wgu = h->wt(ETXMK_T_WGU, l);
     y.wd = h->wt(ETXMK_T_WD, l);
-    y.kc = (uint16_t*)h->kv + (uint64_t)l * 2 * kvl;
-    y.vc = y.kc + kvl;
+    y.kc = (uint16_t*)h->kv + (uint64_t)l * kv_pools(&c) * kvl;
+    y.vc = ds ? nullptr : y.kc + kvl;
+    if (ds) {
+      const TensorSlot* kvb = h->slot(ETXMK_T_WKVB, l);
+      y.wuk = h->w + kvb->off;
+      y.wuv = y.wuk + 2ull * c.NH * c.kv_lora * c.qk_nope;
+      y.wsgu = h->wt(ETXMK_T_WSGU, l);
+      y.wsd = h->wt(ETXMK_T_WSD, l);
+    }
   }
   HIPCHK(hipMemcpy(h->wsp + h->ws.layers, lw.data(), sizeof(LayerW) * c.L, hipMemcpyHostToDevice));
-  // RoPE tables, bf16 values in fp32 (ref_numpy.py:76-81; host.hip:164-178)
-  const int half = c.HD / 2;
+  const int half = ds ? c.qk_rope / 2 : c.HD / 2;
   std::vector<float> cs((size_t)c.max_ctx * half), sn((size_t)c.max_ctx * half);
-  for (int i = 0; i < half; ++i) {
-    const float inv = 1.0f / powf(c.theta, (float)(2 * i) / (float)c.HD);
-    for (int t = 0; t < c.max_ctx; ++t) {
-      const float f = (float)t * inv;
-      auto rb = [](float x) { uint32_t u; memcpy(&u, &x, 4); u = (u + 0x7FFFu + ((u >> 16) & 1u)) & 0xFFFF0000u; float r; memcpy(&r, &u, 4); return r; };
-      cs[(size_t)t * half + i] = rb(cosf(f));
-      sn[(size_t)t * half + i] = rb(sinf(f));
+  if (ds) {
+    yarn_tables(c, cs.data(), sn.data());
+  } else {
+    // RoPE tables, bf16 values in fp32 (ref_numpy.py:76-81; host.hip:164-178)
+    for (int i = 0; i < half; ++i) {
+      const float inv = 1.0f / powf(c.theta, (float)(2 * i) / (float)c.HD);
+      for (int t = 0; t < c.max_ctx; ++t) {
+        const float f = (float)t * inv;
+        auto rb = [](float x) { uint32_t u; memcpy(&u, &x, 4); u = (u + 0x7FFFu + ((u >> 16) & 1u)) & 0xFFFF0000u; float r; memcpy(&r, &u, 4); return r; };
+        cs[(size_t)t * half + i] = rb(cosf(f));
+        sn[(size_t)t * half + i] = rb(sinf(f));
+      }
     }
   }
   HIPCHK(hipMemcpy(h->wsp + h->ws.rcos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice));
@@ -353,7 +503,8 @@ int etxmk_bind(etxmk_handle* h, void* weights, void* kv, void* workspace) {
   HIPCHK(hipMemset(h->wsp + h->ws.out_tokens, 0, 4ull * (c.max_ctx + 1) * c.batch));
   HIPCHK(hipMemset(h->wsp + h->ws.x, 0, 4ull * c.H * c.batch));
   HIPCHK(hipMemset(h->wsp + h->ws.x16, 0, 2ull * c.H * c.batch));
-  HIPCHK(hipMemset(h->wsp + h->ws.acnt, 0, 4ull * 64 * c.NKV * c.batch));
+  HIPCHK(hipMemset(h->wsp + h->ws.acnt, 0, acnt_bytes(c)));
+  if (ds) HIPCHK(hipMemset(h->wsp + h->ws.h16d, 0, 2ull * (c.first_dense > 0 ? ds_ip(c) : 8) * c.batch));  // zero pads
   h->bar_epoch = 0;
   return ETXMK_OK;
 }
@@ -367,7 +518,7 @@ int etxmk_tensor_info(etxmk_handle* h, int kind, int layer, int expert, uint64_t
   if (expert < 0 || expert >= s->count) return fail(ETXMK_EINVAL, "expert %d outside 0..%d", expert, s->count - 1);
   if (offset) *offset = s->off + (uint64_t)expert * s->tensor_bytes();
   if (rows) *rows = s->rows;
-  if (cols) *cols = s->cols;
+  if (cols) *cols = s->logical_cols();
   if (permuted) *permuted = s->perm;
   return ETXMK_OK;
 }
@@ -406,11 +557,16 @@ int etxmk_init_weights_seeded(etxmk_handle* h, uint64_t seed, float scale, void*
     }
     if (norm) {
       hipLaunchKernelGGL(etxmk_fill_u16, dim3(64), dim3(256), 0, st, dst, n, (uint16_t)0x3F80);
+    } else if (s.split) {
+      const etxmk_config& c = h->c;
+      hipLaunchKernelGGL(etxmk_pack_kvb, dim3((unsigned)((n + 255) / 256 < 65536 ? (n + 255) / 256 : 65536)), dim3(256), 0,
+                         st, dst, (const uint16_t*)nullptr, seed, stream_id(s.kind, s.layer, 0), c.NH, c.qk_nope,
+                         c.v_head, c.kv_lora, scale);
     } else {
       if (n % 8) return fail(ETXMK_EINVAL, "tensor kind %d has %zu elements (not a multiple of 8)", s.kind, n);
       const size_t blocks = (n / 8 + 255) / 256;
       hipLaunchKernelGGL(etxmk_gen_weights, dim3((unsigned)(blocks < 65536 ? blocks : 65536)), dim3(256), 0, st, dst, seed,
-                         stream_id(s.kind, s.layer, 0), s.count, s.rows, s.cols, s.perm, scale);
+                         stream_id(s.kind, s.layer, 0), s.count, s.rows, s.cols, s.logical_cols(), s.perm, scale);
     }
     HIPCHK(hipGetLastError());
   }
@@ -425,11 +581,19 @@ int etxmk_load_tensor(etxmk_handle* h, int kind, int layer, int expert, const vo
   if (!src) return fail(ETXMK_EINVAL, "src is NULL");
   hipStream_t st = (hipStream_t)stream;
   const bool global = kind == ETXMK_T_EMBED || kind == ETXMK_T_LMHEAD || kind == ETXMK_T_FINAL_NORM;
-  if (h->slot(kind, global ? -1 : layer)->fp8) return quantize(h->w + off, (const uint16_t*)src, 0, 0, 1, rows, cols, 0.0f, st);
-  if (perm) {
+  const TensorSlot* ts = h->slot(kind, global ? -1 : layer);
+  if (ts->fp8) return quantize(h->w + off, (const uint16_t*)src, 0, 0, 1, rows, cols, 0.0f, st);
+  if (ts->split) {
+    const etxmk_config& c = h->c;
     const size_t n = (size_t)rows * cols;
+    hipLaunchKernelGGL(etxmk_pack_kvb, dim3((unsigned)((n + 255) / 256 < 65536 ? (n + 255) / 256 : 65536)), dim3(256), 0, st,
+                       (uint16_t*)(h->w + off), (const uint16_t*)src, (uint64_t)0, (uint64_t)0, c.NH, c.qk_nope, c.v_head,
+                       c.kv_lora, 0.0f);
+    HIPCHK(hipGetLastError());
+  } else if (perm) {
+    const size_t n = (size_t)rows * ts->cols;
     hipLaunchKernelGGL(etxmk_pack_rows, dim3((unsigned)((n + 255) / 256 < 65536 ? (n + 255) / 256 : 65536)), dim3(256), 0, st,
-                       (uint16_t*)(h->w + off), (const uint16_t*)src, rows, cols);
+                       (uint16_t*)(h->w + off), (const uint16_t*)src, rows, ts->cols, cols);
     HIPCHK(hipGetLastError());
   } else {
     HIPCHK(hipMemcpyAsync(h->w + off, src, (size_t)rows * cols * 2, hipMemcpyDeviceToDevice, st));
@@ -464,6 +628,17 @@ int etxmk_fill_kv_seeded_seq(etxmk_handle* h, uint64_t seed, int32_t seq, int32_
   if (npos < 0 || npos > c.max_ctx) return fail(ETXMK_EINVAL, "npos %d outside 0..%d", npos, c.max_ctx);
   if (npos == 0) return ETXMK_OK;
   const uint64_t kvl = kv_layer_elems(&c);
+  if (is_ds(c)) {                          // the latent cache (stream kind 10, as the K cache of the Qwen3 path)
+    for (int l = 0; l < c.L; ++l) {
+      uint16_t* kc = (uint16_t*)h->kv + (uint64_t)l * kvl;
+      const size_t n = (size_t)npos * MLA_CD;
+      hipLaunchKernelGGL(etxmk_gen_latent, dim3((unsigned)((n + 255) / 256 < 65536 ? (n + 255) / 256 : 65536)), dim3(256), 0,
+                         (hipStream_t)stream, kc, h->wsptr<const int32_t>(h->ws.btab) + (size_t)seq * nbps_of(&c),
+                         stream_key(seed, stream_id(10, l, seq)), npos, MLA_CD, c.block_size);
+      HIPCHK(hipGetLastError());
+    }
+    return ETXMK_OK;
+  }
   for (int l = 0; l < c.L; ++l) {
     uint16_t* kc = (uint16_t*)h->kv + (uint64_t)l * 2 * kvl;
     const size_t n = (size_t)npos * c.NKV * c.HD;
@@ -512,7 +687,7 @@ int etxmk_read_tokens(etxmk_handle* h, int32_t* out, int32_t n, void* stream) {
 
 int etxmk_set_residual(etxmk_handle* h, const float* x, void* stream) {
   if (!h || !h->wsp) return fail(ETXMK_EUNBOUND, "handle not bound");
-  if (h->c.batch != 1) return fail(ETXMK_EINVAL, "the residual entry points serve single-sequence handles");
+  if (h->c.batch != 1 || is_ds(h->c)) return fail(ETXMK_EINVAL, "the residual entry points serve single-sequence Qwen3 handles");
   if (!x) return fail(ETXMK_EINVAL, "x is NULL");
   HIPCHK(hipMemcpyAsync(h->wsp + h->ws.x, x, 4ull * h->c.H, hipMemcpyHostToDevice, (hipStream_t)stream));
   HIPCHK(hipStreamSynchronize((hipStream_t)stream));
@@ -521,7 +696,7 @@ int etxmk_set_residual(etxmk_handle* h, const float* x, void* stream) {
 
 int etxmk_read_residual(etxmk_handle* h, float* x, void* stream) {
   if (!h || !h->wsp) return fail(ETXMK_EUNBOUND, "handle not bound");
-  if (h->c.batch != 1) return fail(ETXMK_EINVAL, "the residual entry points serve single-sequence handles");
+  if (h->c.batch != 1 || is_ds(h->c)) return fail(ETXMK_EINVAL, "the residual entry points serve single-sequence Qwen3 handles");
   if (!x) return fail(ETXMK_EINVAL, "x is NULL");
   HIPCHK(hipMemcpyAsync(x, h->wsp + h->ws.x, 4ull * h->c.H, hipMemcpyDeviceToHost, (hipStream_t)stream));
   HIPCHK(hipStreamSynchronize((hipStream_t)stream));
@@ -574,9 +749,12 @@ static int launch(etxmk_handle* h, const int32_t* posv, int pos, int write_next,
                   hipStream_t st) {
   if (!h || !h->wsp) return fail(ETXMK_EUNBOUND, "handle not bound");
   const etxmk_config& c = h->c;
-  const bool batched = c.batch > 1;
-  if (batched && !posv) return fail(ETXMK_EINVAL, "a batched handle steps through etxmk_step_batch");
-  if (!batched && posv) pos = posv[0];
+  const bool ds = is_ds(c);
+  const bool batched = c.batch > 1 || ds;  // DeepSeek-V2 runs its batched kernel, a single sequence as a batch of one
+  if (c.batch > 1 && !posv) return fail(ETXMK_EINVAL, "a batched handle steps through etxmk_step_batch");
+  if (c.batch == 1 && posv) pos = posv[0];
+  int32_t pos1 = pos;
+  if (batched && !posv) posv = &pos1;
   for (int b = 0; b < (batched ? c.batch : 1); ++b) {
     const int q = batched ? posv[b] : pos;
     if (q < 0 || q >= c.max_ctx) return fail(ETXMK_EINVAL, "sequence %d position %d outside 0..%d", b, q, c.max_ctx - 1);
@@ -591,6 +769,8 @@ static int launch(etxmk_handle* h, const int32_t* posv, int pos, int write_next,
     if ((int64_t)h->nwg * NWAVE * (RES_ROWS / NWAVE) < c.H)
       return fail(ETXMK_EINVAL, "grid of %d workgroups too small for H %d at batch > 1 (at least %d)", h->nwg, c.H,
                   (c.H + RES_ROWS - 1) / RES_ROWS);
+    if (ds && h->nwg < c.NH)                 // the W_UV phase gives a workgroup rows of at most two heads
+      return fail(ETXMK_EINVAL, "grid of %d workgroups below the %d heads", h->nwg, c.NH);
   }
   Params p{};
   p.H = c.H; p.NH = c.NH; p.NKV = c.NKV; p.HD = c.HD; p.I = c.I; p.E = c.E; p.TOPK = c.TOPK; p.MI = c.MI; p.L = c.L; p.V = c.V;
@@ -598,6 +778,10 @@ static int launch(etxmk_handle* h, const int32_t* posv, int pos, int write_next,
   p.nblocks = nblocks_of(&c);
   p.eps = c.eps;
   p.attn_scale = (float)(1.0 / sqrt((double)c.HD));
+  if (ds) {                                  // softmax_scale (reference_decode.py:198-206): q_head_dim^-0.5 * mscale^2
+    const double mm = c.rope_factor <= 1.0f ? 1.0 : 0.1 * c.rope_mscale_all * log((double)c.rope_factor) + 1.0;
+    p.attn_scale = (float)(pow((double)(c.qk_nope + c.qk_rope), -0.5) * mm * mm);
+  }
   p.embed = (const uint16_t*)h->wt(ETXMK_T_EMBED, -1);
   p.lm_head = (const uint16_t*)h->wt(ETXMK_T_LMHEAD, -1);
   p.final_norm = (const uint16_t*)h->wt(ETXMK_T_FINAL_NORM, -1);
@@ -623,7 +807,7 @@ static int launch(etxmk_handle* h, const int32_t* posv, int pos, int write_next,
   p.nwg = h->nwg;
   p.spin_ticks = 200000000ull;            // 2 s of the 100 MHz s_memrealtime clock
   {                                        // QKV rows staged in LDS a layer ahead when a workgroup's share fits
-    const int rows = (c.NH + 2 * c.NKV) * c.HD, R = (rows + h->nwg - 1) / h->nwg;
+    const int rows = nqkv_of(c), R = (rows + h->nwg - 1) / h->nwg;
     p.qkv_rows = (!batched && h->fused && c.wdtype == ETXMK_W_BF16 && c.H % 512 == 0 &&
                   (uint64_t)R * c.H * 2 <= (uint64_t)QKVW_BYTES) ? R : 0;
   }
@@ -633,13 +817,29 @@ static int launch(etxmk_handle* h, const int32_t* posv, int pos, int write_next,
   p.x16 = h->wsptr<uint16_t>(h->ws.x16);
   p.o16 = h->wsptr<uint16_t>(h->ws.o16);
   p.h16 = h->wsptr<uint16_t>(h->ws.h16);
+  p.nqkv = nqkv_of(c);
+  p.Ip = ds ? ds_ip(c) : c.I;
+  p.h16d = h->wsptr<uint16_t>(h->ws.h16d);
+  p.arch = c.arch;
+  if (ds) {
+    p.I = c.dense_I;
+    p.first_dense = c.first_dense;
+    p.SI = ds_si(c);
+    p.routed_scale = c.routed_scale;
+    p.qc = h->wsptr<float>(h->ws.qc);
+    p.cnew = h->wsptr<float>(h->ws.cnew);
+    p.oc = h->wsptr<float>(h->ws.oc);
+    p.h16s = h->wsptr<uint16_t>(h->ws.h16s);
+  }
+  // attention items: per 64-position chunk of each sequence, NKV (Qwen3) or one per group of 8 heads (DeepSeek-V2)
+  const int per_chunk = ds ? ds_nhg(c) : c.NKV;
   p.ibase[0] = 0;
-  for (int b = 0; b < c.batch; ++b) {       // attention items: NKV per 64-position chunk of each sequence
+  for (int b = 0; b < c.batch; ++b) {
     p.posb[b] = batched ? posv[b] : pos;
-    p.ibase[b + 1] = p.ibase[b] + c.NKV * (p.posb[b] / CHUNK + 1);
+    p.ibase[b + 1] = p.ibase[b] + per_chunk * (p.posb[b] / CHUNK + 1);
   }
   if (h->fused) {
-    const void* fn = batched ? batch_kernel(c) : fused_kernel(c);
+    const void* fn = ds ? ds_kernel(c) : batched ? batch_kernel(c) : fused_kernel(c);
     if (!fn) return fail(ETXMK_EINVAL, "no persistent kernel for H %d, NH*HD %d, %s %d (use the unfused mode)", c.H,
                          c.NH * c.HD, c.moe ? "MI" : "I", c.moe ? c.MI : c.I);
     p.bar_base = h->bar_epoch;
@@ -690,7 +890,7 @@ int etxmk_step_batch(etxmk_handle* h, const int32_t* positions, int32_t write_ne
 
 int etxmk_step_layers(etxmk_handle* h, int32_t pos, int32_t l0, int32_t l1, void* stream) {
   if (!h) return fail(ETXMK_EINVAL, "NULL handle");
-  if (h->c.batch != 1) return fail(ETXMK_EINVAL, "layer-range steps serve single-sequence handles");
+  if (h->c.batch != 1 || is_ds(h->c)) return fail(ETXMK_EINVAL, "layer-range steps serve single-sequence Qwen3 handles");
   return launch(h, nullptr, pos, 0, l0, l1, 0, 0, (hipStream_t)stream);
 }
 
@@ -702,7 +902,7 @@ int etxmk_sync(etxmk_handle* h, void* stream) {
   if (ab) {
     HIPCHK(hipMemset(h->wsp + h->ws.abort_w, 0, 4));
     HIPCHK(hipMemset(h->wsp + h->ws.bar, 0, 4 * 64 * 17));
-    HIPCHK(hipMemset(h->wsp + h->ws.acnt, 0, 4ull * 64 * h->c.NKV * h->c.batch));
+    HIPCHK(hipMemset(h->wsp + h->ws.acnt, 0, acnt_bytes(h->c)));
     h->bar_epoch = 0;
     return fail(ETXMK_ABORTED, "device abort word %d (%s)", ab,
                 ab == 2 ? "a grid barrier wait exceeded its limit" : ab == 3 ? "no finite logit in the head" : "host abort");

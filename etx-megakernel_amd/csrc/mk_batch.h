@@ -184,6 +184,46 @@ __device__ __forceinline__ void dot_rows_b(const RowRegs<K> (&r)[NR], XP xp, int
     for (int b = 0; b < B; ++b) v[i][b] = b < nv ? wave_sum(acc[i][b]) : 0.0f;
 }
 
+// a long row (Bf16Row LONG) dotted with up to B input rows: dot_row_long's segments, each block's weights used for
+// every input, per (row, input) the order of dot_row
+template <int K, int B, class XP>
+__device__ __forceinline__ void dot_row_long_b(const uint16_t* row, XP xp, int nv, int lane, float (&v)[B]) {
+  constexpr int SEG = seg_of(KS<K>::KB), NS = SEG ? KS<K>::KB / SEG : 0;
+  static_assert(SEG > 0 && KS<K>::TW == 0, "long rows are whole segments of 4 to 12 blocks");
+  u32x4 RA[SEG], RB[SEG];
+  float acc[B];
+#pragma unroll
+  for (int b = 0; b < B; ++b) acc[b] = 0.0f;
+  auto ld = [&](u32x4(&R)[SEG], int sg) {
+#pragma unroll
+    for (int k = 0; k < SEG; ++k) R[k] = ld_nt16(row + 512 * (sg * SEG + k) + lane * 8);
+  };
+  auto acc_seg = [&](const u32x4(&R)[SEG], int sg) {
+#pragma unroll
+    for (int k = 0; k < SEG; ++k)
+#pragma unroll
+      for (int b = 0; b < B; ++b)
+        if (b < nv) {
+          const u32x4 xv = *(const u32x4*)(xp(b) + 512 * (sg * SEG + k) + lane * 8);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            acc[b] = __builtin_fmaf(bf_lo(R[k][j]), bf_lo(xv[j]), acc[b]);
+            acc[b] = __builtin_fmaf(bf_hi(R[k][j]), bf_hi(xv[j]), acc[b]);
+          }
+        }
+  };
+  ld(RA, 0);
+#pragma unroll 1
+  for (int sg = 0; sg < NS; sg += 2) {
+    if (sg + 1 < NS) ld(RB, sg + 1);
+    acc_seg(RA, sg);
+    if (sg + 2 < NS) ld(RA, sg + 2);
+    if (sg + 1 < NS) acc_seg(RB, sg + 1);
+  }
+#pragma unroll
+  for (int b = 0; b < B; ++b) v[b] = b < nv ? wave_sum(acc[b]) : 0.0f;
+}
+
 // gemv_run with B input rows per group: groups of NR rows dealt round-robin to the grid's waves; two register
 // buffers alternate, so one group's weights stream while the other group is reduced (a batched group carries
 // B x NR dots, which covers the latency of the next group's loads).  The first group is issued before `prologue`
@@ -192,40 +232,57 @@ __device__ __forceinline__ void dot_rows_b(const RowRegs<K> (&r)[NR], XP xp, int
 template <class WR, int NR, int B, class RowF, class NVF, class XF, class EpiF, class Pro>
 __device__ __forceinline__ bool gemv_run_b(int ngroups, RowF rowf, NVF nvec, XF xvec, EpiF epi, Pro prologue, int nwg,
                                            uint64_t* trace, int s_phase) {
-  static_assert(!WR::LONG, "batched GEMV rows are at most 8192 long");
   using Regs = typename WR::Regs;
   const int lane = lane_id();
   const int gw = blockIdx.x * NWAVE + wave_u(), nw = nwg * NWAVE;
-  Regs RA[NR], RB[NR];
-  auto issue = [&](Regs(&R)[NR], int g) {
+  if constexpr (WR::LONG) {                               // rows streamed in segments (dot_row_long_b)
+    if (!prologue()) return false;
+    for (int g = gw; g < ngroups; g += nw) {
+      const int nv = nvec(g);
+      float v[NR][B];
 #pragma unroll
-    for (int i = 0; i < NR; ++i) {
-      const uint8_t* rp = rowf(g, i);
-      if (rp) WR::load(R[i], rp, lane);
+      for (int i = 0; i < NR; ++i) {
+        const uint8_t* rp = rowf(g, i);
+        if (rp) dot_row_long_b<WR::K, B>((const uint16_t*)rp, [&](int b) { return xvec(g, b); }, nv, lane, v[i]);
+        else
+#pragma unroll
+          for (int b = 0; b < B; ++b) v[i][b] = 0.0f;
+      }
+      epi(g, nv, v);
     }
-  };
-  auto compute = [&](const Regs(&R)[NR], int g) {
-    const int nv = nvec(g);
-    float v[NR][B];
-    dot_rows_any<WR, NR, B>(R, [&](int b) { return xvec(g, b); }, nv, lane, v);
-    epi(g, nv, v);
-  };
-  int g = gw;
-  if (g < ngroups) issue(RA, g);
-  if (trace && threadIdx.x == 0)
-    *(MK_G uint64_t*)(trace + ((size_t)s_phase * nwg + blockIdx.x) * 3 + 2) = __builtin_amdgcn_s_memrealtime();
-  if (!prologue()) return false;
-  while (g < ngroups) {
-    const int g1 = g + nw;
-    if (g1 < ngroups) issue(RB, g1);
-    compute(RA, g);
-    if (g1 >= ngroups) break;
-    const int g2 = g1 + nw;
-    if (g2 < ngroups) issue(RA, g2);
-    compute(RB, g1);
-    g = g2;
+    return true;
+  } else {
+    Regs RA[NR], RB[NR];
+    auto issue = [&](Regs(&R)[NR], int g) {
+#pragma unroll
+      for (int i = 0; i < NR; ++i) {
+        const uint8_t* rp = rowf(g, i);
+        if (rp) WR::load(R[i], rp, lane);
+      }
+    };
+    auto compute = [&](const Regs(&R)[NR], int g) {
+      const int nv = nvec(g);
+      float v[NR][B];
+      dot_rows_any<WR, NR, B>(R, [&](int b) { return xvec(g, b); }, nv, lane, v);
+      epi(g, nv, v);
+    };
+    int g = gw;
+    if (g < ngroups) issue(RA, g);
+    if (trace && threadIdx.x == 0)
+      *(MK_G uint64_t*)(trace + ((size_t)s_phase * nwg + blockIdx.x) * 3 + 2) = __builtin_amdgcn_s_memrealtime();
+    if (!prologue()) return false;
+    while (g < ngroups) {
+      const int g1 = g + nw;
+      if (g1 < ngroups) issue(RB, g1);
+      compute(RA, g);
+      if (g1 >= ngroups) break;
+      const int g2 = g1 + nw;
+      if (g2 < ngroups) issue(RA, g2);
+      compute(RB, g1);
+      g = g2;
+    }
+    return true;
   }
-  return true;
 }
 
 // fp8 rows (Fp8Row) dotted with up to B input rows: each block's codes are decoded once and used for every input;
@@ -286,7 +343,7 @@ __device__ __forceinline__ void phase_qkv_b(const Params& p, int layer, S& s, Wa
   constexpr int KK = WR::K;
   const LayerW Lw = layer_w(p, layer);
   const bool first = layer == p.l0 && p.do_embed;
-  const int rows = (p.NH + 2 * p.NKV) * p.HD, nb = p.B;
+  const int rows = p.nqkv, nb = p.B;
   const uint8_t* W = Lw.wqkv;
   gemv_run_b<WR, 2, B>(
       (rows + 1) / 2,
@@ -529,7 +586,7 @@ template <class WR, int B, class S, class Wait>
 __device__ __forceinline__ void phase_gateup_b(const Params& p, int layer, S& s, Wait wait) {
   constexpr int KK = WR::K;
   const LayerW Lw = layer_w(p, layer);
-  const int I = p.I, nb = p.B;
+  const int I = p.I, IS = p.Ip, nb = p.B;                 // h rows are Ip long; entries [I, Ip) stay zero
   const uint8_t* W = Lw.wgu;
   gemv_run_b<WR, 2, B>(
       I, [&](int g, int i) -> const uint8_t* { return mrow<WR>(W, (size_t)2 * g + i); }, [&](int) { return nb; },
@@ -539,7 +596,7 @@ __device__ __forceinline__ void phase_gateup_b(const Params& p, int layer, S& s,
 #pragma unroll
         for (int b = 0; b < B; ++b)
           if (lane == b && b < nv)
-            st_ag_u16(p.h16 + (size_t)b * I + perm_stored(g, I), f2bf(bfr(bfr(silu(bfr(v[0][b]))) * bfr(v[1][b]))));
+            st_ag_u16(p.h16d + (size_t)b * IS + perm_stored(g, IS), f2bf(bfr(bfr(silu(bfr(v[0][b]))) * bfr(v[1][b]))));
       },
       [&]() {
         if (!wait()) return false;
@@ -568,7 +625,7 @@ __device__ __forceinline__ void phase_down_b(const Params& p, int layer, S& s, W
       [&]() {
         load_res_rows<B>(p, H, false, s);
         if (!wait()) return false;
-        copy_rows_lds(p.h16, nb * KK, s.v.xs);
+        copy_rows_lds(p.h16d, nb * KK, s.v.xs);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
         return true;

@@ -43,9 +43,11 @@ constexpr int MAX_B = 16;               // sequences per batched step
 
 // one layer's tensors; matrices are byte addresses of rows in their format (Bf16Row / Fp8Row below)
 struct LayerW {
-  const uint16_t *ln1, *ln2, *qn, *kn;
+  const uint16_t *ln1, *ln2, *qn, *kn;            // DeepSeek-V2: kn is the kv_a_layernorm weight [kv_lora]
   const uint8_t *wqkv, *wo, *wr, *w13, *w2, *wgu, *wd;
-  uint16_t *kc, *vc;
+  uint16_t *kc, *vc;                              // DeepSeek-V2: kc is the latent cache, vc unused
+  const uint8_t *wuk, *wuv, *wsgu, *wsd;          // DeepSeek-V2: W_UK^T [NH][kv_lora][qk_nope], W_UV [NH*v_head][kv_lora],
+                                                  // shared experts gate/up [2*SI][H] (interleaved) and down [H][SI]
 };
 
 struct Params {
@@ -89,6 +91,16 @@ struct Params {
   uint16_t* h16;                        // MoE [pairs][MI] / dense [B][I] MLP activations, bf16 lane-permuted
   int posb[MAX_B];                      // sequence b's position
   int ibase[MAX_B + 1];                 // attention items of the sequences before b (NKV * chunks each)
+  int nqkv;                             // rows of the fused QKV matrix (DeepSeek-V2: q_proj and kv_a_proj_with_mqa)
+  uint16_t* h16d;                       // dense MLP activations [B][Ip] (Ip: I rounded up to the row format; pads zero)
+  int Ip;
+  // DeepSeek-V2 (arch 1)
+  int arch, first_dense, SI;            // SI = n_shared * MI, the shared experts' width
+  float routed_scale;
+  float* qc;                            // [B][NH][kv_lora] absorbed queries, fp32
+  float* cnew;                          // [B][kv_lora + qk_rope] this step's latent row (bf16 values)
+  float* oc;                            // [B][NH][kv_lora] attention output in the latent space, fp32, W_UV row order
+  uint16_t* h16s;                       // [B][SI] shared experts' activations, bf16 lane-permuted
 };
 
 // the attention phase's LDS (one (sequence, kv head, chunk) item at a time)
@@ -353,12 +365,20 @@ __device__ __forceinline__ float dot_row(const RowRegs<K>& r, const uint16_t* xs
   return wave_sum(acc);
 }
 
-// Long rows (more than 16 blocks of 512): streamed in segments of 8 blocks, the next segment's loads in flight
-// while the current one is accumulated; the accumulation order is the same as dot_row's.
+// Long rows (more than 16 blocks of 512): streamed in segments of SEG blocks (a divisor of the block count near
+// 8), the next segment's loads in flight while the current one is accumulated; the accumulation order is the same
+// as dot_row's.
+constexpr int seg_of(int kb) {
+  for (int s = 8; s >= 4; --s)
+    if (kb % s == 0) return s;
+  for (int s = 9; s <= 12; ++s)
+    if (kb % s == 0) return s;
+  return 0;
+}
 template <int K>
 __device__ __forceinline__ float dot_row_long(const uint16_t* row, const uint16_t* xs, int lane) {
-  constexpr int SEG = 8, NS = KS<K>::KB / SEG;
-  static_assert(KS<K>::KB % SEG == 0 && KS<K>::TW == 0, "long rows are whole segments");
+  constexpr int SEG = seg_of(KS<K>::KB), NS = SEG ? KS<K>::KB / SEG : 0;
+  static_assert(SEG > 0 && KS<K>::TW == 0, "long rows are whole segments of 4 to 12 blocks");
   u32x4 A[SEG], B[SEG];
   float acc = 0.0f;
   auto ld = [&](u32x4(&R)[SEG], int sg) {
@@ -626,7 +646,7 @@ template <int KK>
 __device__ __forceinline__ void qkv_to_lds(const Params& p, int layer, Smem& s) {
   static_assert(KK % 512 == 0, "LDS-staged QKV rows are whole 512-element blocks");
   const LayerW Lw = layer_w(p, layer);
-  const int rows = (p.NH + 2 * p.NKV) * p.HD, R = p.qkv_rows, r0 = (int)blockIdx.x * R;
+  const int rows = p.nqkv, R = p.qkv_rows, r0 = (int)blockIdx.x * R;
   const int lane = lane_id();
   for (int i = wave_u(); i < R && r0 + i < rows; i += NWAVE) {
     const uint16_t* src = (const uint16_t*)Lw.wqkv + (size_t)(r0 + i) * KK + 8 * lane;
@@ -641,7 +661,7 @@ __device__ __forceinline__ void qkv_to_lds(const Params& p, int layer, Smem& s) 
 template <int KK, class Wait>
 __device__ __forceinline__ void phase_qkv_lds(const Params& p, int layer, Smem& s, Wait wait) {
   const LayerW Lw = layer_w(p, layer);
-  const int rows = (p.NH + 2 * p.NKV) * p.HD, R = p.qkv_rows, r0 = (int)blockIdx.x * R;
+  const int rows = p.nqkv, R = p.qkv_rows, r0 = (int)blockIdx.x * R;
   const int lane = lane_id();
   float* qkv = p.qkv;
   if (!wait()) return;
@@ -672,7 +692,7 @@ __device__ __forceinline__ void phase_qkv(const Params& p, int layer, Smem& s, W
   constexpr int KK = WR::K;
   const LayerW Lw = layer_w(p, layer);
   const bool first = layer == p.l0 && p.do_embed;
-  const int rows = (p.NH + 2 * p.NKV) * p.HD;
+  const int rows = p.nqkv;
   float* qkv = p.qkv;
   const uint8_t* W = Lw.wqkv;
   gemv_run<WR, 2>(
@@ -1064,7 +1084,10 @@ __device__ __forceinline__ void route_topk_into(const Params& p, const float* lo
       if (k < K && ids[k] < id) ++before;
     if (lane < K) {
       ids_out[lane] = id;
-      wts_out[lane] = bfr(p.norm_topk ? wk / sel : wk);
+      // Qwen3: bf16 weights, renormalised (ref_numpy.py:138-140); DeepSeek-V2: fp32 probability times
+      // routed_scaling_factor, or renormalised with a 1e-20 guard (reference_decode.py:271-278)
+      if (p.arch == ETXMK_ARCH_DSV2) wts_out[lane] = p.norm_topk ? wk / (sel + 1e-20f) : wk * p.routed_scale;
+      else wts_out[lane] = bfr(p.norm_topk ? wk / sel : wk);
       if (order_out) order_out[before] = lane;
     }
   }

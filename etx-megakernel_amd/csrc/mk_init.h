@@ -5,10 +5,11 @@
 
 namespace mk {
 
-// n_t consecutive tensors of rows x cols (experts of one layer); element (r, k) of tensor e is number r*cols+k
-// of stream sid0 + e; stored at its lane-permuted position when perm != 0.
+// n_t consecutive tensors of rows x cols (experts of one layer); element (r, k) of tensor e is number r*lcols+k
+// of stream sid0 + e for k < lcols (the logical row length) and zero in the pads [lcols, cols); stored at its
+// lane-permuted position when perm != 0.
 extern "C" __global__ void etxmk_gen_weights(uint16_t* dst, uint64_t seed, uint64_t sid0, int n_t, int rows, int cols,
-                                             int perm, float scale) {
+                                             int lcols, int perm, float scale) {
   const size_t per = (size_t)rows * cols;
   const size_t total8 = per * n_t / 8;
   for (size_t q8 = (size_t)blockIdx.x * blockDim.x + threadIdx.x; q8 < total8; q8 += (size_t)gridDim.x * blockDim.x) {
@@ -21,7 +22,7 @@ extern "C" __global__ void etxmk_gen_weights(uint16_t* dst, uint64_t seed, uint6
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int k = perm ? perm_logical(p0 + u, cols) : p0 + u;
-      out[u] = f2bf(scale * normal_at(key, (uint64_t)r * cols + k));
+      out[u] = k < lcols ? f2bf(scale * normal_at(key, (uint64_t)r * lcols + k)) : (uint16_t)0;
     }
     *(u32x4*)(dst + q) = *(const u32x4*)out;
   }
@@ -31,11 +32,49 @@ extern "C" __global__ void etxmk_fill_u16(uint16_t* dst, size_t n, uint16_t v) {
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) dst[i] = v;
 }
 
-extern "C" __global__ void etxmk_pack_rows(uint16_t* dst, const uint16_t* src, int rows, int cols) {
+// natural rows of lcols bf16 -> lane-permuted rows of cols (pads zero)
+extern "C" __global__ void etxmk_pack_rows(uint16_t* dst, const uint16_t* src, int rows, int cols, int lcols) {
   const size_t total = (size_t)rows * cols;
   for (size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x; q < total; q += (size_t)gridDim.x * blockDim.x) {
     const int r = (int)(q / cols), p = (int)(q - (size_t)r * cols);
-    dst[q] = src[(size_t)r * cols + perm_logical(p, cols)];
+    const int k = perm_logical(p, cols);
+    dst[q] = k < lcols ? src[(size_t)r * lcols + k] : (uint16_t)0;
+  }
+}
+
+// DeepSeek-V2 kv_b_proj ([NH*(nope + vh)][kvl] natural: per head nope W_UK rows, then vh W_UV rows) stored as
+// W_UK^T [NH][kvl][nope] (lane-permuted rows of nope) followed by W_UV [NH*vh][kvl] (lane-permuted rows of kvl).
+// Values from src (natural rows) or, when src is null, element (r, k) of the natural tensor is number r*kvl + k
+// of stream sid.
+extern "C" __global__ void etxmk_pack_kvb(uint16_t* dst, const uint16_t* src, uint64_t seed, uint64_t sid, int NH,
+                                          int nope, int vh, int kvl, float scale) {
+  const size_t n_uk = (size_t)NH * kvl * nope, total = (size_t)NH * (nope + vh) * kvl;
+  const uint64_t key = stream_key(seed, sid);
+  for (size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x; q < total; q += (size_t)gridDim.x * blockDim.x) {
+    size_t r, k;                                          // natural (row, column) of stored element q
+    if (q < n_uk) {
+      const size_t row = q / nope;                        // W_UK^T row (h, i)
+      const int h = (int)(row / kvl), i = (int)(row % kvl), d = perm_logical((int)(q % nope), nope);
+      r = (size_t)h * (nope + vh) + d;
+      k = i;
+    } else {
+      const size_t q2 = q - n_uk, row = q2 / kvl;         // W_UV row (h, d)
+      const int h = (int)(row / vh), d = (int)(row % vh), i = perm_logical((int)(q2 % kvl), kvl);
+      r = (size_t)h * (nope + vh) + nope + d;
+      k = i;
+    }
+    dst[q] = src ? src[r * kvl + k] : f2bf(scale * normal_at(key, (uint64_t)(r * kvl + k)));
+  }
+}
+
+// latent cache positions [0, npos) of one sequence: element (t, i) is number t*CD + i of the layer's stream, stored
+// at [block][i / 8][block_size][i % 8]
+extern "C" __global__ void etxmk_gen_latent(uint16_t* kc, const int32_t* btab, uint64_t key, int npos, int CD, int BS) {
+  const size_t total = (size_t)npos * CD;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+    const int d = (int)(i % CD), t = (int)(i / CD);
+    const int blk = btab[t / BS], off = t % BS;
+    kc[(((size_t)blk * (CD / 8) + d / 8) * BS + off) * 8 + d % 8] = f2bf(normal_at(key, i));
   }
 }
 

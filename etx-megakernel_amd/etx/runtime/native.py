@@ -23,6 +23,7 @@ ABI_VERSION = 2
 OK, EINVAL, EHIP, ABORTED, EUNBOUND = 0, 1, 2, 3, 4
 T_EMBED, T_LMHEAD, T_WQKV, T_WO, T_ROUTER, T_W13, T_W2, T_WGU, T_WD = 1, 2, 3, 4, 5, 6, 7, 8, 9
 T_LN1, T_LN2, T_QNORM, T_KNORM, T_FINAL_NORM = 20, 21, 22, 23, 24
+T_WKVB, T_WSGU, T_WSD = 14, 15, 16             # DeepSeek-V2: kv_b_proj, shared experts' gate/up and down
 
 
 class EtxmkError(RuntimeError):
@@ -272,8 +273,25 @@ class Decoder:
         if self.tensor_format(kind, layer)[0] != W_BF16:
             raise ValueError(f"tensor kind {kind} is held as fp8: use tensor_fp8")
         off, r, c, perm = self.tensor_info(kind, layer, expert)
-        t = self.weights[off:off + r * c * 2].view(self.torch.int16).cpu().numpy().view(np.uint16).reshape(r, c)
-        return unpermute_rows(t) if (perm and natural) else t
+        if kind == T_WKVB and self.cfg.arch == ARCH_DSV2:
+            raise ValueError("kv_b_proj is stored split (W_UK^T, W_UV): read it with kv_b()")
+        cs = self.tensor_format(kind, layer)[1] // 2          # stored row length (padded rows are longer than c)
+        t = self.weights[off:off + r * cs * 2].view(self.torch.int16).cpu().numpy().view(np.uint16).reshape(r, cs)
+        return (unpermute_rows(t) if (perm and natural) else t)[:, :c] if natural else t
+
+    def kv_b(self, layer: int) -> np.ndarray:
+        """DeepSeek-V2 kv_b_proj of a layer in its natural layout [NH*(qk_nope + v_head)][kv_lora] (uint16 bits),
+        rebuilt from the stored W_UK^T and W_UV."""
+        c = self.cfg
+        off, r, kvl, _ = self.tensor_info(T_WKVB, layer)
+        raw = self.weights[off:off + r * kvl * 2].view(self.torch.int16).cpu().numpy().view(np.uint16)
+        NH, nope, vh = c.NH, c.qk_nope, c.v_head
+        uk = unpermute_rows(raw[:NH * kvl * nope].reshape(NH * kvl, nope)).reshape(NH, kvl, nope)
+        uv = unpermute_rows(raw[NH * kvl * nope:].reshape(NH * vh, kvl)).reshape(NH, vh, kvl)
+        out = np.empty((NH, nope + vh, kvl), np.uint16)
+        out[:, :nope] = uk.transpose(0, 2, 1)
+        out[:, nope:] = uv
+        return out.reshape(NH * (nope + vh), kvl)
 
     def load_tensor(self, kind: int, layer: int, expert: int, src):
         """src: torch bf16/int16 tensor on the device in natural [rows][cols] layout."""
@@ -292,7 +310,10 @@ class Decoder:
         _check(self.L, self.L.etxmk_fill_kv_seeded_seq(self.h, seed, seq, npos, self._stream()))
 
     def kv_layer(self, layer: int):
-        """(K, V) of one layer as uint16 bf16 bits, paged layout, flat."""
+        """(K, V) of one layer as uint16 bf16 bits, paged layout, flat; DeepSeek-V2: (latent cache, None)."""
+        if self.cfg.arch == ARCH_DSV2:
+            n = self.sizes["kv"] // 2 // self.cfg.L
+            return self.kv.view(self.torch.int16)[layer * n:(layer + 1) * n].cpu().numpy().view(np.uint16), None
         n = self.sizes["kv"] // 2 // self.cfg.L // 2
         base = layer * 2 * n
         flat = self.kv.view(self.torch.int16)

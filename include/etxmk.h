@@ -36,6 +36,12 @@ extern "C" {
 #define ETXMK_T_W2 7
 #define ETXMK_T_WGU 8
 #define ETXMK_T_WD 9
+/* DeepSeek-V2: kv_b_proj [NH*(qk_nope + v_head)][kv_lora] (stored split: W_UK^T [NH][kv_lora][qk_nope], then W_UV
+ * [NH*v_head][kv_lora]), shared experts' gate/up [2*n_shared*MI][H] (gate and up rows interleaved) and down
+ * [H][n_shared*MI]; ETXMK_T_WQKV holds q_proj then kv_a_proj_with_mqa, ETXMK_T_KNORM the kv_a_layernorm weight */
+#define ETXMK_T_WKVB 14
+#define ETXMK_T_WSGU 15
+#define ETXMK_T_WSD 16
 #define ETXMK_T_LN1 20
 #define ETXMK_T_LN2 21
 #define ETXMK_T_QNORM 22

@@ -89,3 +89,27 @@ def test_fp8_needs_a_persistent_kernel():
     with pytest.raises(N.EtxmkError) as e:
         N.sizes(configs.with_layers(configs.QWEN3_8B, 36, wdtype=N.W_FP8))
     assert e.value.code == N.EINVAL and "fp8" in str(e.value)
+
+
+def test_deepseek_v2_lite_sizes():
+    """Weights: every DeepSeek-V2-Lite tensor once (the dense layer's down rows padded to 11264), bf16."""
+    c = configs.DEEPSEEK_V2_LITE
+    SI, IP, NQA = c.n_shared * c.MI, (c.dense_I + 511) // 512 * 512, c.nqkv
+    attn = NQA * c.H + c.NH * (c.qk_nope + c.v_head) * c.kv_lora + c.H * c.NH * c.v_head + c.kv_lora + 2 * c.H
+    dense = 2 * c.dense_I * c.H + c.H * IP
+    moe = c.E * c.H + c.E * 3 * c.MI * c.H + 3 * SI * c.H
+    elems = c.L * attn + c.first_dense * dense + (c.L - c.first_dense) * moe + 2 * c.V * c.H + c.H
+    s = N.sizes(c)
+    assert elems * 2 <= s["weights"] < elems * 2 + 256 * 20 * c.L
+    assert 31.0e9 < s["weights"] < 31.6e9                  # 15.7B parameters
+    assert s["kv"] == 2 * c.L * ((c.max_ctx + 15) // 16) * 16 * (c.kv_lora + c.qk_rope)   # one latent pool
+
+
+@pytest.mark.parametrize("bad", [dict(wdtype=1), dict(batch=5), dict(kv_lora=256), dict(block_size=8),
+                                 dict(HD=128), dict(NH=12), dict(MI=1024)])
+def test_deepseek_config_refused(bad):
+    d = configs.DEEPSEEK_V2_LITE.as_dict()
+    d.update(bad)
+    with pytest.raises(N.EtxmkError) as e:
+        N.sizes(N.ModelConfig(**d))
+    assert e.value.code == N.EINVAL
