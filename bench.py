@@ -3,6 +3,7 @@
 
     python bench.py [--gpus 1] [--steps 32] [--warmup 4] [--ctx 1024] [--no-cpu] [--unfused]
     python bench.py --batch 16 [--ctx-lo 512 --ctx-hi 4096]      (batched step; not the headline line)
+    python bench.py --model deepseek-v2-lite --batch 4 --ctx-lo 512 --ctx-hi 2048   (BASELINE.json configs[3])
 
 Setup (untimed): seeded random-init weights N(0, 0.02) in HBM, a prompt of `ctx` seeded random token ids fed
 token by token through the decode step (as examples/llm/host.hip:203-213 does), then `warmup` greedy steps.
@@ -60,10 +61,34 @@ def bytes_per_token(cfg, context: int) -> dict:
     return {"weights": weights, "kv": kv, "total": weights + kv}
 
 
+def bytes_per_step_ds(cfg, contexts, union) -> dict:
+    """DeepSeek-V2 step (the ledger of BASELINE.json configs[3]): every attention weight once (q_proj and
+    kv_a rows, kv_b_proj, o_proj, norms), the dense layers' MLP, the MoE layers' router and shared experts once and
+    their distinct routed experts once (union[l], measured), the latent cache read over each context plus one row
+    written, one embedding row per sequence, lm_head."""
+    H, V, NH, bf = cfg.H, cfg.V, cfg.NH, 2
+    B = len(contexts)
+    glob = (B * H + H + V * H) * bf
+    attn = (2 * H + cfg.kv_lora) * bf + cfg.nqkv * H * bf + NH * (cfg.qk_nope + cfg.v_head) * cfg.kv_lora * bf \
+        + H * NH * cfg.v_head * bf
+    dense = 3 * cfg.dense_I * H * bf
+    SI = cfg.n_shared * cfg.MI
+    moe = cfg.E * H * bf + 3 * SI * H * bf
+    expert = 3 * cfg.MI * H * bf
+    weights = glob + cfg.L * attn + cfg.first_dense * dense + (cfg.L - cfg.first_dense) * moe \
+        + sum(int(u) * expert for u in union[cfg.first_dense:])
+    row = (cfg.kv_lora + cfg.qk_rope) * bf
+    kv = cfg.L * sum((int(c) + 1) * row for c in contexts)
+    return {"weights": weights, "kv": kv, "total": weights + kv}
+
+
 def bytes_per_step(cfg, contexts, union) -> dict:
     """Algorithmic HBM bytes of one batched step: every non-expert weight once, each layer's distinct routed experts
     once (union[l], measured), each sequence's KV read over its context plus one position written, one embedding
     row per sequence (byte_ledger.py:121-178 rules with the expert union of a batch)."""
+    from etx.runtime import native as N
+    if cfg.arch == N.ARCH_DSV2:
+        return bytes_per_step_ds(cfg, contexts, union)
     H, HD, NH, NKV, V = cfg.H, cfg.HD, cfg.NH, cfg.NKV, cfg.V
     bf = 2
     B = len(contexts)
@@ -89,11 +114,12 @@ def main_batch(a):
     from etx.runtime import native as N
     from etx.models import configs
     B = a.batch
+    ds = a.model == "deepseek-v2-lite"
     rng = np.random.default_rng(a.seed + 4)
     ctx = rng.integers(a.ctx_lo, a.ctx_hi + 1, B).astype(np.int32)
     max_ctx = int(ctx.max()) + a.warmup + a.steps + 2
-    cfg = configs.with_layers(configs.QWEN3_30B_A3B, configs.QWEN3_30B_A3B.L, batch=B, max_ctx=max_ctx,
-                              wdtype=N.W_FP8 if a.fp8 else N.W_BF16)
+    base = configs.DEEPSEEK_V2_LITE if ds else configs.QWEN3_30B_A3B
+    cfg = configs.with_layers(base, base.L, batch=B, max_ctx=max_ctx, wdtype=N.W_FP8 if a.fp8 else N.W_BF16)
     wname = "fp8 e4m3 (per-row scales; router, embedding, lm_head bf16)" if a.fp8 else "bf16"
     dev = torch.device("cuda:0")
     t0 = time.time()
@@ -143,28 +169,35 @@ def main_batch(a):
         if a.trace_out:
             np.save(a.trace_out, t)
         phase_us = trace_summary(t, cfg)
-    union = [len(np.unique(d["ids"][l])) for l in range(cfg.L)]
+    union = [len(np.unique(d["ids"][l])) if l >= cfg.first_dense else 0 for l in range(cfg.L)]
     mean_ctx = (first_timed + pos - 1) / 2.0
     by = bytes_per_step(cfg, np.round(mean_ctx).astype(int), union)
     gbps = by["total"] / (ms * 1e-3) / 1e9
+    umean = float(np.mean(union[cfg.first_dense:]))
     log(f"[gpu] {a.steps} batched steps: {ms:.4f} ms/step ({ms / B:.4f} ms/token, {B * 1e3 / ms:.1f} tokens/s), "
-        f"{gbps:.1f} GB/s = {gbps / HBM_PEAK_GBPS:.3f} of 8 TB/s; expert union per layer mean {np.mean(union):.1f}")
+        f"{gbps:.1f} GB/s = {gbps / HBM_PEAK_GBPS:.3f} of 8 TB/s; expert union per MoE layer mean {umean:.1f}")
+    shape = "DeepSeek-V2-Lite" if ds else "Qwen3-30B-A3B"
+    if ds:
+        workload = (f"{cfg.name} decode, batch {B}, bf16 weights, multi-head latent attention over a paged latent "
+                    f"cache, contexts uniform in [{a.ctx_lo}, {a.ctx_hi}], greedy (BASELINE.json configs[3])")
+    else:
+        workload = (f"{cfg.name} decode, batch {B}, {wname} weights, contexts uniform in [{a.ctx_lo}, {a.ctx_hi}], "
+                    f"greedy" + (" (BASELINE.json configs[4])" if a.fp8 else " (configs[4] shape with bf16 weights)"))
     out = {
-        "metric": f"decode ms/step at batch {B}, Qwen3-30B-A3B shape; tokens/s; achieved HBM GB/s vs peak",
+        "metric": f"decode ms/step at batch {B}, {shape} shape; tokens/s; achieved HBM GB/s vs peak",
         "value": round(ms, 4), "unit": "ms/step", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
         "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
         "dtype": "fp8-e4m3 weights x bf16 activations, fp32 accumulation" if a.fp8 else "bf16",
-        "data": f"synthetic: seeded random-init weights N(0,0.02) ({wname}); per-sequence KV of seeded N(0,1) values",
-        "config": {"workload": f"{cfg.name} decode, batch {B}, {wname} weights, contexts uniform in "
-                               f"[{a.ctx_lo}, {a.ctx_hi}], greedy"
-                               + (" (BASELINE.json configs[4])" if a.fp8 else " (configs[4] shape with bf16 weights)"),
-                   "batch": B, "contexts": [int(c) for c in ctx], "layers": cfg.L, "experts": cfg.E,
+        "data": f"synthetic: seeded random-init weights N(0,0.02) ({wname}); per-sequence "
+                f"{'latent cache' if ds else 'KV'} of seeded N(0,1) values",
+        "config": {"workload": workload, "batch": B, "contexts": [int(c) for c in ctx], "layers": cfg.L, "experts": cfg.E,
                    "top_k": cfg.TOPK, "vocab": cfg.V, "mode": "fused megakernel", "seed": a.seed},
         "tokens_per_s": round(B * 1e3 / ms, 2), "ms_per_token": round(ms / B, 4),
-        "host_wall_ms_per_step": round(wall / a.steps, 4), "expert_union_mean": round(float(np.mean(union)), 2),
+        "host_wall_ms_per_step": round(wall / a.steps, 4), "expert_union_mean": round(umean, 2),
         "bytes_per_step": by["total"], "achieved_GBps": round(gbps, 1),
         "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None, "kernel": "etxmk_fused_b*"},
+                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "kernel": "etxmk_ds_b4*" if ds else "etxmk_fused_b*"},
         "cpu_baseline": None,
     }
     if phase_us:
@@ -208,16 +241,23 @@ def cpu_baseline(cfg, ctx: int, seed: int) -> dict:
 def trace_summary(t, cfg):
     """Per-phase timeline of one traced step.  t[k][wg] = (wait for phase k's inputs returned, arrived after phase k,
     first weight loads issued (GEMV phases) / chunk partials issued (attention)), microseconds from the launch."""
-    names = (["qkv", "attn", "oproj", "router", "expert_up", "expert_down"] if cfg.moe
-             else ["qkv", "attn", "oproj", "gateup", "down"])
-    nl = len(names)
-    nb = nl * cfg.L
+    from etx.runtime import native as N
+    if cfg.arch == N.ARCH_DSV2:
+        att = ["qkv", "absorb", "attn", "wuv", "oproj"]
+        per_layer = [att + (["gateup", "down"] if l < cfg.first_dense else ["router_shared", "expert_up", "expert_down"])
+                     for l in range(cfg.L)]
+    else:
+        per_layer = [["qkv", "attn", "oproj", "router", "expert_up", "expert_down"] if cfg.moe
+                     else ["qkv", "attn", "oproj", "gateup", "down"]] * cfg.L
+    flat = [n for names_l in per_layer for n in names_l]
+    names = list(dict.fromkeys(flat))
+    nb = len(flat)
     end = np.nanmax(t[:, :, 1], axis=1)                   # phase k complete: last arrival
     span = np.diff(np.concatenate([[0.0], end[:nb + 1]]))
-    per = span[:nb].reshape(cfg.L, nl)
-    phase_us = {n: round(float(per[:, i].mean()), 2) for i, n in enumerate(names)}
+    idx = {n: np.array([k for k, m in enumerate(flat) if m == n]) for n in names}
+    phase_us = {n: round(float(span[idx[n]].mean()), 2) for n in names}
     phase_us["head"] = round(float(span[nb]), 2)
-    avg = lambda v: {n: round(float(np.nanmean(v.reshape(cfg.L, nl)[:, i])), 2) for i, n in enumerate(names)}
+    avg = lambda v: {n: round(float(np.nanmean(v[idx[n]])), 2) for n in names}
     lag = np.full(nb, np.nan)
     lag[1:] = np.nanmedian(t[1:nb, :, 0], axis=1) - end[:nb - 1]
     lagmax = np.full(nb, np.nan)
@@ -258,12 +298,14 @@ def main():
     ap.add_argument("--ctx-lo", type=int, default=512)
     ap.add_argument("--ctx-hi", type=int, default=4096)
     ap.add_argument("--fp8", action="store_true", help="fp8 e4m3 weights with per-row scales (BASELINE.json configs[4])")
+    ap.add_argument("--model", default="qwen3-30b-a3b", choices=["qwen3-30b-a3b", "deepseek-v2-lite"],
+                    help="deepseek-v2-lite: the batched multi-head latent attention step (BASELINE.json configs[3])")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py: this build runs on exactly one GPU (asked for {a.gpus}); multi-GPU sharding is a design "
               f"note only", file=sys.stderr)
         sys.exit(2)
-    if a.batch > 1:
+    if a.batch > 1 or a.model == "deepseek-v2-lite":
         return main_batch(a)
 
     import numpy as np

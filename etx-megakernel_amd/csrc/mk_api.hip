@@ -272,7 +272,7 @@ int kv_pools(const etxmk_config* c) { return c->arch == ETXMK_ARCH_DSV2 ? 1 : 2;
 
 struct WsLayout {
   uint64_t x, x16, qkv, o, o16, logits, hbuf, h16, apart, acnt, amax, bar, abort_w, tokens, out_tokens, btab, rcos, rsin,
-      layers, h16d, qc, cnew, oc, h16s, total;
+      layers, h16d, qc, h16s, total;
 };
 
 WsLayout ws_layout(const etxmk_config* c) {
@@ -305,9 +305,7 @@ WsLayout ws_layout(const etxmk_config* c) {
   w.layers = take(sizeof(LayerW) * (uint64_t)c->L);
   if (ds) {
     w.h16d = take(2ull * (c->first_dense > 0 ? ds_ip(*c) : 8) * B);
-    w.qc = take(4ull * c->NH * c->kv_lora * B);
-    w.cnew = take(4ull * MLA_CD * B);
-    w.oc = take(4ull * c->NH * c->kv_lora * B);
+    w.qc = take(4ull * c->L * c->NH * c->kv_lora * B);   // one buffer per layer (read through the scalar cache)
     w.h16s = take(2ull * ds_si(*c) * B);
   } else {
     w.h16d = w.h16;
@@ -769,8 +767,6 @@ static int launch(etxmk_handle* h, const int32_t* posv, int pos, int write_next,
     if ((int64_t)h->nwg * NWAVE * (RES_ROWS / NWAVE) < c.H)
       return fail(ETXMK_EINVAL, "grid of %d workgroups too small for H %d at batch > 1 (at least %d)", h->nwg, c.H,
                   (c.H + RES_ROWS - 1) / RES_ROWS);
-    if (ds && h->nwg < c.NH)                 // the W_UV phase gives a workgroup rows of at most two heads
-      return fail(ETXMK_EINVAL, "grid of %d workgroups below the %d heads", h->nwg, c.NH);
   }
   Params p{};
   p.H = c.H; p.NH = c.NH; p.NKV = c.NKV; p.HD = c.HD; p.I = c.I; p.E = c.E; p.TOPK = c.TOPK; p.MI = c.MI; p.L = c.L; p.V = c.V;
@@ -827,8 +823,6 @@ static int launch(etxmk_handle* h, const int32_t* posv, int pos, int write_next,
     p.SI = ds_si(c);
     p.routed_scale = c.routed_scale;
     p.qc = h->wsptr<float>(h->ws.qc);
-    p.cnew = h->wsptr<float>(h->ws.cnew);
-    p.oc = h->wsptr<float>(h->ws.oc);
     p.h16s = h->wsptr<uint16_t>(h->ws.h16s);
   }
   // attention items: per 64-position chunk of each sequence, NKV (Qwen3) or one per group of 8 heads (DeepSeek-V2)

@@ -97,9 +97,7 @@ struct Params {
   // DeepSeek-V2 (arch 1)
   int arch, first_dense, SI;            // SI = n_shared * MI, the shared experts' width
   float routed_scale;
-  float* qc;                            // [B][NH][kv_lora] absorbed queries, fp32
-  float* cnew;                          // [B][kv_lora + qk_rope] this step's latent row (bf16 values)
-  float* oc;                            // [B][NH][kv_lora] attention output in the latent space, fp32, W_UV row order
+  float* qc;                            // [L][B][NH][kv_lora] absorbed queries, fp32
   uint16_t* h16s;                       // [B][SI] shared experts' activations, bf16 lane-permuted
 };
 

@@ -9,11 +9,12 @@
 //
 // Phases of a layer:
 //   P1  input RMSNorm + GEMV over the fused [q_proj; kv_a_proj_with_mqa] rows          -> qkv [B][NQA] (bf16 values)
-//   P1b absorbed queries q_c[h] = W_UK[h]^T q_nope[h] (fp32, not rounded); per sequence the new latent row
-//       (kv_a_layernorm, RoPE of k_pe) appended to the latent cache                     -> qc, cnew, cache
-//   P2  latent attention per (sequence, head group of 8, 64-position chunk): s = (q_c . c + q_pe . k_pe) * scale,
-//       chunk softmax partials; the last chunk of a (sequence, head group) to arrive merges them -> oc (fp32)
-//   P2c W_UV: out[h*v_head + d] = bfr(W_UV[h][d] . o_c[h])                               -> o16
+//   P1b absorbed queries q_c[h] = W_UK[h]^T q_nope[h] (fp32, not rounded)                -> qc (one buffer per layer)
+//   P2  latent attention per (sequence, head group of 8, 64-position chunk): the chunk holding the current position
+//       builds the new latent row (kv_a_layernorm, RoPE of k_pe) and appends it to the cache; s = (q_c . c +
+//       q_pe . k_pe) * scale, chunk softmax partials (a, m, l)                               -> apart
+//   P2c per (sequence, head, quarter of v_head): merge of the partials into o_c (fp32), then
+//       out[h*v_head + d] = bfr(W_UV[h][d] . o_c[h])                                     -> o16
 //   P3  O projection + residual (mk_batch.h)
 //   MoE layers: P4 post-attention RMSNorm, fp32 router logits and the shared experts' gate/up | P5 top-k with fp32
 //   weights (probability * routed_scale) and the routed gate/up | P6 routed and shared down, combine, residual
@@ -40,8 +41,7 @@ constexpr int MAX_B_DS = 4;             // sequences per DeepSeek-V2 step
 // both touch 64 distinct 16-byte slots whose bank groups differ within every 16 lanes.
 struct MlaTiles {
   u32x4 t[MLA_CG][CHUNK];
-  alignas(16) float qc[MLA_G][MLA_KVL];   // absorbed queries of the item's heads
-  alignas(16) float qpe[MLA_G][MLA_R];    // roped q_pe
+  alignas(16) float xo[MLA_KVL];          // P2c: o_c of the item, in the W_UV rows' stored order
   alignas(16) float p[MLA_G][2 * MAX_CHUNKS];  // chunk: exp(s - m) per position; merge: chunk weights, chunk sums
   float m[MLA_G];
   alignas(16) float cn[MLA_CD];           // the sequence's new latent row
@@ -94,9 +94,9 @@ __device__ __forceinline__ void rope_ds_pair(float a, float b, float c, float s,
 }
 
 // The new latent row of sequence b, one wave: c = kv_a_layernorm(kv_a) (reference_decode.py:231; the sum of
-// squares in dot order, then bfr(w * bfr(x * r))) and k_pe roped (:234), as bf16 into the latent cache at the
-// sequence's position (:236-237) and as fp32 into p.cnew for the attention phase
-__device__ __forceinline__ void latent_row(const Params& p, const LayerW& Lw, int b) {
+// squares in dot order, then bfr(w * bfr(x * r))) and k_pe roped (:234), as fp32 (bf16 values) into cn; with
+// `append` also as bf16 into the latent cache at the sequence's position (:236-237)
+__device__ __forceinline__ void latent_row(const Params& p, const LayerW& Lw, int b, bool append, float* cn) {
   const int lane = lane_id(), pos = p.posb[b], BS = p.BS;
   const float* kva = p.qkv + (size_t)b * p.nqkv + p.NH * MLA_QD;
   float x[MLA_KVL / 64];
@@ -111,13 +111,12 @@ __device__ __forceinline__ void latent_row(const Params& p, const LayerW& Lw, in
   const float r = 1.0f / __builtin_sqrtf(acc / (float)MLA_KVL + p.eps);
   const int blk = ld_i(p.btab + (size_t)b * p.nbps + pos / BS), off = pos % BS;
   uint16_t* row = Lw.kc + (size_t)blk * MLA_CG * BS * 8 + off * 8;   // dim k at row + (k / 8) * BS * 8 + k % 8
-  float* cn = p.cnew + (size_t)b * MLA_CD;
 #pragma unroll
   for (int e = 0; e < MLA_KVL / 64; ++e) {
     const int k = lane + 64 * e;
     const float c = bfr(bf2f(ld_u16(Lw.kn + k)) * bfr(x[e] * r));
-    st_u16(row + (size_t)(k / 8) * BS * 8 + k % 8, f2bf(c));
-    st_ag(cn + k, c);
+    if (append) st_u16(row + (size_t)(k / 8) * BS * 8 + k % 8, f2bf(c));
+    cn[k] = c;
   }
   if (lane < MLA_R / 2) {
     const float cs = ld_f(p.rope_cos + (size_t)pos * (MLA_R / 2) + lane);
@@ -125,15 +124,22 @@ __device__ __forceinline__ void latent_row(const Params& p, const LayerW& Lw, in
     float lo, hi;
     rope_ds_pair(a0, a1, cs, sn, lo, hi);
     const int k0 = MLA_KVL + lane, k1 = MLA_KVL + MLA_R / 2 + lane;
-    st_u16(row + (size_t)(k0 / 8) * BS * 8 + k0 % 8, f2bf(lo));
-    st_u16(row + (size_t)(k1 / 8) * BS * 8 + k1 % 8, f2bf(hi));
-    st_ag(cn + k0, lo);
-    st_ag(cn + k1, hi);
+    if (append) {
+      st_u16(row + (size_t)(k0 / 8) * BS * 8 + k0 % 8, f2bf(lo));
+      st_u16(row + (size_t)(k1 / 8) * BS * 8 + k1 % 8, f2bf(hi));
+    }
+    cn[k0] = lo;
+    cn[k1] = hi;
   }
 }
 
+// the absorbed queries of (layer, sequence b, head h)
+__device__ __forceinline__ float* qc_of(const Params& p, int layer, int b, int h) {
+  return p.qc + (((size_t)layer * p.B + b) * p.NH + h) * MLA_KVL;
+}
+
 // P1b: q_c[b][h][i] = sum_d q_nope[b][h][d] * W_UK[h][d][i] (reference_decode.py:245-249), the canonical dot of
-// the W_UK^T row (h, i) (qk_nope long) with the bf16 q_nope of (b, h), kept in fp32; and the new latent rows
+// the W_UK^T row (h, i) (qk_nope long) with the bf16 q_nope of (b, h), kept in fp32
 template <int B, class S, class Wait>
 __device__ __forceinline__ void phase_absorb_b(const Params& p, int layer, S& s, Wait wait) {
   using WR = Bf16Row<MLA_NOPE>;
@@ -146,7 +152,7 @@ __device__ __forceinline__ void phase_absorb_b(const Params& p, int layer, S& s,
       [&](int) { return nb; },
       [&](int g, int b) { return (const uint16_t*)(s.v.xs + (b * NH + (g * NR) / MLA_KVL) * MLA_NOPE); },
       [&](int g, int nv, const float(&v)[NR][B]) {
-        lane_store_b<NR, B>(v, nv, [&](int i, int b, float val) { st_ag(p.qc + (size_t)b * rows + g * NR + i, val); });
+        lane_store_b<NR, B>(v, nv, [&](int i, int b, float val) { st_ag(qc_of(p, layer, b, 0) + g * NR + i, val); });
       },
       [&]() {
         if (!wait()) return false;
@@ -162,8 +168,6 @@ __device__ __forceinline__ void phase_absorb_b(const Params& p, int layer, S& s,
           for (int e = 0; e < 8; e += 2) o[e / 2] = (uint32_t)f2bf(v[e]) | ((uint32_t)f2bf(v[e + 1]) << 16);
           *(u32x4*)(s.v.xs + 8 * c) = u32x4{o[0], o[1], o[2], o[3]};
         }
-        for (int b = 0; b < nb; ++b)
-          if ((int)blockIdx.x == p.nwg - 1 - b && wave_u() == 0) latent_row(p, Lw, b);
         __syncthreads();
         return true;
       },
@@ -184,17 +188,17 @@ __device__ __forceinline__ MlaItem mla_item(const Params& p, int item, int NHG) 
 // P2: absorbed attention over the latent cache (reference_decode.py:250-253 in chunked form).  Per item (sequence
 // b, head group, chunk c of positions 0..pos): s_t = ((q_c . c_t over kv_lora, one ascending fma chain) +
 // (q_pe . k_pe_t over qk_rope, ascending)) * scale; the chunk's max m, p_t = exp(s_t - m), l = sum p_t and
-// a[i] = sum_t p_t c_t[i] (ascending t).  The last chunk of (b, head group) to arrive merges: M = max m_c,
-// w_c = exp(m_c - M), L = sum w_c l_c, A = sum w_c a_c (ascending c), o_c = A / L in fp32.
+// a[i] = sum_t p_t c_t[i] (ascending t) -> the chunk partial (a, m, l).  The merge follows in P2c.
 template <int B, class S, class Wait>
 __device__ __forceinline__ void phase_mla_attn(const Params& p, int layer, S& s, Wait wait) {
+  static_assert(MLA_G == NWAVE, "one head per wave");
   const int NH = p.NH, GH = NH < MLA_G ? NH : MLA_G, NHG = NH / GH, BS = p.BS;
   const int nitems = p.ibase[p.B];
   const LayerW Lw = layer_w(p, layer);
   const int lane = lane_id(), wave = wave_u();
   // the chunk's cached latent rows, HBM -> LDS (global_load_lds, 16 bytes per lane): wave w copies groups w, w+8, ...
   // (the rows do not depend on this step, so the first item's copies are issued before the wait; the current
-  // position comes from p.cnew instead)
+  // position's row is computed here instead)
   auto load_tile = [&](const MlaItem& it) {
     const int t0 = it.c * CHUNK, n = it.pos + 1;
     const int g16 = t0 + (lane & ~15);                   // the swizzle permutes inside 16 positions: one block
@@ -210,70 +214,81 @@ __device__ __forceinline__ void phase_mla_attn(const Params& p, int layer, S& s,
   if (!wait()) return;
   for (int item = blockIdx.x; item < nitems; item += p.nwg) {
     const MlaItem it = mla_item(p, item, NHG);
-    const int b = it.b, c = it.c, pos = it.pos, n = pos + 1, nch = (n + CHUNK - 1) / CHUNK;
+    const int b = it.b, c = it.c, pos = it.pos, n = pos + 1;
     const int t0 = c * CHUNK, len = min(CHUNK, n - t0);
     const bool has_new = pos < t0 + len;
     if (item != (int)blockIdx.x) load_tile(it);
-    const float* qkv = p.qkv + (size_t)b * p.nqkv;
-    for (int j = wave; j < GH; j += NWAVE) {              // queries of head hg*GH + j
-      const int h = it.hg * GH + j;
-      const float* qc = p.qc + ((size_t)b * NH + h) * MLA_KVL;
-      float v[MLA_KVL / 64];
+    // queries of head hg*GH + wave, in registers: q_c dims lane + 64e (agent-scope loads: written by P1b), and q_pe
+    // roped (reference_decode.py:235): lane i < 32 holds dims i (lo) and i + 32 (hi).  The score loop takes each
+    // dim's value from its lane with v_readlane: wave-uniform operands with no memory wait in the dependent chain.
+    const int j = wave, h = it.hg * GH + j;
+    float qv[MLA_KVL / 64], qlo = 0.0f, qhi = 0.0f;
+    if (j < GH) {
+      const float* qc = qc_of(p, layer, b, h);
 #pragma unroll
-      for (int e = 0; e < MLA_KVL / 64; ++e) v[e] = ld_ag(qc + lane + 64 * e);
-      if (lane < MLA_R / 2) {                             // q_pe roped (reference_decode.py:235)
-        const float* qp = qkv + h * MLA_QD + MLA_NOPE;
+      for (int e = 0; e < MLA_KVL / 64; ++e) qv[e] = ld_ag(qc + lane + 64 * e);
+      if (lane < MLA_R / 2) {
+        const float* qp = p.qkv + (size_t)b * p.nqkv + h * MLA_QD + MLA_NOPE;
         const float a0 = ld_ag(qp + 2 * lane), a1 = ld_ag(qp + 2 * lane + 1);
         const float cs = ld_f(p.rope_cos + (size_t)pos * (MLA_R / 2) + lane);
         const float sn = ld_f(p.rope_sin + (size_t)pos * (MLA_R / 2) + lane);
-        float lo, hi;
-        rope_ds_pair(a0, a1, cs, sn, lo, hi);
-        s.a.qpe[j][lane] = lo;
-        s.a.qpe[j][lane + MLA_R / 2] = hi;
+        rope_ds_pair(a0, a1, cs, sn, qlo, qhi);
       }
-#pragma unroll
-      for (int e = 0; e < MLA_KVL / 64; ++e) s.a.qc[j][lane + 64 * e] = v[e];
     }
-    if (has_new && wave == NWAVE - 1)
-      for (int k = lane; k < MLA_CD; k += 64) s.a.cn[k] = ld_ag(p.cnew + (size_t)b * MLA_CD + k);
+    // the chunk holding the current position builds its latent row (the first head group appends it to the cache)
+    if (has_new && wave == NWAVE - 1) latent_row(p, Lw, b, it.hg == 0, s.a.cn);
     __builtin_amdgcn_s_waitcnt(0);                        // this wave's tile copies have landed in LDS
     __syncthreads();
     if (has_new && (int)threadIdx.x < MLA_CG) {           // the current position's row into its slots
-      const int j = threadIdx.x, tn = pos - t0;
+      const int jj = threadIdx.x, tn = pos - t0;
       uint32_t o[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) o[e] = (uint32_t)f2bf(s.a.cn[8 * j + 2 * e]) | ((uint32_t)f2bf(s.a.cn[8 * j + 2 * e + 1]) << 16);
-      s.a.t[j][tn ^ (j & 15)] = u32x4{o[0], o[1], o[2], o[3]};
+      for (int e = 0; e < 4; ++e) o[e] = (uint32_t)f2bf(s.a.cn[8 * jj + 2 * e]) | ((uint32_t)f2bf(s.a.cn[8 * jj + 2 * e + 1]) << 16);
+      s.a.t[jj][tn ^ (jj & 15)] = u32x4{o[0], o[1], o[2], o[3]};
     }
     __syncthreads();
     // scores: wave = head, lane = position
-    for (int j = wave; j < GH; j += NWAVE) {
+    if (j < GH) {
+      auto bcast = [](float v, int l) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l)); };
       float s1 = 0.0f, s2 = 0.0f;
-#pragma unroll 8
-      for (int g = 0; g < MLA_KVL / 8; ++g) {
-        const u32x4 kw = s.a.t[g][lane ^ (g & 15)];
-        const float4 qa = *(const float4*)&s.a.qc[j][8 * g], qb = *(const float4*)&s.a.qc[j][8 * g + 4];
-        s1 = __builtin_fmaf(qa.x, bf_lo(kw[0]), s1);
-        s1 = __builtin_fmaf(qa.y, bf_hi(kw[0]), s1);
-        s1 = __builtin_fmaf(qa.z, bf_lo(kw[1]), s1);
-        s1 = __builtin_fmaf(qa.w, bf_hi(kw[1]), s1);
-        s1 = __builtin_fmaf(qb.x, bf_lo(kw[2]), s1);
-        s1 = __builtin_fmaf(qb.y, bf_hi(kw[2]), s1);
-        s1 = __builtin_fmaf(qb.z, bf_lo(kw[3]), s1);
-        s1 = __builtin_fmaf(qb.w, bf_hi(kw[3]), s1);
-      }
+      // tile reads run one block of 4 groups ahead of the fma chain; a group's 8 query values are broadcast first
+      constexpr int GB = 4, NB = MLA_CG / GB;
+      u32x4 kA[GB], kB[GB];
+      auto ld = [&](u32x4(&k)[GB], int blk) {
 #pragma unroll
-      for (int g = 0; g < MLA_R / 8; ++g) {
-        const u32x4 kw = s.a.t[MLA_KVL / 8 + g][lane ^ (g & 15)];
-        const float4 qa = *(const float4*)&s.a.qpe[j][8 * g], qb = *(const float4*)&s.a.qpe[j][8 * g + 4];
-        s2 = __builtin_fmaf(qa.x, bf_lo(kw[0]), s2);
-        s2 = __builtin_fmaf(qa.y, bf_hi(kw[0]), s2);
-        s2 = __builtin_fmaf(qa.z, bf_lo(kw[1]), s2);
-        s2 = __builtin_fmaf(qa.w, bf_hi(kw[1]), s2);
-        s2 = __builtin_fmaf(qb.x, bf_lo(kw[2]), s2);
-        s2 = __builtin_fmaf(qb.y, bf_hi(kw[2]), s2);
-        s2 = __builtin_fmaf(qb.z, bf_lo(kw[3]), s2);
-        s2 = __builtin_fmaf(qb.w, bf_hi(kw[3]), s2);
+        for (int u = 0; u < GB; ++u) {
+          const int g = blk * GB + u;
+          k[u] = s.a.t[g][lane ^ (g & 15)];
+        }
+      };
+      auto qdim = [&](int i) -> float {                   // dim i of [q_c; q_pe]
+        if (i < MLA_KVL) return bcast(qv[i >> 6], i & 63);
+        const int d = i - MLA_KVL;
+        return d < MLA_R / 2 ? bcast(qlo, d) : bcast(qhi, d - MLA_R / 2);
+      };
+      auto acc = [&](const u32x4(&k)[GB], int blk) {
+#pragma unroll
+        for (int u = 0; u < GB; ++u) {
+          const int g = blk * GB + u;
+          float q[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) q[e] = qdim(8 * g + e);
+          float& sa = g < MLA_KVL / 8 ? s1 : s2;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            sa = __builtin_fmaf(q[2 * e], bf_lo(k[u][e]), sa);
+            sa = __builtin_fmaf(q[2 * e + 1], bf_hi(k[u][e]), sa);
+          }
+        }
+      };
+      static_assert(NB % 2 == 0 && (MLA_KVL / 8) % GB == 0, "whole blocks, pairs of blocks");
+      ld(kA, 0);
+#pragma unroll
+      for (int blk = 0; blk < NB; blk += 2) {
+        ld(kB, blk + 1);
+        acc(kA, blk);
+        if (blk + 2 < NB) ld(kA, blk + 2);
+        acc(kB, blk + 1);
       }
       const bool valid = lane < len;
       const float sc = valid ? (s1 + s2) * p.attn_scale : -__builtin_huge_valf();
@@ -283,7 +298,7 @@ __device__ __forceinline__ void phase_mla_attn(const Params& p, int layer, S& s,
     }
     __syncthreads();
     // P.V: wave = head, lane = dim group (dims 8 lane .. 8 lane + 7), positions ascending
-    for (int j = wave; j < GH; j += NWAVE) {
+    if (j < GH) {
       float a[8], l = 0.0f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) a[e] = 0.0f;
@@ -306,121 +321,99 @@ __device__ __forceinline__ void phase_mla_attn(const Params& p, int layer, S& s,
         step(t + 3, pq.w);
       }
       for (; t < len; ++t) step(t, s.a.p[j][t]);
-      const int h = it.hg * GH + j;
       float* part = p.apart + (((size_t)b * NH + h) * MAX_CHUNKS + c) * MLA_PART;
 #pragma unroll
       for (int e = 0; e < 8; e += 2) st_ag2(part + 8 * lane + e, a[e], a[e + 1]);
       if (lane == 0) st_ag2(part + MLA_KVL, s.a.m[j], l);
     }
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    uint32_t* cnt = p.acnt + ((size_t)b * NHG + it.hg) * 64;
-    if (threadIdx.x == 0)
-      s.last = (__hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u == (uint32_t)nch);
-    __syncthreads();
-    if (s.last) {
-      for (int j = wave; j < GH; j += NWAVE) {
-        const int h = it.hg * GH + j;
-        const float* part = p.apart + ((size_t)b * NH + h) * MAX_CHUNKS * MLA_PART;
-        float mloc = -__builtin_huge_valf(), lloc = 0.0f, mhi = -__builtin_huge_valf(), lhi = 0.0f;
-        if (lane < nch) ld_ag2(part + (size_t)lane * MLA_PART + MLA_KVL, mloc, lloc);
-        if (lane + 64 < nch) ld_ag2(part + (size_t)(lane + 64) * MLA_PART + MLA_KVL, mhi, lhi);
-        const float M = wave_max(fmaxf(mloc, mhi));
-        s.a.p[j][lane] = lane < nch ? expf_mk(mloc - M) : 0.0f;
-        s.a.p[j][64 + lane] = lane + 64 < nch ? expf_mk(mhi - M) : 0.0f;
-        s.a.p[j][MAX_CHUNKS + lane] = lloc;
-        s.a.p[j][MAX_CHUNKS + 64 + lane] = lhi;
-        float A[8], L = 0.0f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) A[e] = 0.0f;
-        constexpr int MB = 4;                             // chunks whose loads are in flight together
-        for (int c0 = 0; c0 < nch; c0 += MB) {
-          float av[MB][8];
-#pragma unroll
-          for (int u = 0; u < MB; ++u) {
-            const int cc = min(c0 + u, nch - 1);          // past the last chunk: a repeat, never used
-#pragma unroll
-            for (int e = 0; e < 8; e += 2) ld_ag2(part + (size_t)cc * MLA_PART + 8 * lane + e, av[u][e], av[u][e + 1]);
-          }
-#pragma unroll
-          for (int u = 0; u < MB; ++u)
-            if (c0 + u < nch) {
-              const float wc = s.a.p[j][c0 + u];
-              L = __builtin_fmaf(wc, s.a.p[j][MAX_CHUNKS + c0 + u], L);
-#pragma unroll
-              for (int e = 0; e < 8; ++e) A[e] = __builtin_fmaf(wc, av[u][e], A[e]);
-            }
-        }
-        // o_c in the W_UV rows' stored order (lane l of that GEMV holds dims l, l+64, ..., l+448)
-        float* oc = p.oc + ((size_t)b * NH + h) * MLA_KVL;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) st_ag(oc + perm_stored(8 * lane + e, MLA_KVL), A[e] / L);
-      }
-      if (threadIdx.x == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __syncthreads();
+    __syncthreads();                                      // the tile and p are free for the next item
   }
 }
 
-// P2c: out[b][h*v_head + d] = bfr(W_UV[h][d] . o_c[b][h]) (reference_decode.py:254-256), the canonical dot of a
-// kv_lora-long bf16 row with the fp32 o_c; written as the O projection's lane-permuted bf16 rows.  Workgroup w owns
-// rows [w*R, w*R + R) (R <= v_head, so at most two heads); their o_c rows are staged in LDS once.
+// P2c: per (sequence b, head h, quarter of its v_head rows): the merge of the chunk partials (M = max m_c,
+// w_c = exp(m_c - M), L = sum w_c l_c, A = sum w_c a_c in ascending c, o_c = A / L in fp32), then
+// out[b][h*v_head + d] = bfr(W_UV[h][d] . o_c) (reference_decode.py:254-256), the canonical dot of a kv_lora-long
+// bf16 row with the fp32 o_c, written as the O projection's lane-permuted bf16 rows.  Thread i merges dim i.
 template <int B, class S, class Wait>
 __device__ __forceinline__ void phase_wuv_b(const Params& p, int layer, S& s, Wait wait) {
   using WR = Bf16Row<MLA_KVL>;
-  constexpr int D = 8;                                    // rows of a wave in flight
-  static_assert(B * 2 * MLA_KVL * 2 <= S::XCAP, "o_c rows exceed the LDS budget");
+  constexpr int Q = 4, RQ = MLA_VH / Q, RW = RQ / NWAVE;  // quarters, rows per quarter, rows per wave
+  constexpr int CB = 32;                                  // chunks whose partial loads are in flight together
+  static_assert(NT == MLA_KVL, "one thread per latent dim");
   const LayerW Lw = layer_w(p, layer);
-  const int NH = p.NH, rows = NH * MLA_VH, nb = p.B, lane = lane_id(), wave = wave_u();
-  const int R = (rows + p.nwg - 1) / p.nwg, r0 = (int)blockIdx.x * R, r1 = min(rows, r0 + R);
-  const int h0 = r0 / MLA_VH, nh = r0 < r1 ? (r1 - 1) / MLA_VH - h0 + 1 : 0;
-  float* xs = (float*)s.v.xs;                             // [b][head - h0][kv_lora]
-  typename WR::Regs W[D];
-  auto issue = [&](int r) {
-#pragma unroll
-    for (int d = 0; d < D; ++d)
-      if (r + NWAVE * d < r1) WR::load(W[d], mrow<WR>(Lw.wuv, r + NWAVE * d), lane);
+  const int NH = p.NH, KA = NH * MLA_VH, nitems = p.B * NH * Q;
+  const int lane = lane_id(), wave = wave_u(), tid = threadIdx.x;
+  float* sw = &s.a.p[0][0];                               // chunk weights w_c
+  float* sl = &s.a.p[1][0];                               // chunk sums l_c
+  float* xo = s.a.xo;
+  typename WR::Regs W[RW];
+  auto rows_of = [&](int item, int& b, int& h, int& d0) {
+    b = item / (NH * Q);
+    const int r = item - b * NH * Q;
+    h = r / Q;
+    d0 = (r % Q) * RQ + wave * RW;
   };
-  int r = r0 + wave;
-  issue(r);
+  auto issue = [&](int item) {
+    int b, h, d0;
+    rows_of(item, b, h, d0);
+#pragma unroll
+    for (int k = 0; k < RW; ++k) WR::load(W[k], mrow<WR>(Lw.wuv, (size_t)h * MLA_VH + d0 + k), lane);
+  };
+  if ((int)blockIdx.x < nitems) issue(blockIdx.x);
   if (!wait()) return;
-  for (int b = 0; b < nb; ++b)
-    copy_rows_lds((const uint16_t*)(p.oc + ((size_t)b * NH + h0) * MLA_KVL), nh * MLA_KVL * 2,
-                  (uint16_t*)(xs + (size_t)b * 2 * MLA_KVL));
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  for (; r < r1; r += D * NWAVE) {
+  for (int item = blockIdx.x; item < nitems; item += p.nwg) {
+    int b, h, d0;
+    rows_of(item, b, h, d0);
+    if (item != (int)blockIdx.x) issue(item);
+    const int nch = p.posb[b] / CHUNK + 1;
+    const float* part = p.apart + ((size_t)b * NH + h) * MAX_CHUNKS * MLA_PART;
+    float av[CB];
+    auto load_a = [&](int c0) {
 #pragma unroll
-    for (int d = 0; d < D; ++d) {
-      const int rr = r + NWAVE * d;
-      if (rr < r1) {
-        const int hl = rr / MLA_VH - h0;
-        float v[B];
-#pragma unroll
-        for (int b = 0; b < B; ++b) {
-          v[b] = 0.0f;
-          if (b < nb) {
-            const float* x = xs + ((size_t)b * 2 + hl) * MLA_KVL + 8 * lane;
-            const float4 x0 = *(const float4*)x, x1 = *(const float4*)(x + 4);
-            const u32x4 w = W[d].w[0];
-            float acc = 0.0f;
-            acc = __builtin_fmaf(bf_lo(w[0]), x0.x, acc);
-            acc = __builtin_fmaf(bf_hi(w[0]), x0.y, acc);
-            acc = __builtin_fmaf(bf_lo(w[1]), x0.z, acc);
-            acc = __builtin_fmaf(bf_hi(w[1]), x0.w, acc);
-            acc = __builtin_fmaf(bf_lo(w[2]), x1.x, acc);
-            acc = __builtin_fmaf(bf_hi(w[2]), x1.y, acc);
-            acc = __builtin_fmaf(bf_lo(w[3]), x1.z, acc);
-            acc = __builtin_fmaf(bf_hi(w[3]), x1.w, acc);
-            v[b] = wave_sum(acc);
-          }
-        }
-#pragma unroll
-        for (int b = 0; b < B; ++b)
-          if (lane == b && b < nb) st_ag_u16(p.o16 + (size_t)b * rows + perm_stored(rr, rows), f2bf(v[b]));
-      }
+      for (int u = 0; u < CB; ++u) av[u] = ld_ag(part + (size_t)min(c0 + u, nch - 1) * MLA_PART + tid);
+    };
+    load_a(0);
+    if (wave == 0) {                                      // chunk weights and sums (lane c holds chunks c, c + 64)
+      float m0 = -__builtin_huge_valf(), l0 = 0.0f, m1 = -__builtin_huge_valf(), l1 = 0.0f;
+      if (lane < nch) ld_ag2(part + (size_t)lane * MLA_PART + MLA_KVL, m0, l0);
+      if (lane + 64 < nch) ld_ag2(part + (size_t)(lane + 64) * MLA_PART + MLA_KVL, m1, l1);
+      const float M = wave_max(fmaxf(m0, m1));
+      sw[lane] = lane < nch ? expf_mk(m0 - M) : 0.0f;
+      sw[64 + lane] = lane + 64 < nch ? expf_mk(m1 - M) : 0.0f;
+      sl[lane] = l0;
+      sl[64 + lane] = l1;
     }
-    if (r + D * NWAVE < r1) issue(r + D * NWAVE);
+    __syncthreads();
+    float A = 0.0f, L = 0.0f;
+    for (int c0 = 0; c0 < nch; c0 += CB) {
+      if (c0 > 0) load_a(c0);
+#pragma unroll
+      for (int u = 0; u < CB; ++u)
+        if (c0 + u < nch) {
+          const float wc = sw[c0 + u];
+          L = __builtin_fmaf(wc, sl[c0 + u], L);
+          A = __builtin_fmaf(wc, av[u], A);
+        }
+    }
+    xo[perm_stored(tid, MLA_KVL)] = A / L;
+    __syncthreads();
+    const float4 x0 = *(const float4*)&xo[8 * lane], x1 = *(const float4*)&xo[8 * lane + 4];
+#pragma unroll
+    for (int k = 0; k < RW; ++k) {
+      const u32x4 w = W[k].w[0];
+      float acc = 0.0f;
+      acc = __builtin_fmaf(bf_lo(w[0]), x0.x, acc);
+      acc = __builtin_fmaf(bf_hi(w[0]), x0.y, acc);
+      acc = __builtin_fmaf(bf_lo(w[1]), x0.z, acc);
+      acc = __builtin_fmaf(bf_hi(w[1]), x0.w, acc);
+      acc = __builtin_fmaf(bf_lo(w[2]), x1.x, acc);
+      acc = __builtin_fmaf(bf_hi(w[2]), x1.y, acc);
+      acc = __builtin_fmaf(bf_lo(w[3]), x1.z, acc);
+      acc = __builtin_fmaf(bf_hi(w[3]), x1.w, acc);
+      acc = wave_sum(acc);
+      if (lane == 0) st_ag_u16(p.o16 + (size_t)b * KA + perm_stored(h * MLA_VH + d0 + k, KA), f2bf(acc));
+    }
+    __syncthreads();                                      // xo, sw, sl are free for the next item
   }
 }
 
