@@ -166,6 +166,57 @@ int check_ds(const etxmk_config* c) {
   return ETXMK_OK;
 }
 
+// the symbol of the persistent kernel a step of this configuration launches, its batch capacity, or nullptr
+const char* kernel_symbol(const etxmk_config& c, int* cap) {
+  const int km = c.moe ? c.MI : c.I;
+  if (c.arch == ETXMK_ARCH_DSV2) {
+#define MK_NAME_DS(name, h_, ka_, km_, ksh_, e_, ip_, b_)                                                          \
+    if (c.H == h_ && c.NH * c.v_head == ka_ && c.MI == km_ && ds_si(c) == ksh_ && c.E == e_ &&                   \
+        (c.first_dense == 0 || ds_ip(c) == ip_) && c.batch <= b_) {                                               \
+      *cap = b_;                                                                                                  \
+      return #name;                                                                                               \
+    }
+    MK_DS_SHAPES(MK_NAME_DS)
+#undef MK_NAME_DS
+    return nullptr;
+  }
+  if (c.batch == 1) {
+#define MK_NAME(name, h_, ka_, km_, moe_, e_, fp8_)                                                               \
+    if (c.H == h_ && c.NH * c.HD == ka_ && km == km_ && (c.moe != 0) == moe_ && (!moe_ || c.E == e_) &&          \
+        (c.wdtype == ETXMK_W_FP8) == fp8_) {                                                                      \
+      *cap = 1;                                                                                                   \
+      return #name;                                                                                               \
+    }
+    MK_FUSED_SHAPES_BF16(MK_NAME)
+    MK_FUSED_SHAPES_FP8(MK_NAME)
+#undef MK_NAME
+    return nullptr;
+  }
+  const char* best = nullptr;
+  int bc = 0;
+#define MK_NAME_B(name, h_, ka_, km_, moe_, e_, fp8_, b_)                                                         \
+  if (c.H == h_ && c.NH * c.HD == ka_ && km == km_ && (c.moe != 0) == moe_ && (!moe_ || c.E == e_) &&            \
+      (c.wdtype == ETXMK_W_FP8) == fp8_ && c.batch <= b_ && (!best || b_ < bc)) {                                 \
+    best = #name;                                                                                                 \
+    bc = b_;                                                                                                      \
+  }
+  MK_BATCH_SHAPES_BF16(MK_NAME_B)
+  MK_BATCH_SHAPES_FP8(MK_NAME_B)
+#undef MK_NAME_B
+  *cap = bc;
+  return best;
+}
+
+// grid barriers of a step over layers [l0, l1) (plus the head): one per phase
+int barriers_of(const etxmk_config& c, int l0, int l1, int head) {
+  if (c.arch == ETXMK_ARCH_DSV2) {                         // 5 attention phases, then 2 dense or 3 MoE phases
+    int n = 0;
+    for (int l = l0; l < l1; ++l) n += l < c.first_dense ? 7 : 8;
+    return n + (head ? 1 : 0);
+  }
+  return (c.moe ? 6 : 5) * (l1 - l0) + (head ? 1 : 0);
+}
+
 int check_config(const etxmk_config* c) {
   if (!c) return fail(ETXMK_EINVAL, "config is NULL");
   if (c->H <= 0 || c->NH <= 0 || c->NKV <= 0 || c->L <= 0 || c->V <= 0) return fail(ETXMK_EINVAL, "non-positive dimension");
@@ -379,14 +430,7 @@ struct etxmk_handle {
     const TensorSlot* s = slot(kind, layer);
     return s ? (const uint8_t*)(w + s->off) : nullptr;
   }
-  int barriers(int l0, int l1, int head) const {
-    if (c.arch == ETXMK_ARCH_DSV2) {                       // 5 attention phases, then 2 dense or 3 MoE phases
-      int n = 0;
-      for (int l = l0; l < l1; ++l) n += l < c.first_dense ? 7 : 8;
-      return n + (head ? 1 : 0);
-    }
-    return (c.moe ? 6 : 5) * (l1 - l0) + (head ? 1 : 0);
-  }
+  int barriers(int l0, int l1, int head) const { return barriers_of(c, l0, l1, head); }
 };
 
 extern "C" {
@@ -412,6 +456,26 @@ int etxmk_workspace_bytes(const etxmk_config* cfg, uint64_t* bytes) {
   if (int r = check_config(cfg)) return r;
   if (!bytes) return fail(ETXMK_EINVAL, "bytes is NULL");
   *bytes = ws_layout(cfg).total;
+  return ETXMK_OK;
+}
+
+int etxmk_plan(const etxmk_config* cfg, int32_t fused, etxmk_plan_info* out) {
+  if (int r = check_config(cfg)) return r;
+  if (!out) return fail(ETXMK_EINVAL, "out is NULL");
+  const etxmk_config& c = *cfg;
+  if (!fused && (c.batch > 1 || c.wdtype == ETXMK_W_FP8 || c.arch == ETXMK_ARCH_DSV2))
+    return fail(ETXMK_EINVAL, "the unfused mode runs bf16 Qwen3 handles at batch 1 only");
+  memset(out, 0, sizeof *out);
+  int cap = 1;
+  const char* sym = fused ? kernel_symbol(c, &cap) : "unfused";
+  if (!sym) return fail(ETXMK_EINVAL, "no persistent kernel for this shape (use the unfused mode)");
+  snprintf(out->kernel, sizeof out->kernel, "%s", sym);
+  out->barriers_per_step = barriers_of(c, 0, c.L, 1);
+  out->threads = NT;
+  out->batch_capacity = cap;
+  weight_layout(cfg, &out->weight_bytes);
+  out->kv_bytes = 2ull * kv_pools(cfg) * kv_layer_elems(cfg) * (uint64_t)c.L;
+  out->workspace_bytes = ws_layout(cfg).total;
   return ETXMK_OK;
 }
 

@@ -46,6 +46,12 @@ class EtxmkConfig(C.Structure):
                                          "beta_slow")] + [("rope_orig_max", C.c_int32)]
 
 
+class EtxmkPlanInfo(C.Structure):
+    _fields_ = [("kernel", C.c_char * 96), ("barriers_per_step", C.c_int32), ("threads", C.c_int32),
+                ("batch_capacity", C.c_int32), ("reserved", C.c_int32), ("weight_bytes", C.c_uint64),
+                ("kv_bytes", C.c_uint64), ("workspace_bytes", C.c_uint64)]
+
+
 W_BF16, W_FP8 = 0, 1          # weight types of etxmk_config.wdtype
 ARCH_QWEN3, ARCH_DSV2 = 0, 1  # etxmk_config.arch
 
@@ -159,6 +165,7 @@ def load(path: Path | None = None):
         "etxmk_set_grid": [vp, i32],
         "etxmk_barriers_per_step": [vp, C.POINTER(i32)],
         "etxmk_set_trace": [vp, vp],
+        "etxmk_plan": [C.POINTER(EtxmkConfig), i32, C.POINTER(EtxmkPlanInfo)],
     }
     for name, args in sig.items():
         f = getattr(L, name)
@@ -189,6 +196,32 @@ def sizes(cfg: ModelConfig) -> dict:
         _check(L, fn(C.byref(c), C.byref(v)))
         out[key] = int(v.value)
     return out
+
+
+def plan_info(cfg: ModelConfig, fused: bool = True) -> dict:
+    """The library's plan of a configuration (no GPU needed): the persistent kernel symbol (or "unfused"), grid
+    barriers per step, threads per workgroup, the kernel's batch capacity and the buffer sizes."""
+    L = load()
+    c = cfg.as_struct()
+    out = EtxmkPlanInfo()
+    _check(L, L.etxmk_plan(C.byref(c), int(fused), C.byref(out)))
+    return {"kernel": out.kernel.decode(), "barriers_per_step": int(out.barriers_per_step), "threads": int(out.threads),
+            "batch_capacity": int(out.batch_capacity), "weight_bytes": int(out.weight_bytes),
+            "kv_bytes": int(out.kv_bytes), "workspace_bytes": int(out.workspace_bytes)}
+
+
+def phase_names(cfg: ModelConfig) -> list[list[str]]:
+    """The phases of one step, layer by layer (each ends in a grid barrier), then ["head"] (the lm_head phase; the
+    token write after it ends the step)."""
+    if cfg.arch == ARCH_DSV2:
+        att = ["qkv", "absorb", "attn", "wuv", "oproj"]
+        layers = [att + (["gateup", "down"] if l < cfg.first_dense else ["router_shared", "expert_up", "expert_down"])
+                  for l in range(cfg.L)]
+    elif cfg.moe:
+        layers = [["qkv", "attn", "oproj", "router", "expert_up", "expert_down"] for _ in range(cfg.L)]
+    else:
+        layers = [["qkv", "attn", "oproj", "gateup", "down"] for _ in range(cfg.L)]
+    return layers + [["head"]]
 
 
 def unpermute_rows(stored: np.ndarray, block: int = 512) -> np.ndarray:
@@ -391,6 +424,11 @@ class Decoder:
         else:
             _check(self.L, self.L.etxmk_set_trace(self.h, None))
             self._trace = None
+
+    def trace_ticks(self) -> np.ndarray:
+        """Raw stamps of the last traced step: uint64 [barriers + 1][workgroups][3] of the 100 MHz clock."""
+        self.sync()
+        return self._trace.cpu().numpy().view(np.uint64).reshape(self.barriers_per_step() + 1, self.workgroups(), 3)
 
     def trace(self) -> np.ndarray:
         """Stamps of the last traced step in microseconds from the launch:

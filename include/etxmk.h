@@ -187,6 +187,20 @@ int etxmk_set_grid(etxmk_handle* h, int32_t workgroups);
 /* Grid barriers executed by one step (diagnostics). */
 int etxmk_barriers_per_step(etxmk_handle* h, int32_t* n);
 
+/* The plan of a configuration, without a GPU: the persistent kernel a step launches (its symbol, or "unfused" for
+ * the per-phase kernels), the grid barriers of one step, threads per workgroup, the batch capacity of the kernel and
+ * the three buffer sizes.  Reference: the planned-workload record of etx.api.plan (docs/core/API.md:47-49) and the
+ * `types` / grid data of the build's plan.json (etx/codegen/plan_header.py). */
+typedef struct etxmk_plan_info {
+  char kernel[96];
+  int32_t barriers_per_step;
+  int32_t threads;
+  int32_t batch_capacity;
+  int32_t reserved;
+  uint64_t weight_bytes, kv_bytes, workspace_bytes;
+} etxmk_plan_info;
+int etxmk_plan(const etxmk_config* cfg, int32_t fused, etxmk_plan_info* out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -12,15 +12,11 @@ import pytest
 from oracle import oracle as O
 from etx.runtime import native as N
 from etx.models import configs
+from progress_log import say
 
 pytestmark = pytest.mark.gpu
 
 SEED = 20261201
-
-
-def say(*a):
-    print(*a, flush=True)
-    sys.stdout.flush()
 
 
 def rel(a, b):
