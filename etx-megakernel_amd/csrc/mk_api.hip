@@ -224,7 +224,7 @@ int check_config(const etxmk_config* c) {
   if (c->arch == ETXMK_ARCH_DSV2) return check_ds(c);
   if (c->HD != HDIM) return fail(ETXMK_EINVAL, "head_dim %d unsupported (the attention phase is built for %d)", c->HD, HDIM);
   if (c->NH % c->NKV) return fail(ETXMK_EINVAL, "NH %d not a multiple of NKV %d", c->NH, c->NKV);
-  if (c->NH / c->NKV > MAX_G) return fail(ETXMK_EINVAL, "%d q heads per kv head (at most %d)", c->NH / c->NKV, MAX_G);
+  if (c->NH / c->NKV > NWAVE) return fail(ETXMK_EINVAL, "%d q heads per kv head (at most %d)", c->NH / c->NKV, NWAVE);
   if (c->H > MAX_H || !k_in(c->H, {MK_K_HIDDEN})) return fail(ETXMK_EINVAL, "hidden size %d unsupported", c->H);
   if (!k_in(c->NH * c->HD, {MK_K_ATTN})) return fail(ETXMK_EINVAL, "NH*HD %d unsupported", c->NH * c->HD);
   if (c->batch < 1 || c->batch > MAX_B) return fail(ETXMK_EINVAL, "batch %d outside 1..%d", c->batch, MAX_B);
@@ -889,12 +889,13 @@ static int launch(etxmk_handle* h, const int32_t* posv, int pos, int write_next,
     p.qc = h->wsptr<float>(h->ws.qc);
     p.h16s = h->wsptr<uint16_t>(h->ws.h16s);
   }
-  // attention items: per 64-position chunk of each sequence, NKV (Qwen3) or one per group of 8 heads (DeepSeek-V2)
-  const int per_chunk = ds ? ds_nhg(c) : c.NKV;
+  // attention items of each sequence: DeepSeek-V2 one per (group of 8 heads, 64-position chunk); Qwen3 one per
+  // (kv head, ATTN_CPI_B chunks) in batched kernels (the single-sequence kernel counts its own, one chunk each)
   p.ibase[0] = 0;
   for (int b = 0; b < c.batch; ++b) {
     p.posb[b] = batched ? posv[b] : pos;
-    p.ibase[b + 1] = p.ibase[b] + per_chunk * (p.posb[b] / CHUNK + 1);
+    const int nch = p.posb[b] / CHUNK + 1;
+    p.ibase[b + 1] = p.ibase[b] + (ds ? ds_nhg(c) * nch : c.NKV * ((nch + ATTN_CPI_B - 1) / ATTN_CPI_B));
   }
   if (h->fused) {
     const void* fn = ds ? ds_kernel(c) : batched ? batch_kernel(c) : fused_kernel(c);

@@ -23,6 +23,8 @@ namespace mk {
 
 constexpr int RES_ROWS = 64;            // residual rows per workgroup and sequence held for the epilogues
 constexpr int MAX_PAIRS = MAX_B * MAX_TOPK;
+constexpr int KEY_WORDS = MAX_E * MAX_B / 32;  // routed-pair keys expert * MAX_B + sequence, one bit each
+constexpr int ATTN_CPI_B = 2;           // chunks per attention item in batched kernels (one arrival per two chunks)
 
 template <int B>
 struct SmemB {
@@ -38,7 +40,7 @@ struct SmemB {
       float xres[B][RES_ROWS];          // residual of this workgroup's output rows
       float acc[B][RES_ROWS];           // expert combine carried from one pass over the pairs to the next
     } v;
-    AttnTiles a;
+    AttnTilesT<ATTN_CPI_B> a;
   };
   float rs[B];                          // 1/rms per sequence
   int32_t rids[B][MAX_TOPK];            // routing per sequence, slot order
@@ -49,6 +51,8 @@ struct SmemB {
   int32_t uexp[MAX_PAIRS];              // distinct experts ascending; expert u owns pairs [ustart[u], ustart[u + 1])
   int32_t ustart[MAX_PAIRS + 1];
   int32_t nexp;
+  uint32_t kbits[KEY_WORDS];            // routing: bitmap of the pairs' keys, then their prefix popcounts
+  uint32_t kpre[KEY_WORDS];
   int32_t abort, last, phase;
 };
 
@@ -69,24 +73,21 @@ __device__ __forceinline__ void copy_rows_lds(const uint16_t* src, int nelem, ui
 
 // The residual rows -> s.n.xr (bf16, natural order): the embedding rows of the sequences' tokens for the first
 // layer, else x16.  Then per sequence r = 1/sqrt(mean(x^2) + eps) with the sum of squares in dot order, and the
-// normed lane-permuted rows bfr(w * bfr(x * r)) -> s.n.xs (ref_numpy.py:71-73, as build_norm_x).
+// normed lane-permuted rows bfr(w * bfr(x * r)) -> s.n.xs (ref_numpy.py:71-73, as build_norm_x).  Thread t normalises
+// the 8 consecutive elements of chunk t % (H/8) in rows t / (H/8), t / (H/8) + 512 / (H/8), ...: one 16-byte read of
+// x and of w, eight 2-byte writes to their permuted positions.
 template <int H, int B, class S>
 __device__ __forceinline__ void build_norm_xb(const Params& p, bool first, const uint16_t* w, S& s) {
   static_assert(B * H <= S::NCAP, "residual rows exceed the LDS budget");
-  constexpr int C8 = H / 8, QPER = (C8 + NT - 1) / NT;
+  constexpr int C8 = H / 8, RSTEP = NT / C8;
+  static_assert(NT % C8 == 0, "a workgroup covers whole rows of chunks");
   const int nb = p.B, lane = lane_id(), wave = wave_u();
-  uint16_t wv[QPER][8];
-#pragma unroll
-  for (int j = 0; j < QPER; ++j) {
-    const int q = threadIdx.x + j * NT;
-    if (q < C8)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) wv[j][e] = ld_u16(w + perm_logical(8 * q + e, H));
-  }
+  const int c = (int)threadIdx.x % C8, b0 = (int)threadIdx.x / C8;
+  const u32x4 wv = ld16(w + 8 * c);
   if (first) {
-    for (int c = threadIdx.x; c < nb * C8; c += NT) {
-      const int b = c / C8, q = c - b * C8;
-      *(u32x4*)(s.n.xr + 8 * c) = ld16(p.embed + (size_t)token_of_b(p, b) * H + 8 * q);
+    for (int q = threadIdx.x; q < nb * C8; q += NT) {
+      const int b = q / C8, qq = q - b * C8;
+      *(u32x4*)(s.n.xr + 8 * q) = ld16(p.embed + (size_t)token_of_b(p, b) * H + 8 * qq);
     }
   } else {
     copy_rows_lds(p.x16, nb * H, s.n.xr);
@@ -95,31 +96,25 @@ __device__ __forceinline__ void build_norm_xb(const Params& p, bool first, const
   __syncthreads();
   for (int b = wave; b < nb; b += NWAVE) {
     float acc = 0.0f;
-#pragma unroll 8
-    for (int k = lane; k < H; k += 64) {
-      const float v = bf2f(s.n.xr[b * H + k]);
+#pragma unroll
+    for (int i = 0; i < H / 64; ++i) {
+      const float v = bf2f(s.n.xr[b * H + lane + 64 * i]);
       acc = __builtin_fmaf(v, v, acc);
     }
     acc = wave_sum(acc);
     if (lane == 0) s.rs[b] = 1.0f / __builtin_sqrtf(acc / (float)H + p.eps);
   }
   __syncthreads();
+  for (int b = b0; b < nb; b += RSTEP) {
+    const float r = s.rs[b];
+    const u32x4 xv = *(const u32x4*)(s.n.xr + b * H + 8 * c);
+    uint16_t* dst = s.n.xs + b * H;
 #pragma unroll
-  for (int j = 0; j < QPER; ++j) {
-    const int q = threadIdx.x + j * NT;
-    if (q < C8)
-      for (int b = 0; b < nb; ++b) {
-        const float r = s.rs[b];
-        uint32_t o[4];
-#pragma unroll
-        for (int e = 0; e < 8; e += 2) {
-          const int k0 = perm_logical(8 * q + e, H), k1 = perm_logical(8 * q + e + 1, H);
-          const uint32_t b0 = f2bf(bfr(bf2f(wv[j][e]) * bfr(bf2f(s.n.xr[b * H + k0]) * r)));
-          const uint32_t b1 = f2bf(bfr(bf2f(wv[j][e + 1]) * bfr(bf2f(s.n.xr[b * H + k1]) * r)));
-          o[e / 2] = b0 | (b1 << 16);
-        }
-        *(u32x4*)(s.n.xs + b * H + 8 * q) = u32x4{o[0], o[1], o[2], o[3]};
-      }
+    for (int e = 0; e < 4; ++e) {
+      const int k = 8 * c + 2 * e;
+      dst[perm_stored(k, H)] = f2bf(bfr(bf_lo(wv[e]) * bfr(bf_lo(xv[e]) * r)));
+      dst[perm_stored(k + 1, H)] = f2bf(bfr(bf_hi(wv[e]) * bfr(bf_hi(xv[e]) * r)));
+    }
   }
   __syncthreads();
 }
@@ -420,23 +415,52 @@ __device__ __forceinline__ void phase_router_b(const Params& p, int layer, S& s,
       p.nwg, p.trace, s.phase);
 }
 
-// Top-k of every sequence (route_topk_into: wave w routes sequences w, w + 8), then the routed (sequence, slot)
-// pairs sorted by (expert, sequence) and the distinct experts in ascending order.  Every workgroup computes the
+// Top-k of every sequence (wave w routes sequences w, w + 8, its logits loads issued together), then the routed
+// (sequence, slot) pairs sorted by (expert, sequence) and the distinct experts in ascending order.  The sort: every
+// pair sets bit expert * MAX_B + sequence of a bitmap (keys are distinct), one wave turns the words into prefix
+// popcounts, and a pair's rank is the prefix of its word plus the set bits below it.  Every workgroup computes the
 // same lists from the same logits.
 template <int B, int EC, class S>
 __device__ __forceinline__ void route_all(const Params& p, S& s) {
+  constexpr int PW = (B + NWAVE - 1) / NWAVE;             // sequences per wave
   const int nb = p.B, K = p.TOPK, np = nb * K, lane = lane_id(), wave = wave_u();
-  for (int b = wave; b < nb; b += NWAVE)
-    route_topk_into<EC>(p, p.logits + (size_t)b * p.E, &s.rids[b][0], &s.rwts[b][0], nullptr);
+  for (int t = threadIdx.x; t < KEY_WORDS; t += NT) s.kbits[t] = 0u;
+  RouteLogits<EC> lg[PW];
+#pragma unroll
+  for (int j = 0; j < PW; ++j)
+    if (wave + NWAVE * j < nb) route_load<EC>(p, p.logits + (size_t)(wave + NWAVE * j) * p.E, lg[j]);
+#pragma unroll
+  for (int j = 0; j < PW; ++j) {
+    const int b = wave + NWAVE * j;
+    if (b < nb) route_topk_from<EC>(p, lg[j], &s.rids[b][0], &s.rwts[b][0], nullptr);
+  }
   __syncthreads();
-  if ((int)threadIdx.x < np) {                             // rank of each pair among all pairs (keys are distinct)
+  int key = 0;
+  if ((int)threadIdx.x < np) {
     const int b = threadIdx.x / K, k = threadIdx.x - b * K;
-    const int key = s.rids[b][k] * MAX_B + b;
-    int rank = 0;
-    for (int t = 0; t < np; ++t) {
-      const int bt = t / K;
-      rank += (s.rids[bt][t - bt * K] * MAX_B + bt) < key;
+    key = s.rids[b][k] * MAX_B + b;
+    atomicOr(&s.kbits[key >> 5], 1u << (key & 31));
+  }
+  __syncthreads();
+  if (wave == 0) {                                         // exclusive prefix popcount of the words, lane by lane
+    uint32_t carry = 0;
+    for (int w0 = 0; w0 < KEY_WORDS; w0 += 64) {
+      const int wd = w0 + lane;
+      const uint32_t c = wd < KEY_WORDS ? (uint32_t)__builtin_popcount(s.kbits[wd]) : 0u;
+      uint32_t incl = c;
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const uint32_t o = (uint32_t)__shfl_up((int)incl, d, 64);
+        if (lane >= d) incl += o;
+      }
+      if (wd < KEY_WORDS) s.kpre[wd] = carry + incl - c;
+      carry += (uint32_t)__shfl((int)incl, 63, 64);
     }
+  }
+  __syncthreads();
+  if ((int)threadIdx.x < np) {
+    const int b = threadIdx.x / K, k = threadIdx.x - b * K;
+    const int rank = (int)s.kpre[key >> 5] + __builtin_popcount(s.kbits[key >> 5] & ((1u << (key & 31)) - 1u));
     s.pexp[rank] = s.rids[b][k];
     s.pseq[rank] = b;
     s.pw[rank] = s.rwts[b][k];

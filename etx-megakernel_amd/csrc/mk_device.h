@@ -102,14 +102,16 @@ struct Params {
 };
 
 // the attention phase's LDS (one (sequence, kv head, chunk) item at a time)
-struct AttnTiles {
-  u32x4 kt[HDIM / 8][CHUNK];            // K tile: [8-dim group][position in chunk], 16 bytes each
-  u32x4 vt[CHUNK / 8][2][CHUNK];        // V tile: [8-position group][dim half][dim in half], 16 bytes each
-  alignas(16) float q[MAX_G][HDIM];     // roped q heads of the kv group
+// CPI chunks of 64 positions per attention item (one tile pair each)
+template <int CPI>
+struct AttnTilesT {
+  static constexpr int cpi = CPI;
+  u32x4 kt[CPI][HDIM / 8][CHUNK];       // K tiles: [chunk][8-dim group][position in chunk], 16 bytes each
+  u32x4 vt[CPI][CHUNK / 8][2][CHUNK];   // V tiles: [chunk][8-position group][dim half][dim in half], 16 bytes each
   float knew[HDIM], vnew[HDIM];         // this step's k (roped) and v of the kv group
-  float p[MAX_G][2 * MAX_CHUNKS];       // exp(s - m_c) of the chunk per head; merge: chunk weights, then sums
-  float m[MAX_G];
+  float p[MAX_G][2 * MAX_CHUNKS];       // merge: chunk weights, then chunk sums, per head
 };
+using AttnTiles = AttnTilesT<1>;
 
 struct Smem {
   union {
@@ -729,12 +731,12 @@ __device__ __forceinline__ void qk_norm(float& a0, float& a1, float w0, float w1
   a1 = bfr(w1 * bfr(a1 * r));
 }
 
-// One attention work item: sequence b (always 0 in single-sequence kernels), kv head g, chunk c of the sequence's
-// positions 0..pos.  Items are numbered sequence by sequence (p.ibase), kv head fastest.
+// One attention work item: sequence b (always 0 in single-sequence kernels), kv head g, and CPI consecutive chunks
+// cp*CPI, ... of the sequence's positions 0..pos.  Items are numbered sequence by sequence (p.ibase), kv head fastest.
 struct AttnItem {
-  int b, g, c, pos;
+  int b, g, cp, pos;
 };
-template <int B>
+template <int B, int CPI>
 __device__ __forceinline__ AttnItem attn_item(const Params& p, int item) {
   int b = 0, r = item;
   if constexpr (B > 1) {
@@ -746,55 +748,63 @@ __device__ __forceinline__ AttnItem attn_item(const Params& p, int item) {
 
 template <int B, class S, class Wait>
 __device__ __forceinline__ void phase_attn(const Params& p, int layer, S& s, Wait wait) {
+  constexpr int CPI = decltype(s.a)::cpi;
   const int NKV = p.NKV, NH = p.NH, G = NH / NKV, HD = HDIM, BS = p.BS;
   const int NQKV = (NH + 2 * NKV) * HD;
-  const int nitems = B > 1 ? p.ibase[p.B] : NKV * ((p.pos + CHUNK) / CHUNK);
+  const int nitems = B > 1 ? p.ibase[p.B] : NKV * ((p.pos / CHUNK + CPI) / CPI);
   const LayerW Lw = layer_w(p, layer);
   const int lane = lane_id(), wave = wave_u();
-  // The chunk's cached K and V go straight from HBM into LDS tiles (global_load_lds, 16 bytes per lane); they do
+  // The chunks' cached K and V go straight from HBM into LDS tiles (global_load_lds, 16 bytes per lane); they do
   // not depend on this step, so the first item's copies are issued before the wait.  Wave w copies K dim-groups
-  // 2w, 2w+1 (lane = position) and the V position-group w (lane = dim, both halves).
+  // 2w, 2w+1 (lane = position) and the V position-group w (lane = dim, both halves) of every chunk of the item.
   auto load_kv = [&](int item) {
-    const AttnItem it = attn_item<B>(p, item);
-    const int g = it.g, c = it.c, pos = it.pos, n = pos + 1;
+    const AttnItem it = attn_item<B, CPI>(p, item);
+    const int g = it.g, pos = it.pos, n = pos + 1, nch = (n + CHUNK - 1) / CHUNK;
     const int32_t* btab = p.btab + (size_t)it.b * p.nbps;
-    const int t0 = c * CHUNK, len = min(CHUNK, n - t0);
-    const int t = t0 + lane;
-    if (lane < len && t != pos) {
-      const int blk = ld_i(btab + t / BS), off = t % BS;
-      const uint16_t* kp = Lw.kc + (((size_t)blk * NKV + g) * (HD / 8)) * BS * 8 + off * 8;
 #pragma unroll
-      for (int jj = 2 * wave; jj < 2 * wave + 2; ++jj)
-        __builtin_amdgcn_global_load_lds((const MK_G void*)(kp + (size_t)jj * BS * 8),
-                                         (__attribute__((address_space(3))) void*)&s.a.kt[jj][0], 16, 0, 0);
-    }
-    const int tb = t0 + wave * 8;                         // 8 positions per 16-byte load
-    if (tb < t0 + len) {
-      const int blk = ld_i(btab + tb / BS), off = tb % BS;
-      const uint16_t* vp = Lw.vc + ((size_t)blk * NKV + g) * HD * BS + off;
-      __builtin_amdgcn_global_load_lds((const MK_G void*)(vp + (size_t)lane * BS),
-                                       (__attribute__((address_space(3))) void*)&s.a.vt[wave][0][0], 16, 0, 0);
-      __builtin_amdgcn_global_load_lds((const MK_G void*)(vp + (size_t)(lane + 64) * BS),
-                                       (__attribute__((address_space(3))) void*)&s.a.vt[wave][1][0], 16, 0, 0);
+    for (int ci = 0; ci < CPI; ++ci) {
+      const int c = it.cp * CPI + ci;
+      if (c < nch) {
+        const int t0 = c * CHUNK, len = min(CHUNK, n - t0);
+        const int t = t0 + lane;
+        if (lane < len && t != pos) {
+          const int blk = ld_i(btab + t / BS), off = t % BS;
+          const uint16_t* kp = Lw.kc + (((size_t)blk * NKV + g) * (HD / 8)) * BS * 8 + off * 8;
+#pragma unroll
+          for (int jj = 2 * wave; jj < 2 * wave + 2; ++jj)
+            __builtin_amdgcn_global_load_lds((const MK_G void*)(kp + (size_t)jj * BS * 8),
+                                             (__attribute__((address_space(3))) void*)&s.a.kt[ci][jj][0], 16, 0, 0);
+        }
+        const int tb = t0 + wave * 8;                     // 8 positions per 16-byte load
+        if (tb < t0 + len) {
+          const int blk = ld_i(btab + tb / BS), off = tb % BS;
+          const uint16_t* vp = Lw.vc + ((size_t)blk * NKV + g) * HD * BS + off;
+          __builtin_amdgcn_global_load_lds((const MK_G void*)(vp + (size_t)lane * BS),
+                                           (__attribute__((address_space(3))) void*)&s.a.vt[ci][wave][0][0], 16, 0, 0);
+          __builtin_amdgcn_global_load_lds((const MK_G void*)(vp + (size_t)(lane + 64) * BS),
+                                           (__attribute__((address_space(3))) void*)&s.a.vt[ci][wave][1][0], 16, 0, 0);
+        }
+      }
     }
   };
   // RoPE factors of the position (ref_numpy.py:76-81 tables), reloaded when an item's sequence has another
-  int rpos = (int)blockIdx.x < nitems ? attn_item<B>(p, blockIdx.x).pos : 0;
+  int rpos = (int)blockIdx.x < nitems ? attn_item<B, CPI>(p, blockIdx.x).pos : 0;
   float rc = ld_f(p.rope_cos + (size_t)rpos * (HD / 2) + lane), rs = ld_f(p.rope_sin + (size_t)rpos * (HD / 2) + lane);
   const float qn0 = bf2f(ld_u16(Lw.qn + lane)), qn1 = bf2f(ld_u16(Lw.qn + lane + 64));
   const float kn0 = bf2f(ld_u16(Lw.kn + lane)), kn1 = bf2f(ld_u16(Lw.kn + lane + 64));
   if ((int)blockIdx.x < nitems) load_kv(blockIdx.x);
   if (!wait()) return;
   for (int item = blockIdx.x; item < nitems; item += p.nwg) {
-    const AttnItem it = attn_item<B>(p, item);
-    const int g = it.g, c = it.c, pos = it.pos, n = pos + 1, nch = (n + CHUNK - 1) / CHUNK;
+    const AttnItem it = attn_item<B, CPI>(p, item);
+    const int g = it.g, pos = it.pos, n = pos + 1, nch = (n + CHUNK - 1) / CHUNK;
+    const int c0 = it.cp * CPI, nc = min(CPI, nch - c0);   // chunks c0 .. c0 + nc - 1
     const int32_t* btab = p.btab + (size_t)it.b * p.nbps;
     const float* qkv = p.qkv + (size_t)it.b * NQKV;
     float* apart = p.apart + (size_t)it.b * NH * MAX_CHUNKS * PART;
     uint32_t* acnt = p.acnt + (size_t)it.b * NKV * 64;
     float* o = p.o + (size_t)it.b * NH * HD;
-    const int t0 = c * CHUNK, len = min(CHUNK, n - t0);
-    const bool has_new = pos < t0 + len;                 // this chunk holds the current position
+    const bool has_new = c0 + nc == nch;                   // this item holds the chunk with the current position
+    const int cn = nch - 1 - c0, tn = pos - (nch - 1) * CHUNK;   // its chunk slot and position in the chunk
     if (item != (int)blockIdx.x) load_kv(item);
     if constexpr (B > 1) {
       if (pos != rpos) {
@@ -803,12 +813,17 @@ __device__ __forceinline__ void phase_attn(const Params& p, int layer, S& s, Wai
         rs = ld_f(p.rope_sin + (size_t)pos * (HD / 2) + lane);
       }
     }
-    for (int j = wave; j < G; j += NWAVE) {               // roped q of head g*G + j (ref_numpy.py:116-120)
+    // wave j computes head g*G + j (G <= 8, checked by the host): its roped q stays in registers, dims lane (q0)
+    // and lane + 64 (q1) (ref_numpy.py:116-120); the score and P.V loops take each dim's or position's value from its
+    // lane with v_readlane (wave-uniform operands, no LDS traffic for q or p)
+    const int j = wave;
+    float q0 = 0.0f, q1 = 0.0f;
+    if (j < G) {
       const float* src = qkv + (size_t)(g * G + j) * HD;
       float a0 = ld_ag(src + lane), a1 = ld_ag(src + lane + 64);
       if (p.qk_norm) qk_norm(a0, a1, qn0, qn1, p.eps);
-      s.a.q[j][lane] = bfr(bfr(a0 * rc) + bfr(-a1 * rs));
-      s.a.q[j][lane + 64] = bfr(bfr(a1 * rc) + bfr(a0 * rs));
+      q0 = bfr(bfr(a0 * rc) + bfr(-a1 * rs));
+      q1 = bfr(bfr(a1 * rc) + bfr(a0 * rs));
     }
     if (has_new && wave == NWAVE - 1) {                   // this step's k (normed, roped) and v
       const float* ks = qkv + (size_t)(NH + g) * HD;
@@ -824,11 +839,11 @@ __device__ __forceinline__ void phase_attn(const Params& p, int layer, S& s, Wai
     __builtin_amdgcn_s_waitcnt(0);                        // this wave's tile copies have landed in LDS
     __syncthreads();
     if (has_new && threadIdx.x < HD / 2) {                // this step's k, v (bf16 values) into the tiles
-      const int tp = pos - t0, d0 = 2 * threadIdx.x;      // two dims per thread
+      const int d0 = 2 * threadIdx.x;                     // two dims per thread
       const uint32_t kw = (uint32_t)f2bf(s.a.knew[d0]) | ((uint32_t)f2bf(s.a.knew[d0 + 1]) << 16);
-      ((uint32_t*)&s.a.kt[d0 / 8][tp])[(d0 % 8) / 2] = kw;
-      uint16_t* v0 = (uint16_t*)&s.a.vt[tp / 8][d0 / 64][d0 % 64] + (tp % 8);
-      uint16_t* v1 = (uint16_t*)&s.a.vt[tp / 8][(d0 + 1) / 64][(d0 + 1) % 64] + (tp % 8);
+      ((uint32_t*)&s.a.kt[cn][d0 / 8][tn])[(d0 % 8) / 2] = kw;
+      uint16_t* v0 = (uint16_t*)&s.a.vt[cn][tn / 8][d0 / 64][d0 % 64] + (tn % 8);
+      uint16_t* v1 = (uint16_t*)&s.a.vt[cn][tn / 8][(d0 + 1) / 64][(d0 + 1) % 64] + (tn % 8);
       *v0 = f2bf(s.a.vnew[d0]);
       *v1 = f2bf(s.a.vnew[d0 + 1]);
     }
@@ -838,42 +853,19 @@ __device__ __forceinline__ void phase_attn(const Params& p, int layer, S& s, Wai
       st_u16(Lw.kc + ((((size_t)blk * NKV + g) * (HD / 8) + d / 8) * BS + off) * 8 + d % 8, f2bf(s.a.knew[d]));
       st_u16(Lw.vc + (((size_t)blk * NKV + g) * HD + d) * BS + off, f2bf(s.a.vnew[d]));
     }
-    // scores (:126): lane = position t0 + lane; s_t = (q . k_t in ascending d) * scale; chunk max; p = exp(s - m)
-    {
-      const int t = t0 + lane;
-      const bool valid = lane < len;
-      for (int j = wave; j < G; j += NWAVE) {
-        float acc = 0.0f;
-#pragma unroll
-        for (int jj = 0; jj < HD / 8; ++jj) {
-          const u32x4 kw = s.a.kt[jj][lane];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            acc = __builtin_fmaf(s.a.q[j][8 * jj + 2 * e], bf_lo(kw[e]), acc);
-            acc = __builtin_fmaf(s.a.q[j][8 * jj + 2 * e + 1], bf_hi(kw[e]), acc);
-          }
-        }
-        const float sc = valid ? acc * p.attn_scale : -__builtin_huge_valf();
-        const float m = wave_max(sc);
-        s.a.p[j][lane] = valid ? expf_mk(sc - m) : 0.0f;
-        if (lane == 0) s.a.m[j] = m;
-      }
-    }
-    __syncthreads();
-    // V (:127-128): lanes = dims (lane, lane + 64); a = sum_t p_t v_t[d] and l = sum_t p_t, ascending t
-    // one 16-byte read per dim half (8 positions of this lane's dim) and two for the 8 probabilities: conflict-free,
-    // where per-position dword reads of the 16-byte-strided tile conflict 4 ways.  Full chunks take the loop without
-    // position tests (per-position tests would be hoisted as 64 scalar masks); only a head's last chunk is partial.
-    auto pv = [&](int j, auto full, float& a0, float& a1, float& l) {
+    auto bcast = [](float v, int l) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l)); };
+    // per chunk: scores (:126): lane = position t0 + lane; s_t = (q . k_t in ascending d) * scale; the chunk max m;
+    // p_t = exp(s_t - m) in lane t.  Then V (:127-128): lanes = dims (lane, lane + 64); a = sum_t p_t v_t[d] and
+    // l = sum_t p_t, ascending t, from one 16-byte read per dim half (8 positions of this lane's dim).  Full chunks
+    // take the loop without position tests; only a head's last chunk is partial.
+    auto pv = [&](int ci, int len, float pr, auto full, float& a0, float& a1, float& l) {
 #pragma unroll
       for (int hb = 0; hb < CHUNK / 8; ++hb) {
-        const u32x4 w0 = s.a.vt[hb][0][lane], w1 = s.a.vt[hb][1][lane];
-        const float4 pa = *(const float4*)&s.a.p[j][hb * 8], pb = *(const float4*)&s.a.p[j][hb * 8 + 4];
-        const float pp[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
+        const u32x4 w0 = s.a.vt[ci][hb][0][lane], w1 = s.a.vt[ci][hb][1][lane];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           if (decltype(full)::value || hb * 8 + e < len) {
-            const float pt = pp[e];
+            const float pt = bcast(pr, hb * 8 + e);
             const float v0 = (e & 1) ? bf_hi(w0[e >> 1]) : bf_lo(w0[e >> 1]);
             const float v1 = (e & 1) ? bf_hi(w1[e >> 1]) : bf_lo(w1[e >> 1]);
             a0 = __builtin_fmaf(pt, v0, a0);
@@ -883,24 +875,45 @@ __device__ __forceinline__ void phase_attn(const Params& p, int layer, S& s, Wai
         }
       }
     };
-    for (int j = wave; j < G; j += NWAVE) {
-      float a0 = 0.0f, a1 = 0.0f, l = 0.0f;
-      if (len == CHUNK) pv(j, std::true_type{}, a0, a1, l);
-      else pv(j, std::false_type{}, a0, a1, l);
-      float* part = apart + ((size_t)(g * G + j) * MAX_CHUNKS + c) * PART;
-      st_ag(part + lane, a0);
-      st_ag(part + lane + 64, a1);
-      if (lane == 0) { st_ag(part + HD, s.a.m[j]); st_ag(part + HD + 1, l); }
+    if (j < G) {
+#pragma unroll
+      for (int ci = 0; ci < CPI; ++ci) {
+        if (ci < nc) {
+          const int c = c0 + ci, len = min(CHUNK, n - c * CHUNK);
+          const bool valid = lane < len;
+          float acc = 0.0f;
+#pragma unroll
+          for (int jj = 0; jj < HD / 8; ++jj) {
+            const u32x4 kw = s.a.kt[ci][jj][lane];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int d = 8 * jj + 2 * e;
+              acc = __builtin_fmaf(bcast(d < 64 ? q0 : q1, d & 63), bf_lo(kw[e]), acc);
+              acc = __builtin_fmaf(bcast(d + 1 < 64 ? q0 : q1, (d + 1) & 63), bf_hi(kw[e]), acc);
+            }
+          }
+          const float sc = valid ? acc * p.attn_scale : -__builtin_huge_valf();
+          const float m = wave_max(sc);
+          const float pr = valid ? expf_mk(sc - m) : 0.0f;
+          float a0 = 0.0f, a1 = 0.0f, l = 0.0f;
+          if (len == CHUNK) pv(ci, len, pr, std::true_type{}, a0, a1, l);
+          else pv(ci, len, pr, std::false_type{}, a0, a1, l);
+          float* part = apart + ((size_t)(g * G + j) * MAX_CHUNKS + c) * PART;
+          st_ag(part + lane, a0);
+          st_ag(part + lane + 64, a1);
+          if (lane == 0) { st_ag(part + HD, m); st_ag(part + HD + 1, l); }
+        }
+      }
     }
     if (p.trace && threadIdx.x == 0)                      // slot 2 of the attention phase: chunk partials issued
       *(MK_G uint64_t*)(p.trace + ((size_t)s.phase * p.nwg + blockIdx.x) * 3 + 2) = __builtin_amdgcn_s_memrealtime();
-    // the last chunk of kv head g to arrive merges: M = max m_c, w_c = exp(m_c - M), L = sum w_c l_c,
+    // the last item of kv head g to arrive merges: M = max m_c, w_c = exp(m_c - M), L = sum w_c l_c,
     // A[d] = sum w_c a_c[d] (ascending c), o = bfr(A / L)
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (threadIdx.x == 0) {
-      const uint32_t old = __hip_atomic_fetch_add(acnt + 64 * g, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      s.last = (old + 1u == (uint32_t)nch);
+      const uint32_t old = __hip_atomic_fetch_add(acnt + 64 * g, (uint32_t)nc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s.last = (old + (uint32_t)nc == (uint32_t)nch);
     }
     __syncthreads();
     if (s.last) {
@@ -910,10 +923,10 @@ __device__ __forceinline__ void phase_attn(const Params& p, int layer, S& s, Wai
         // first MB chunks' a[] are loaded together with (m, l) (they do not depend on the maximum): one round trip.
         constexpr int MB = 18;
         float av0[MB], av1[MB];
-        auto load_a = [&](int c0) {
+        auto load_a = [&](int cb) {
 #pragma unroll
           for (int u = 0; u < MB; ++u) {
-            const int c = min(c0 + u, nch - 1);             // past the last chunk: a repeat, never used
+            const int c = min(cb + u, nch - 1);             // past the last chunk: a repeat, never used
             av0[u] = ld_ag(part + (size_t)c * PART + lane);
             av1[u] = ld_ag(part + (size_t)c * PART + lane + 64);
           }
@@ -931,13 +944,13 @@ __device__ __forceinline__ void phase_attn(const Params& p, int layer, S& s, Wai
         s.a.p[j][MAX_CHUNKS + lane] = lloc;
         s.a.p[j][MAX_CHUNKS + 64 + lane] = lhi;
         float Ls = 0.0f, A0 = 0.0f, A1 = 0.0f;
-        for (int c0 = 0; c0 < nch; c0 += MB) {
-          if (c0 > 0) load_a(c0);
+        for (int cb = 0; cb < nch; cb += MB) {
+          if (cb > 0) load_a(cb);
 #pragma unroll
           for (int u = 0; u < MB; ++u)
-            if (c0 + u < nch) {
-              const float wc = s.a.p[j][c0 + u];
-              Ls = __builtin_fmaf(wc, s.a.p[j][MAX_CHUNKS + c0 + u], Ls);
+            if (cb + u < nch) {
+              const float wc = s.a.p[j][cb + u];
+              Ls = __builtin_fmaf(wc, s.a.p[j][MAX_CHUNKS + cb + u], Ls);
               A0 = __builtin_fmaf(wc, av0[u], A0);
               A1 = __builtin_fmaf(wc, av1[u], A1);
             }
@@ -1018,19 +1031,28 @@ __device__ __forceinline__ void phase_router(const Params& p, int layer, Smem& s
 // drops to -2, below every probability and below the -1 of absent experts.  The chosen probabilities are
 // renormalised in slot order and rounded to bf16; `order` lists the slots by ascending expert id (the index_add_
 // order of the combine).  Results land in the wave's private LDS row s.ids/wts/order[wave].
+template <int EC>
+struct RouteLogits {
+  static constexpr int NW = ((EC > 0 ? EC : MAX_E) + 63) / 64;
+  float v[NW];
+};
+// lane l's logits of experts l, l + 64, ... (agent-scope: written by the router phase); absent experts -inf
 template <int EC = 0>
-__device__ __forceinline__ void route_topk_into(const Params& p, const float* logits, int32_t* ids_out, float* wts_out,
+__device__ __forceinline__ void route_load(const Params& p, const float* logits, RouteLogits<EC>& r) {
+  const int E = EC > 0 ? EC : p.E, lane = lane_id();
+#pragma unroll
+  for (int w = 0; w < RouteLogits<EC>::NW; ++w) {
+    const int e = lane + 64 * w;
+    r.v[w] = e < E ? ld_ag(logits + e) : -__builtin_huge_valf();
+  }
+}
+template <int EC = 0>
+__device__ __forceinline__ void route_topk_from(const Params& p, RouteLogits<EC> r, int32_t* ids_out, float* wts_out,
                                                 int32_t* order_out) {
-  constexpr int EMAX = EC > 0 ? EC : MAX_E;
-  constexpr int NW = (EMAX + 63) / 64;
+  constexpr int NW = RouteLogits<EC>::NW;
   const int E = EC > 0 ? EC : p.E, K = p.TOPK;
   const int lane = lane_id();
-  float pv[NW];
-#pragma unroll
-  for (int w = 0; w < NW; ++w) {
-    const int e = lane + 64 * w;
-    pv[w] = e < E ? ld_ag(logits + e) : -__builtin_huge_valf();
-  }
+  float (&pv)[NW] = r.v;
   float m = pv[0];
 #pragma unroll
   for (int w = 1; w < NW; ++w) m = fmaxf(m, pv[w]);
@@ -1089,6 +1111,13 @@ __device__ __forceinline__ void route_topk_into(const Params& p, const float* lo
       if (order_out) order_out[before] = lane;
     }
   }
+}
+template <int EC = 0>
+__device__ __forceinline__ void route_topk_into(const Params& p, const float* logits, int32_t* ids_out, float* wts_out,
+                                                int32_t* order_out) {
+  RouteLogits<EC> r;
+  route_load<EC>(p, logits, r);
+  route_topk_from<EC>(p, r, ids_out, wts_out, order_out);
 }
 template <int EC = 0>
 __device__ __forceinline__ void route_topk(const Params& p, Smem& s) {

@@ -73,6 +73,8 @@ struct SmemD {
   int32_t uexp[MAX_PAIRS];
   int32_t ustart[MAX_PAIRS + 1];
   int32_t nexp;
+  uint32_t kbits[KEY_WORDS];
+  uint32_t kpre[KEY_WORDS];
   int32_t abort, last, phase;
 };
 
