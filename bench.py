@@ -242,13 +242,7 @@ def trace_summary(t, cfg):
     """Per-phase timeline of one traced step.  t[k][wg] = (wait for phase k's inputs returned, arrived after phase k,
     first weight loads issued (GEMV phases) / chunk partials issued (attention)), microseconds from the launch."""
     from etx.runtime import native as N
-    if cfg.arch == N.ARCH_DSV2:
-        att = ["qkv", "absorb", "attn", "wuv", "oproj"]
-        per_layer = [att + (["gateup", "down"] if l < cfg.first_dense else ["router_shared", "expert_up", "expert_down"])
-                     for l in range(cfg.L)]
-    else:
-        per_layer = [["qkv", "attn", "oproj", "router", "expert_up", "expert_down"] if cfg.moe
-                     else ["qkv", "attn", "oproj", "gateup", "down"]] * cfg.L
+    per_layer = N.phase_names(cfg)[:-1]
     flat = [n for names_l in per_layer for n in names_l]
     names = list(dict.fromkeys(flat))
     nb = len(flat)

@@ -320,15 +320,25 @@ __device__ __forceinline__ void dot_rows_any(const typename WR::Regs (&r)[NR], X
   else dot_rows_b<WR::K, NR, B>(r, xp, nv, lane, v);
 }
 
-// store NR x B values: lane i*B + b stores (i, b) for b < nv
-template <int NR, int B, class F>
-__device__ __forceinline__ void lane_store_b(const float (&v)[NR][B], int nv, F f) {
+// value (i, b) of v[NR][B] (wave-uniform) selected into lane i*B + b; other lanes get 0
+template <int NR, int B>
+__device__ __forceinline__ float lane_pick(const float (&v)[NR][B]) {
   const int lane = lane_id();
+  float r = 0.0f;
 #pragma unroll
   for (int i = 0; i < NR; ++i)
 #pragma unroll
     for (int b = 0; b < B; ++b)
-      if (lane == i * B + b && b < nv) f(i, b, v[i][b]);
+      if (i * B + b < 64) r = lane == i * B + b ? v[i][b] : r;
+  return r;
+}
+// store NR x B values: lane i*B + b stores (i, b) for b < nv, one divergent call
+template <int NR, int B, class F>
+__device__ __forceinline__ void lane_store_b(const float (&v)[NR][B], int nv, F f) {
+  static_assert(NR * B <= 64, "one lane per value");
+  const int lane = lane_id(), i = lane / B, b = lane - i * B;
+  const float val = lane_pick<NR, B>(v);
+  if (i < NR && b < nv) f(i, b, val);
 }
 
 // ---------------------------------------------------------------- phases (batched)
@@ -518,11 +528,9 @@ __device__ __forceinline__ void phase_expert_up_b(const Params& p, int layer, S&
       [&](int g, int b) { return (const uint16_t*)(s.n.xs + s.pseq[s.ustart[g / MI] + b] * KK); },
       [&](int g, int nv, const float(&v)[2][B]) {
         const int u = g / MI, j = g - u * MI, lane = lane_id();
-#pragma unroll
-        for (int b = 0; b < B; ++b)
-          if (lane == b && b < nv)
-            st_ag_u16(p.h16 + (size_t)(s.ustart[u] + b) * MI + perm_stored(j, MI),
-                      f2bf(bfr(bfr(silu(bfr(v[0][b]))) * bfr(v[1][b]))));
+        const float gv = lane_pick<1, B>((const float(&)[1][B])v[0]), uv = lane_pick<1, B>((const float(&)[1][B])v[1]);
+        if (lane < nv)
+          st_ag_u16(p.h16 + (size_t)(s.ustart[u] + lane) * MI + perm_stored(j, MI), f2bf(bfr(bfr(silu(bfr(gv))) * bfr(uv))));
       },
       [&]() { return true; }, p.nwg, p.trace, s.phase);
 }
@@ -617,10 +625,9 @@ __device__ __forceinline__ void phase_gateup_b(const Params& p, int layer, S& s,
       [&](int, int b) { return (const uint16_t*)(s.n.xs + b * KK); },
       [&](int g, int nv, const float(&v)[2][B]) {
         const int lane = lane_id();
-#pragma unroll
-        for (int b = 0; b < B; ++b)
-          if (lane == b && b < nv)
-            st_ag_u16(p.h16d + (size_t)b * IS + perm_stored(g, IS), f2bf(bfr(bfr(silu(bfr(v[0][b]))) * bfr(v[1][b]))));
+        const float gv = lane_pick<1, B>((const float(&)[1][B])v[0]), uv = lane_pick<1, B>((const float(&)[1][B])v[1]);
+        if (lane < nv)
+          st_ag_u16(p.h16d + (size_t)lane * IS + perm_stored(g, IS), f2bf(bfr(bfr(silu(bfr(gv))) * bfr(uv))));
       },
       [&]() {
         if (!wait()) return false;
@@ -663,24 +670,21 @@ __device__ __forceinline__ void phase_head_b(const Params& p, S& s, Wait wait) {
   using WR = Bf16Row<KK>;                                 // lm_head stays bf16 in every weight type
   const int V = p.V, nb = p.B;
   const uint8_t* W = (const uint8_t*)p.lm_head;
-  uint64_t best[B];
-#pragma unroll
-  for (int b = 0; b < B; ++b) best[b] = 0;
+  uint64_t best = 0;                                      // lane b: the best key of sequence b
   const bool ran = gemv_run_b<WR, 2, B>(
       (V + 1) / 2,
       [&](int g, int i) -> const uint8_t* { const int r = 2 * g + i; return r < V ? mrow<WR>(W, r) : nullptr; },
       [&](int) { return nb; }, [&](int, int b) { return (const uint16_t*)(s.n.xs + b * KK); },
       [&](int g, int nv, const float(&v)[2][B]) {
+        const int lane = lane_id();
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
           const int r = 2 * g + i;
-          if (r < V)
-#pragma unroll
-            for (int b = 0; b < B; ++b)
-              if (b < nv) {
-                const uint64_t key = argmax_key(bfr(v[i][b]), r);
-                best[b] = key > best[b] ? key : best[b];
-              }
+          const float val = lane_pick<1, B>((const float(&)[1][B])v[i]);
+          if (r < V && lane < nv) {
+            const uint64_t key = argmax_key(bfr(val), r);
+            best = key > best ? key : best;
+          }
         }
       },
       [&]() {
@@ -692,10 +696,8 @@ __device__ __forceinline__ void phase_head_b(const Params& p, S& s, Wait wait) {
         return true;
       },
       p.nwg, p.trace, s.phase);
-  if (ran && lane_id() == 0)
-#pragma unroll
-    for (int b = 0; b < B; ++b)
-      if (b < nb && best[b]) __hip_atomic_fetch_max(p.amax + 32 * b, best[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (ran && lane_id() < nb && best)
+    __hip_atomic_fetch_max(p.amax + 32 * lane_id(), best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <class Wait>

@@ -437,10 +437,8 @@ __device__ __forceinline__ void phase_router_shared_b(const Params& p, int layer
           lane_store_b<2, B>(v, nv, [&](int i, int b, float val) { st_ag(p.logits + (size_t)b * E + 2 * g + i, val); });
         } else {
           const int j = g - E2, lane = lane_id();
-#pragma unroll
-          for (int b = 0; b < B; ++b)
-            if (lane == b && b < nv)
-              st_ag_u16(p.h16s + (size_t)b * SI + perm_stored(j, SI), f2bf(bfr(bfr(silu(bfr(v[0][b]))) * bfr(v[1][b]))));
+          const float gv = lane_pick<1, B>((const float(&)[1][B])v[0]), uv = lane_pick<1, B>((const float(&)[1][B])v[1]);
+          if (lane < nv) st_ag_u16(p.h16s + (size_t)lane * SI + perm_stored(j, SI), f2bf(bfr(bfr(silu(bfr(gv))) * bfr(uv))));
         }
       },
       [&]() {
