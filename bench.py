@@ -288,6 +288,8 @@ def main():
                     help="profiling runs: first copy 1 GiB device to device, the known-size reference for HBM counters")
     ap.add_argument("--kv-fill", action="store_true",
                     help="profiling runs: fill the KV cache with seeded N(0,1) instead of prefilling the prompt")
+    ap.add_argument("--prefill-rows", type=int, default=16,
+                    help="prompt positions per prefill launch (batched kernel); 0 or 1: one decode step per position")
     ap.add_argument("--batch", type=int, default=1, help="sequences per step (> 1: the batched step, not the headline)")
     ap.add_argument("--ctx-lo", type=int, default=512)
     ap.add_argument("--ctx-hi", type=int, default=4096)
@@ -310,6 +312,9 @@ def main():
     cfg = configs.QWEN3_30B_A3B
     if a.fp8:
         cfg = configs.with_layers(cfg, cfg.L, wdtype=N.W_FP8)
+    rows = a.prefill_rows if a.prefill_rows > 1 and not a.unfused else 0
+    if rows:
+        cfg = configs.with_layers(cfg, cfg.L, prefill=rows)
     if a.ctx + a.warmup + a.steps + 1 > cfg.max_ctx:
         raise SystemExit(f"ctx {a.ctx} + warmup + steps exceeds max_ctx {cfg.max_ctx}")
     dev = torch.device("cuda:0")
@@ -328,6 +333,7 @@ def main():
         f"{dec.barriers_per_step()} grid barriers per step")
     prompt = np.random.default_rng(a.seed).integers(0, cfg.V, a.ctx).astype(np.int32)
     t1 = time.time()
+    prefill = None
     if a.kv_fill:
         dec.fill_kv_seeded(a.seed, a.ctx)
         toks = np.zeros(a.ctx + 1, np.int32)
@@ -336,11 +342,32 @@ def main():
         log(f"[gpu] KV cache filled with {a.ctx} seeded positions")
     else:
         dec.set_tokens(prompt)
-        for pos in range(a.ctx):
-            dec.step(pos, write_next=pos + 1 >= a.ctx)
-            if pos % 256 == 255:
-                dec.sync()
-                log(f"[gpu] prefill {pos + 1}/{a.ctx} ({(time.time() - t1) / (pos + 1) * 1e3:.3f} ms/token)")
+        dec.sync()
+        stream = torch.cuda.current_stream(dev)
+        p0, p1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        p0.record(stream)
+        if rows:
+            for q in range(0, a.ctx, rows):
+                n = min(rows, a.ctx - q)
+                dec.prefill(q, n, write_next=q + n == a.ctx)
+                if q // rows % 16 == 15:
+                    dec.sync()
+                    log(f"[gpu] prefill {q + n}/{a.ctx} ({(time.time() - t1) / (q + n) * 1e3:.3f} ms/token)")
+        else:
+            for pos in range(a.ctx):
+                dec.step(pos, write_next=pos + 1 >= a.ctx)
+                if pos % 256 == 255:
+                    dec.sync()
+                    log(f"[gpu] prefill {pos + 1}/{a.ctx} ({(time.time() - t1) / (pos + 1) * 1e3:.3f} ms/token)")
+        p1.record(stream)
+        dec.sync()
+        pms = p0.elapsed_time(p1)
+        prefill = {"tokens": a.ctx, "positions_per_launch": rows or 1, "launches": -(-a.ctx // (rows or 1)),
+                   "ms": round(pms, 2), "ms_per_token": round(pms / a.ctx, 4),
+                   "tokens_per_s": round(a.ctx / (pms * 1e-3), 1),
+                   "kernel": "batched persistent kernel, one row per position" if rows else "decode step per token"}
+        log(f"[gpu] prefill of {a.ctx} positions: {pms:.1f} ms ({pms / a.ctx:.4f} ms/token, "
+            f"{rows or 1} per launch)")
     dec.sync()
     pos = a.ctx
     for _ in range(a.warmup):
@@ -383,7 +410,8 @@ def main():
         "dtype": "fp8-e4m3 weights x bf16 activations, fp32 accumulation" if a.fp8 else "bf16",
         "data": "synthetic: seeded random-init " + ("fp8 (quantised from bf16 N(0,0.02))" if a.fp8 else "bf16")
                 + " weights N(0,0.02); " + ("KV cache of seeded N(0,1) values"
-                if a.kv_fill else "prompt of seeded uniform token ids prefilled token by token"),
+                if a.kv_fill else "prompt of seeded uniform token ids, prefilled " +
+                (f"{rows} positions per launch (bit-identical to token by token)" if rows else "token by token")),
         "config": {"workload": f"{cfg.name} decode, batch 1, context {a.ctx} (+{a.warmup} warmup), greedy "
                                f"(BASELINE.json configs[2])",
                    "batch": 1, "context": a.ctx, "layers": cfg.L, "experts": cfg.E, "top_k": cfg.TOPK,
@@ -399,6 +427,8 @@ def main():
     }
     if phase_us:
         out["phase_us"] = phase_us
+    if prefill:
+        out["prefill"] = prefill
     # HBM bytes per launch from the committed counter passes (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of this
     # workload, each scaled by the same counter's reading for a 1 GiB copy)
     tf = ROOT / "profiles" / "etxmk_fused_qwen3-30b-a3b_b1_ctx1024_hbm_traffic.json"

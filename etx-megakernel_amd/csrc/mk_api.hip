@@ -124,14 +124,15 @@ const void* fused_kernel(const etxmk_config& c) {
 }
 
 // the batched persistent kernel for this shape and weight type with the smallest batch capacity that holds
-// c.batch, or nullptr
-const void* batch_kernel(const etxmk_config& c) {
+// `rows` rows (default c.batch), or nullptr
+const void* batch_kernel(const etxmk_config& c, int rows = 0) {
+  if (rows <= 0) rows = c.batch;
   const int km = c.moe ? c.MI : c.I;
   const void* best = nullptr;
   int cap = 0;
 #define MK_PICK_B(name, h_, ka_, km_, moe_, e_, fp8_, b_)                                                         \
   if (c.H == h_ && c.NH * c.HD == ka_ && km == km_ && (c.moe != 0) == moe_ && (!moe_ || c.E == e_) &&            \
-      (c.wdtype == ETXMK_W_FP8) == fp8_ && c.batch <= b_ && (!best || b_ < cap)) {                                \
+      (c.wdtype == ETXMK_W_FP8) == fp8_ && rows <= b_ && (!best || b_ < cap)) {                                   \
     best = (const void*)name;                                                                                     \
     cap = b_;                                                                                                     \
   }
@@ -221,7 +222,11 @@ int check_config(const etxmk_config* c) {
   if (!c) return fail(ETXMK_EINVAL, "config is NULL");
   if (c->H <= 0 || c->NH <= 0 || c->NKV <= 0 || c->L <= 0 || c->V <= 0) return fail(ETXMK_EINVAL, "non-positive dimension");
   if (c->arch != ETXMK_ARCH_QWEN3 && c->arch != ETXMK_ARCH_DSV2) return fail(ETXMK_EINVAL, "architecture %d unknown", c->arch);
-  if (c->arch == ETXMK_ARCH_DSV2) return check_ds(c);
+  if (c->prefill < 0 || c->prefill > MAX_B) return fail(ETXMK_EINVAL, "prefill rows %d outside 0..%d", c->prefill, MAX_B);
+  if (c->arch == ETXMK_ARCH_DSV2) {
+    if (c->prefill > 0) return fail(ETXMK_EINVAL, "prefill launches serve Qwen3 handles");
+    return check_ds(c);
+  }
   if (c->HD != HDIM) return fail(ETXMK_EINVAL, "head_dim %d unsupported (the attention phase is built for %d)", c->HD, HDIM);
   if (c->NH % c->NKV) return fail(ETXMK_EINVAL, "NH %d not a multiple of NKV %d", c->NH, c->NKV);
   if (c->NH / c->NKV > NWAVE) return fail(ETXMK_EINVAL, "%d q heads per kv head (at most %d)", c->NH / c->NKV, NWAVE);
@@ -244,6 +249,9 @@ int check_config(const etxmk_config* c) {
   if (c->batch > 1 && !batch_kernel(*c))
     return fail(ETXMK_EINVAL, "no batched persistent kernel for batch %d, H %d, NH*HD %d, %s %d", c->batch, c->H,
                 c->NH * c->HD, c->moe ? "MI" : "I", c->moe ? c->MI : c->I);
+  if (c->prefill > 0 && !batch_kernel(*c, c->prefill))
+    return fail(ETXMK_EINVAL, "no batched persistent kernel for %d prefill rows, H %d, NH*HD %d, %s %d", c->prefill,
+                c->H, c->NH * c->HD, c->moe ? "MI" : "I", c->moe ? c->MI : c->I);
   return ETXMK_OK;
 }
 
@@ -313,6 +321,7 @@ std::vector<TensorSlot> weight_layout(const etxmk_config* c, uint64_t* total) {
 // paged KV: every sequence of the batch owns up to nbps blocks of one shared pool
 int nbps_of(const etxmk_config* c) { return (c->max_ctx + c->block_size - 1) / c->block_size; }
 int nblocks_of(const etxmk_config* c) { return c->batch * nbps_of(c); }
+int rows_of(const etxmk_config& c) { return c.batch > c.prefill ? c.batch : c.prefill; }
 
 // per layer: K and V pools of this many elements each (DeepSeek-V2: one latent pool)
 uint64_t kv_layer_elems(const etxmk_config* c) {
@@ -332,7 +341,7 @@ WsLayout ws_layout(const etxmk_config* c) {
   auto take = [&](uint64_t bytes) { const uint64_t o = off; off = align_up(off + bytes); return o; };
   const bool ds = c->arch == ETXMK_ARCH_DSV2;
   const int NQKV = nqkv_of(*c), KA = ds ? c->NH * c->v_head : c->NH * c->HD;
-  const uint64_t B = (uint64_t)c->batch;
+  const uint64_t B = (uint64_t)rows_of(*c);   // activation rows: sequences, or prefill positions
   w.x = take(4ull * c->H * B);
   w.x16 = take(2ull * c->H * B);
   w.qkv = take(4ull * NQKV * B);
@@ -347,8 +356,8 @@ WsLayout ws_layout(const etxmk_config* c) {
   w.amax = take(256ull * B);             // one 256-byte line per sequence
   w.bar = take(4 * 64 * 17);          // 8 group counters, 1 global counter, 8 release flags; 256 B apart
   w.abort_w = take(4);
-  w.tokens = take(4ull * (c->max_ctx + 1) * B);
-  w.out_tokens = take(4ull * (c->max_ctx + 1) * B);
+  w.tokens = take(4ull * (c->max_ctx + 1) * c->batch);
+  w.out_tokens = take(4ull * (c->max_ctx + 1) * c->batch);
   w.btab = take(4ull * nblocks_of(c));
   const int rhalf = ds ? c->qk_rope / 2 : c->HD / 2;
   w.rcos = take(4ull * c->max_ctx * rhalf);
@@ -365,7 +374,7 @@ WsLayout ws_layout(const etxmk_config* c) {
   return w;
 }
 
-uint64_t acnt_bytes(const etxmk_config& c) { return 4ull * 64 * (is_ds(c) ? ds_nhg(c) : c.NKV) * c.batch; }
+uint64_t acnt_bytes(const etxmk_config& c) { return 4ull * 64 * (is_ds(c) ? ds_nhg(c) : c.NKV) * rows_of(c); }
 
 // DeepseekV2YarnRotaryEmbedding tables (reference_decode.py:85-118) in the steps the reference's numpy takes in
 // float32: the correction range in double, the ramp, mask and inverse frequencies in float, then cos and sin of
@@ -563,8 +572,8 @@ int etxmk_bind(etxmk_handle* h, void* weights, void* kv, void* workspace) {
   HIPCHK(hipMemset(h->wsp + h->ws.abort_w, 0, 4));
   HIPCHK(hipMemset(h->wsp + h->ws.tokens, 0, 4ull * (c.max_ctx + 1) * c.batch));
   HIPCHK(hipMemset(h->wsp + h->ws.out_tokens, 0, 4ull * (c.max_ctx + 1) * c.batch));
-  HIPCHK(hipMemset(h->wsp + h->ws.x, 0, 4ull * c.H * c.batch));
-  HIPCHK(hipMemset(h->wsp + h->ws.x16, 0, 2ull * c.H * c.batch));
+  HIPCHK(hipMemset(h->wsp + h->ws.x, 0, 4ull * c.H * rows_of(c)));
+  HIPCHK(hipMemset(h->wsp + h->ws.x16, 0, 2ull * c.H * rows_of(c)));
   HIPCHK(hipMemset(h->wsp + h->ws.acnt, 0, acnt_bytes(c)));
   if (ds) HIPCHK(hipMemset(h->wsp + h->ws.h16d, 0, 2ull * (c.first_dense > 0 ? ds_ip(c) : 8) * c.batch));  // zero pads
   h->bar_epoch = 0;
@@ -807,19 +816,23 @@ int etxmk_barriers_per_step(etxmk_handle* h, int32_t* n) {
   return ETXMK_OK;
 }
 
+// pseq >= 0: prefill of sequence pseq, rows b = positions posv[0] + b (nrows of them)
 static int launch(etxmk_handle* h, const int32_t* posv, int pos, int write_next, int l0, int l1, int embed, int head,
-                  hipStream_t st) {
+                  hipStream_t st, int pseq = -1, int nrows = 0) {
   if (!h || !h->wsp) return fail(ETXMK_EUNBOUND, "handle not bound");
   const etxmk_config& c = h->c;
-  const bool ds = is_ds(c);
-  const bool batched = c.batch > 1 || ds;  // DeepSeek-V2 runs its batched kernel, a single sequence as a batch of one
+  const bool ds = is_ds(c), pf = pseq >= 0;
+  // DeepSeek-V2 runs its batched kernel, a single sequence as a batch of one; prefill runs the batched kernel
+  const bool batched = c.batch > 1 || ds || pf;
+  if (!pf) nrows = batched ? c.batch : 1;
   if (c.batch > 1 && !posv) return fail(ETXMK_EINVAL, "a batched handle steps through etxmk_step_batch");
-  if (c.batch == 1 && posv) pos = posv[0];
+  if (c.batch == 1 && posv && !pf) pos = posv[0];
   int32_t pos1 = pos;
   if (batched && !posv) posv = &pos1;
-  for (int b = 0; b < (batched ? c.batch : 1); ++b) {
+  for (int b = 0; b < nrows; ++b) {
     const int q = batched ? posv[b] : pos;
-    if (q < 0 || q >= c.max_ctx) return fail(ETXMK_EINVAL, "sequence %d position %d outside 0..%d", b, q, c.max_ctx - 1);
+    if (q < 0 || q >= c.max_ctx) return fail(ETXMK_EINVAL, "sequence %d position %d outside 0..%d", pf ? pseq : b, q,
+                                             c.max_ctx - 1);
   }
   if (l0 < 0 || l1 > c.L || l0 >= l1) return fail(ETXMK_EINVAL, "layer range [%d, %d) outside [0, %d)", l0, l1, c.L);
   const int need = 8;                       // the grid barrier spreads arrivals over 8 groups
@@ -861,7 +874,9 @@ static int launch(etxmk_handle* h, const int32_t* posv, int pos, int write_next,
   p.abort_word = h->wsptr<int32_t>(h->ws.abort_w);
   p.tokens = h->wsptr<int32_t>(h->ws.tokens);
   p.out_tokens = h->wsptr<int32_t>(h->ws.out_tokens);
-  p.dump_x = h->dump_x; p.dump_ids = h->dump_ids; p.dump_wts = h->dump_wts; p.dump_logits = h->dump_logits;
+  if (!pf) {                               // the dump buffers hold `batch` rows; prefill rows are not dumped
+    p.dump_x = h->dump_x; p.dump_ids = h->dump_ids; p.dump_wts = h->dump_wts; p.dump_logits = h->dump_logits;
+  }
   p.trace = h->fused ? h->trace : nullptr;
   p.pos = batched ? 0 : pos; p.write_next = write_next; p.l0 = l0; p.l1 = l1; p.do_embed = embed; p.do_head = head;
   p.nwg = h->nwg;
@@ -871,9 +886,17 @@ static int launch(etxmk_handle* h, const int32_t* posv, int pos, int write_next,
     p.qkv_rows = (!batched && h->fused && c.wdtype == ETXMK_W_BF16 && c.H % 512 == 0 &&
                   (uint64_t)R * c.H * 2 <= (uint64_t)QKVW_BYTES) ? R : 0;
   }
-  p.B = c.batch;
+  p.B = nrows;
   p.nbps = nbps_of(&c);
   p.tok_stride = c.max_ctx + 1;
+  if (pf) {                                // every row reads the one sequence's block table and token rows
+    p.pf = 1;
+    p.btab += (size_t)pseq * p.nbps;
+    p.tokens += (size_t)pseq * p.tok_stride;
+    p.out_tokens += (size_t)pseq * p.tok_stride;
+    p.nbps = 0;
+    p.tok_stride = 0;
+  }
   p.x16 = h->wsptr<uint16_t>(h->ws.x16);
   p.o16 = h->wsptr<uint16_t>(h->ws.o16);
   p.h16 = h->wsptr<uint16_t>(h->ws.h16);
@@ -892,13 +915,13 @@ static int launch(etxmk_handle* h, const int32_t* posv, int pos, int write_next,
   // attention items of each sequence: DeepSeek-V2 one per (group of 8 heads, 64-position chunk); Qwen3 one per
   // (kv head, ATTN_CPI_B chunks) in batched kernels (the single-sequence kernel counts its own, one chunk each)
   p.ibase[0] = 0;
-  for (int b = 0; b < c.batch; ++b) {
+  for (int b = 0; b < nrows; ++b) {
     p.posb[b] = batched ? posv[b] : pos;
     const int nch = p.posb[b] / CHUNK + 1;
     p.ibase[b + 1] = p.ibase[b] + (ds ? ds_nhg(c) * nch : c.NKV * ((nch + ATTN_CPI_B - 1) / ATTN_CPI_B));
   }
   if (h->fused) {
-    const void* fn = ds ? ds_kernel(c) : batched ? batch_kernel(c) : fused_kernel(c);
+    const void* fn = ds ? ds_kernel(c) : batched ? batch_kernel(c, nrows) : fused_kernel(c);
     if (!fn) return fail(ETXMK_EINVAL, "no persistent kernel for H %d, NH*HD %d, %s %d (use the unfused mode)", c.H,
                          c.NH * c.HD, c.moe ? "MI" : "I", c.moe ? c.MI : c.I);
     p.bar_base = h->bar_epoch;
@@ -945,6 +968,23 @@ int etxmk_step_batch(etxmk_handle* h, const int32_t* positions, int32_t write_ne
   if (!h) return fail(ETXMK_EINVAL, "NULL handle");
   if (!positions) return fail(ETXMK_EINVAL, "positions is NULL");
   return launch(h, positions, 0, write_next_mask, 0, h->c.L, 1, 1, (hipStream_t)stream);
+}
+
+int etxmk_prefill(etxmk_handle* h, int32_t seq, int32_t pos0, int32_t n, int32_t write_next, void* stream) {
+  if (!h) return fail(ETXMK_EINVAL, "NULL handle");
+  const etxmk_config& c = h->c;
+  if (is_ds(c)) return fail(ETXMK_EINVAL, "prefill launches serve Qwen3 handles");
+  if (!h->fused) return fail(ETXMK_EINVAL, "prefill runs the persistent kernel only");
+  if (seq < 0 || seq >= c.batch) return fail(ETXMK_EINVAL, "sequence %d outside 0..%d", seq, c.batch - 1);
+  if (n < 1 || n > rows_of(c)) return fail(ETXMK_EINVAL, "%d prefill positions outside 1..%d", n, rows_of(c));
+  if (pos0 < 0 || pos0 + n > c.max_ctx)
+    return fail(ETXMK_EINVAL, "positions %d..%d outside 0..%d", pos0, pos0 + n - 1, c.max_ctx - 1);
+  if (!batch_kernel(c, n))
+    return fail(ETXMK_EINVAL, "no batched persistent kernel for %d rows, H %d, NH*HD %d, %s %d", n, c.H, c.NH * c.HD,
+                c.moe ? "MI" : "I", c.moe ? c.MI : c.I);
+  int32_t posv[MAX_B];
+  for (int b = 0; b < n; ++b) posv[b] = pos0 + b;
+  return launch(h, posv, 0, write_next ? 1 << (n - 1) : 0, 0, c.L, 1, 1, (hipStream_t)stream, seq, n);
 }
 
 int etxmk_step_layers(etxmk_handle* h, int32_t pos, int32_t l0, int32_t l1, void* stream) {

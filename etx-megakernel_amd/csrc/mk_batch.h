@@ -771,7 +771,8 @@ __device__ __forceinline__ void fused_body_b(const Params& p) {
   X(etxmk_fused_b16_h2048_a4096_moe768_e128, 2048, 4096, 768, true, 128, false, 16) \
   X(etxmk_fused_b4_h512_a512_moe256_e16, 512, 512, 256, true, 16, false, 4)         \
   X(etxmk_fused_b16_h512_a512_moe256_e16, 512, 512, 256, true, 16, false, 16)       \
-  X(etxmk_fused_b4_h512_a512_mlp1024, 512, 512, 1024, false, 0, false, 4)
+  X(etxmk_fused_b4_h512_a512_mlp1024, 512, 512, 1024, false, 0, false, 4)           \
+  X(etxmk_fused_b4_h4096_a4096_mlp12288, 4096, 4096, 12288, false, 0, false, 4)
 #define MK_BATCH_SHAPES_FP8(X)                                                          \
   X(etxmk_fused_fp8_b4_h2048_a4096_moe768_e128, 2048, 4096, 768, true, 128, true, 4)   \
   X(etxmk_fused_fp8_b16_h2048_a4096_moe768_e128, 2048, 4096, 768, true, 128, true, 16) \

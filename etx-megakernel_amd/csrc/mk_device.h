@@ -86,6 +86,8 @@ struct Params {
   // batched steps: per-sequence activations are [B][...] rows of the buffers above; tokens / out_tokens rows are
   // tok_stride long; btab rows nbps long; amax entries 256 bytes apart
   int B, nbps, tok_stride;
+  int pf;                               // prefill: rows b are positions posb[0] + b of one sequence (btab and
+                                        // tokens point at its rows, nbps = tok_stride = 0)
   uint16_t* x16;                        // [B][H] residual, bf16
   uint16_t* o16;                        // [B][NH*HD] attention output, bf16 lane-permuted
   uint16_t* h16;                        // MoE [pairs][MI] / dense [B][I] MLP activations, bf16 lane-permuted
@@ -108,7 +110,6 @@ struct AttnTilesT {
   static constexpr int cpi = CPI;
   u32x4 kt[CPI][HDIM / 8][CHUNK];       // K tiles: [chunk][8-dim group][position in chunk], 16 bytes each
   u32x4 vt[CPI][CHUNK / 8][2][CHUNK];   // V tiles: [chunk][8-position group][dim half][dim in half], 16 bytes each
-  float knew[HDIM], vnew[HDIM];         // this step's k (roped) and v of the kv group
   float p[MAX_G][2 * MAX_CHUNKS];       // merge: chunk weights, then chunk sums, per head
 };
 using AttnTiles = AttnTilesT<1>;
@@ -757,9 +758,12 @@ __device__ __forceinline__ void phase_attn(const Params& p, int layer, S& s, Wai
   // The chunks' cached K and V go straight from HBM into LDS tiles (global_load_lds, 16 bytes per lane); they do
   // not depend on this step, so the first item's copies are issued before the wait.  Wave w copies K dim-groups
   // 2w, 2w+1 (lane = position) and the V position-group w (lane = dim, both halves) of every chunk of the item.
+  // Positions from first_new(pos) on are this launch's (the row's own, and in prefill the earlier rows'): they are
+  // not read from the cache but patched into the tiles from the QKV rows.
+  auto first_new = [&](int pos) { return B > 1 && p.pf ? p.posb[0] : pos; };
   auto load_kv = [&](int item) {
     const AttnItem it = attn_item<B, CPI>(p, item);
-    const int g = it.g, pos = it.pos, n = pos + 1, nch = (n + CHUNK - 1) / CHUNK;
+    const int g = it.g, pos = it.pos, n = pos + 1, nch = (n + CHUNK - 1) / CHUNK, fp = first_new(pos);
     const int32_t* btab = p.btab + (size_t)it.b * p.nbps;
 #pragma unroll
     for (int ci = 0; ci < CPI; ++ci) {
@@ -767,7 +771,7 @@ __device__ __forceinline__ void phase_attn(const Params& p, int layer, S& s, Wai
       if (c < nch) {
         const int t0 = c * CHUNK, len = min(CHUNK, n - t0);
         const int t = t0 + lane;
-        if (lane < len && t != pos) {
+        if (lane < len && t < fp) {
           const int blk = ld_i(btab + t / BS), off = t % BS;
           const uint16_t* kp = Lw.kc + (((size_t)blk * NKV + g) * (HD / 8)) * BS * 8 + off * 8;
 #pragma unroll
@@ -776,7 +780,7 @@ __device__ __forceinline__ void phase_attn(const Params& p, int layer, S& s, Wai
                                              (__attribute__((address_space(3))) void*)&s.a.kt[ci][jj][0], 16, 0, 0);
         }
         const int tb = t0 + wave * 8;                     // 8 positions per 16-byte load
-        if (tb < t0 + len) {
+        if (tb < t0 + len && tb < fp) {
           const int blk = ld_i(btab + tb / BS), off = tb % BS;
           const uint16_t* vp = Lw.vc + ((size_t)blk * NKV + g) * HD * BS + off;
           __builtin_amdgcn_global_load_lds((const MK_G void*)(vp + (size_t)lane * BS),
@@ -803,8 +807,8 @@ __device__ __forceinline__ void phase_attn(const Params& p, int layer, S& s, Wai
     float* apart = p.apart + (size_t)it.b * NH * MAX_CHUNKS * PART;
     uint32_t* acnt = p.acnt + (size_t)it.b * NKV * 64;
     float* o = p.o + (size_t)it.b * NH * HD;
-    const bool has_new = c0 + nc == nch;                   // this item holds the chunk with the current position
-    const int cn = nch - 1 - c0, tn = pos - (nch - 1) * CHUNK;   // its chunk slot and position in the chunk
+    // this launch's positions in the item's chunks: [qlo, qhi] (decode: pos alone, in the item of the last chunk)
+    const int qlo = max(first_new(pos), c0 * CHUNK), qhi = min(pos, (c0 + nc) * CHUNK - 1);
     if (item != (int)blockIdx.x) load_kv(item);
     if constexpr (B > 1) {
       if (pos != rpos) {
@@ -825,34 +829,55 @@ __device__ __forceinline__ void phase_attn(const Params& p, int layer, S& s, Wai
       q0 = bfr(bfr(a0 * rc) + bfr(-a1 * rs));
       q1 = bfr(bfr(a1 * rc) + bfr(a0 * rs));
     }
-    if (has_new && wave == NWAVE - 1) {                   // this step's k (normed, roped) and v
-      const float* ks = qkv + (size_t)(NH + g) * HD;
-      const float* vs = qkv + (size_t)(NH + NKV + g) * HD;
-      float a0 = ld_ag(ks + lane), a1 = ld_ag(ks + lane + 64);
-      const float v0 = ld_ag(vs + lane), v1 = ld_ag(vs + lane + 64);
-      if (p.qk_norm) qk_norm(a0, a1, kn0, kn1, p.eps);
-      s.a.knew[lane] = bfr(bfr(a0 * rc) + bfr(-a1 * rs));
-      s.a.knew[lane + 64] = bfr(bfr(a1 * rc) + bfr(a0 * rs));
-      s.a.vnew[lane] = v0;
-      s.a.vnew[lane + 64] = v1;
+    // k (normed, roped at its position) and v of position q come from the QKV row of that position, row
+    // it.b - (pos - q); wave NWAVE-1-w takes positions qlo + w and qlo + w + NWAVE (a launch has <= 2*NWAVE rows)
+    constexpr int PQ = B > 1 ? 2 : 1;
+    float kn[PQ][2], vn[PQ][2];
+#pragma unroll
+    for (int u = 0; u < PQ; ++u) {
+      const int q = qlo + (NWAVE - 1 - wave) + u * NWAVE;
+      if (q <= qhi) {
+        const float* row = p.qkv + (size_t)(it.b - (pos - q)) * NQKV;
+        const float* ks = row + (size_t)(NH + g) * HD;
+        const float* vs = row + (size_t)(NH + NKV + g) * HD;
+        float a0 = ld_ag(ks + lane), a1 = ld_ag(ks + lane + 64);
+        vn[u][0] = ld_ag(vs + lane);
+        vn[u][1] = ld_ag(vs + lane + 64);
+        float cq = rc, sq = rs;                           // RoPE factors of position q
+        if (q != pos) {
+          cq = ld_f(p.rope_cos + (size_t)q * (HD / 2) + lane);
+          sq = ld_f(p.rope_sin + (size_t)q * (HD / 2) + lane);
+        }
+        if (p.qk_norm) qk_norm(a0, a1, kn0, kn1, p.eps);
+        kn[u][0] = bfr(bfr(a0 * cq) + bfr(-a1 * sq));
+        kn[u][1] = bfr(bfr(a1 * cq) + bfr(a0 * sq));
+      }
     }
     __builtin_amdgcn_s_waitcnt(0);                        // this wave's tile copies have landed in LDS
     __syncthreads();
-    if (has_new && threadIdx.x < HD / 2) {                // this step's k, v (bf16 values) into the tiles
-      const int d0 = 2 * threadIdx.x;                     // two dims per thread
-      const uint32_t kw = (uint32_t)f2bf(s.a.knew[d0]) | ((uint32_t)f2bf(s.a.knew[d0 + 1]) << 16);
-      ((uint32_t*)&s.a.kt[cn][d0 / 8][tn])[(d0 % 8) / 2] = kw;
-      uint16_t* v0 = (uint16_t*)&s.a.vt[cn][tn / 8][d0 / 64][d0 % 64] + (tn % 8);
-      uint16_t* v1 = (uint16_t*)&s.a.vt[cn][tn / 8][(d0 + 1) / 64][(d0 + 1) % 64] + (tn % 8);
-      *v0 = f2bf(s.a.vnew[d0]);
-      *v1 = f2bf(s.a.vnew[d0 + 1]);
+#pragma unroll
+    for (int u = 0; u < PQ; ++u) {                        // the new positions' bf16 k, v into the tiles
+      const int q = qlo + (NWAVE - 1 - wave) + u * NWAVE;
+      if (q <= qhi) {
+        const int ci = q / CHUNK - c0, tn = q % CHUNK;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int d = lane + 64 * h;
+          ((uint16_t*)&s.a.kt[ci][d / 8][tn])[d % 8] = f2bf(kn[u][h]);
+          ((uint16_t*)&s.a.vt[ci][tn / 8][h][lane])[tn % 8] = f2bf(vn[u][h]);
+        }
+        if (q == pos) {                                   // paged append (:121): K [blk][NKV][HD/8][BS][8], V [blk][NKV][HD][BS]
+          const int blk = ld_i(btab + pos / BS), off = pos % BS;
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const int d = lane + 64 * h;
+            st_u16(Lw.kc + ((((size_t)blk * NKV + g) * (HD / 8) + d / 8) * BS + off) * 8 + d % 8, f2bf(kn[u][h]));
+            st_u16(Lw.vc + (((size_t)blk * NKV + g) * HD + d) * BS + off, f2bf(vn[u][h]));
+          }
+        }
+      }
     }
     __syncthreads();
-    if (has_new && threadIdx.x < HD) {                    // paged append (:121): K [blk][NKV][HD/8][BS][8], V [blk][NKV][HD][BS]
-      const int blk = ld_i(btab + pos / BS), off = pos % BS, d = threadIdx.x;
-      st_u16(Lw.kc + ((((size_t)blk * NKV + g) * (HD / 8) + d / 8) * BS + off) * 8 + d % 8, f2bf(s.a.knew[d]));
-      st_u16(Lw.vc + (((size_t)blk * NKV + g) * HD + d) * BS + off, f2bf(s.a.vnew[d]));
-    }
     auto bcast = [](float v, int l) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l)); };
     // per chunk: scores (:126): lane = position t0 + lane; s_t = (q . k_t in ascending d) * scale; the chunk max m;
     // p_t = exp(s_t - m) in lane t.  Then V (:127-128): lanes = dims (lane, lane + 64); a = sum_t p_t v_t[d] and

@@ -43,7 +43,7 @@ class EtxmkConfig(C.Structure):
                [(n, C.c_int32) for n in ("kv_lora", "qk_nope", "qk_rope", "v_head", "n_shared", "first_dense",
                                          "dense_I")] + \
                [(n, C.c_float) for n in ("routed_scale", "rope_factor", "rope_mscale", "rope_mscale_all", "beta_fast",
-                                         "beta_slow")] + [("rope_orig_max", C.c_int32)]
+                                         "beta_slow")] + [("rope_orig_max", C.c_int32), ("prefill", C.c_int32)]
 
 
 class EtxmkPlanInfo(C.Structure):
@@ -94,6 +94,7 @@ class ModelConfig:
     beta_fast: float = 32.0
     beta_slow: float = 1.0
     rope_orig_max: int = 4096
+    prefill: int = 0              # positions per prefill launch (Qwen3): 0 reads prompts token by token
     name: str = field(default="custom", compare=False)
 
     def as_struct(self) -> EtxmkConfig:
@@ -156,6 +157,7 @@ def load(path: Path | None = None):
         "etxmk_read_tokens_seq": [vp, i32, C.POINTER(i32), i32, vp],
         "etxmk_step": [vp, i32, i32, vp],
         "etxmk_step_batch": [vp, C.POINTER(i32), i32, vp],
+        "etxmk_prefill": [vp, i32, i32, i32, i32, vp],
         "etxmk_step_layers": [vp, i32, i32, i32, vp],
         "etxmk_set_residual": [vp, C.POINTER(C.c_float), vp],
         "etxmk_read_residual": [vp, C.POINTER(C.c_float), vp],
@@ -260,6 +262,7 @@ class Decoder:
             _check(self.L, self.L.etxmk_set_fused(h, int(fused)))
             _check(self.L, self.L.etxmk_set_grid(h, int(workgroups)))
         self._nwg = int(workgroups)
+        self.fused = bool(fused)
         self._dumps = None
 
     # ---- plumbing
@@ -400,6 +403,31 @@ class Decoder:
         mask = sum(1 << b for b, f in enumerate(flags) if f)
         _check(self.L, self.L.etxmk_step_batch(self.h, pos.ctypes.data_as(C.POINTER(C.c_int32)), mask, self._stream()))
 
+    def prefill(self, pos0: int, n: int, write_next: bool = True, seq: int = 0):
+        """Positions pos0 .. pos0 + n - 1 of sequence seq in one launch, one row per position."""
+        _check(self.L, self.L.etxmk_prefill(self.h, seq, pos0, n, int(write_next), self._stream()))
+
+    @property
+    def prefill_rows(self) -> int:
+        """Positions one prefill launch takes (0: this handle reads prompts token by token)."""
+        c = self.cfg
+        if c.arch != ARCH_QWEN3 or not self.fused:
+            return 0
+        return max(c.batch, c.prefill) if (c.batch > 1 or c.prefill > 0) else 0
+
+    def feed_prompt(self, n: int, seq: int = 0, rows: int | None = None):
+        """Positions 0 .. n - 1 of sequence seq (its tokens set), the last one writing the greedy token at n: in
+        launches of `rows` positions (default prefill_rows; 0 or 1 = one decode step per position)."""
+        rows = self.prefill_rows if rows is None else rows
+        if rows > 1:
+            for p0 in range(0, n, rows):
+                self.prefill(p0, min(rows, n - p0), write_next=p0 + rows >= n, seq=seq)
+        elif self.cfg.batch == 1:
+            for pos in range(n):
+                self.step(pos, write_next=pos + 1 >= n)
+        else:
+            raise ValueError("a batched handle without prefill rows reads prompts through generate_batch")
+
     def step_layers(self, pos: int, l0: int, l1: int):
         _check(self.L, self.L.etxmk_step_layers(self.h, pos, l0, l1, self._stream()))
 
@@ -449,9 +477,11 @@ class Decoder:
         _check(self.L, self.L.etxmk_barriers_per_step(self.h, C.byref(n)))
         return int(n.value)
 
-    def generate_batch(self, prompts, n_new: int) -> np.ndarray:
-        """Batched greedy decode: sequence b reads prompts[b] token by token, then decodes; every sequence moves one
-        position per step (sequences with shorter prompts start decoding earlier).  Returns [batch][n_new] ids."""
+    def generate_batch(self, prompts, n_new: int, prefill: bool | None = None) -> np.ndarray:
+        """Batched greedy decode; returns [batch][n_new] ids.  With prefill (the default where the handle has
+        prefill rows) each prompt goes through prefill launches, then every sequence decodes from the end of its
+        prompt; without, sequence b reads prompts[b] token by token inside the batched steps and every sequence moves
+        one position per step (sequences with shorter prompts start decoding earlier)."""
         B = self.cfg.batch
         prompts = [list(int(t) for t in p) for p in prompts]
         if len(prompts) != B or min(len(p) for p in prompts) < 1:
@@ -462,6 +492,15 @@ class Decoder:
             raise ValueError(f"prompts + {n_new} new tokens exceed max_ctx {self.cfg.max_ctx}")
         for b, p in enumerate(prompts):
             self.set_tokens(p, seq=b)
+        if prefill is None:
+            prefill = self.prefill_rows > 1
+        if prefill:
+            for b in range(B):
+                self.feed_prompt(lens[b], seq=b)
+            for s in range(n_new - 1):
+                self.step_batch([lens[b] + s for b in range(B)], write_next=True)
+            self.sync()
+            return np.stack([self.read_tokens(lens[b] + n_new - 1, seq=b)[lens[b] - 1:] for b in range(B)])
         # sequence b decodes positions [0, lens[b] + n_new - 1); it waits (repeats its last step's position) once
         # done, which rewrites the same cache entry with the same values
         for s in range(T):
@@ -471,16 +510,22 @@ class Decoder:
         return np.stack([self.read_tokens(lens[b] + n_new - 1, seq=b)[lens[b] - 1:lens[b] - 1 + n_new]
                          for b in range(B)])
 
-    def generate(self, prompt, n_new: int) -> np.ndarray:
-        """Feed the prompt token by token, then n_new greedy steps; returns the generated ids
-        (examples/llm/host.hip:203-213 and ref_numpy.py:181-186 drive the same loop)."""
+    def generate(self, prompt, n_new: int, prefill: bool | None = None) -> np.ndarray:
+        """Feed the prompt (prefill launches where the handle has prefill rows, else token by token), then n_new
+        greedy steps; returns the generated ids (examples/llm/host.hip:203-213 and ref_numpy.py:181-186 drive the
+        same loop token by token; prefill reproduces it bit for bit)."""
         prompt = list(int(t) for t in prompt)
         P = len(prompt)
         if P < 1 or P + n_new > self.cfg.max_ctx:
             raise ValueError(f"prompt {P} + {n_new} new tokens exceed max_ctx {self.cfg.max_ctx}")
+        if self.cfg.batch != 1:
+            raise ValueError("batched handles generate through generate_batch")
         self.set_tokens(prompt)
-        for pos in range(P + n_new - 1):
-            self.step(pos, write_next=pos + 1 >= P)
+        if prefill is None:
+            prefill = self.prefill_rows > 1
+        self.feed_prompt(P, rows=None if prefill else 1)
+        for pos in range(P, P + n_new - 1):
+            self.step(pos, write_next=True)
         self.sync()
         out = self.read_tokens(P + n_new - 1)
         return out[P - 1:P - 1 + n_new]

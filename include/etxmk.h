@@ -67,6 +67,8 @@ typedef struct etxmk_config {
   int32_t n_shared, first_dense, dense_I;
   float routed_scale, rope_factor, rope_mscale, rope_mscale_all, beta_fast, beta_slow;
   int32_t rope_orig_max;
+  /* rows of etxmk_prefill launches (0..16; Qwen3): the workspace holds max(batch, prefill) rows of activations */
+  int32_t prefill;
 } etxmk_config;
 
 /* Weight types.  ETXMK_W_FP8: the QKV, O, expert (gate/up, down) and dense MLP matrices are stored as OCP e4m3
@@ -153,6 +155,15 @@ int etxmk_step(etxmk_handle* h, int32_t pos, int32_t write_next, void* stream);
  * token also goes to its tokens[positions[b] + 1] (clear while the sequence is still reading its prompt).
  * Reference: vl_set_params with one VlParams per request (examples/vllm_llm/vl_tiles.hip:92-95) + etx_host::run. */
 int etxmk_step_batch(etxmk_handle* h, const int32_t* positions, int32_t write_next_mask, void* stream);
+
+/* Batched prefill: positions pos0 .. pos0 + n - 1 of sequence seq (their tokens set beforehand) in one launch of
+ * the batched persistent kernel, one row per position (fused mode, Qwen3, n <= max(batch, prefill)).  Each row
+ * computes what etxmk_step computes at its position, bit for bit: its K/V row goes to the cache, its greedy token
+ * to out_tokens[pos], and, when write_next != 0, the last row's also to tokens[pos0 + n].  The rows attend to the
+ * cache below pos0 and to the launch's own K/V rows (taken from their QKV outputs inside the launch).  Other
+ * sequences are untouched.  Reference: the prompt loop of examples/llm/host.hip:203-213 (one decode step per
+ * prompt token), which this replaces by ceil(prompt / n) launches. */
+int etxmk_prefill(etxmk_handle* h, int32_t seq, int32_t pos0, int32_t n, int32_t write_next, void* stream);
 
 /* Layers [l0, l1) only, on the residual already in the workspace (etxmk_set_residual), no embedding and
  * no head: the single-layer configuration (single-sequence handles).  Reference: a graph of one layer

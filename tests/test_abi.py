@@ -29,7 +29,8 @@ def test_sizes_of_real_configurations():
 
 
 @pytest.mark.parametrize("bad", [dict(HD=64), dict(H=3000), dict(batch=0), dict(batch=17), dict(block_size=48),
-                                 dict(max_ctx=10**6), dict(TOPK=9), dict(E=0), dict(NKV=3)])
+                                 dict(max_ctx=10**6), dict(TOPK=9), dict(E=0), dict(NKV=3), dict(prefill=17),
+                                 dict(prefill=-1)])
 def test_config_refused(bad):
     d = configs.TINY_MOE.as_dict()
     d.update(bad)
@@ -40,10 +41,20 @@ def test_config_refused(bad):
 
 
 def test_batch_needs_a_batched_kernel():
-    # Qwen3-8B's dense down projection (12288 long) has no batched kernel: refused, not run wrongly
-    with pytest.raises(N.EtxmkError) as e:
-        N.sizes(configs.with_layers(configs.QWEN3_8B, 36, batch=2))
-    assert e.value.code == N.EINVAL and "batched" in str(e.value)
+    # Qwen3-8B's dense down projection (12288 long) has a batch-4 kernel only: beyond it refused, not run wrongly
+    N.sizes(configs.with_layers(configs.QWEN3_8B, 36, batch=4))
+    for kw in (dict(batch=5), dict(prefill=16)):
+        with pytest.raises(N.EtxmkError) as e:
+            N.sizes(configs.with_layers(configs.QWEN3_8B, 36, **kw))
+        assert e.value.code == N.EINVAL and "batched" in str(e.value), kw
+
+
+def test_prefill_rows_size_the_activations_only():
+    one = N.sizes(configs.QWEN3_30B_A3B)
+    pf = N.sizes(configs.with_layers(configs.QWEN3_30B_A3B, 48, prefill=16))
+    b16 = N.sizes(configs.with_layers(configs.QWEN3_30B_A3B, 48, batch=16))
+    assert pf["weights"] == one["weights"] and pf["kv"] == one["kv"]     # one sequence's cache
+    assert one["workspace"] < pf["workspace"] < b16["workspace"]         # 16 activation rows, one token row
 
 
 def test_batch_sizes_scale_per_sequence():
@@ -106,7 +117,7 @@ def test_deepseek_v2_lite_sizes():
 
 
 @pytest.mark.parametrize("bad", [dict(wdtype=1), dict(batch=5), dict(kv_lora=256), dict(block_size=8),
-                                 dict(HD=128), dict(NH=12), dict(MI=1024)])
+                                 dict(HD=128), dict(NH=12), dict(MI=1024), dict(prefill=4)])
 def test_deepseek_config_refused(bad):
     d = configs.DEEPSEEK_V2_LITE.as_dict()
     d.update(bad)
