@@ -292,11 +292,14 @@ def main():
                     help="prompt positions per prefill launch (batched kernel); 0 or 1: one decode step per position")
     ap.add_argument("--batch", type=int, default=1, help="sequences per step (> 1: the batched step, not the headline)")
     ap.add_argument("--ctx-lo", type=int, default=512)
-    ap.add_argument("--ctx-hi", type=int, default=4096)
+    ap.add_argument("--ctx-hi", type=int, default=0,
+                    help="batched contexts' upper bound (default 4096; 2048 for deepseek-v2-lite, BASELINE configs[3])")
     ap.add_argument("--fp8", action="store_true", help="fp8 e4m3 weights with per-row scales (BASELINE.json configs[4])")
     ap.add_argument("--model", default="qwen3-30b-a3b", choices=["qwen3-30b-a3b", "deepseek-v2-lite"],
                     help="deepseek-v2-lite: the batched multi-head latent attention step (BASELINE.json configs[3])")
     a = ap.parse_args()
+    if a.ctx_hi <= 0:
+        a.ctx_hi = 2048 if a.model == "deepseek-v2-lite" else 4096
     if a.gpus != 1:
         print(f"bench.py: this build runs on exactly one GPU (asked for {a.gpus}); multi-GPU sharding is a design "
               f"note only", file=sys.stderr)

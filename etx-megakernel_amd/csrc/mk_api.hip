@@ -224,7 +224,7 @@ int check_config(const etxmk_config* c) {
   if (c->arch != ETXMK_ARCH_QWEN3 && c->arch != ETXMK_ARCH_DSV2) return fail(ETXMK_EINVAL, "architecture %d unknown", c->arch);
   if (c->prefill < 0 || c->prefill > MAX_B) return fail(ETXMK_EINVAL, "prefill rows %d outside 0..%d", c->prefill, MAX_B);
   if (c->arch == ETXMK_ARCH_DSV2) {
-    if (c->prefill > 0) return fail(ETXMK_EINVAL, "prefill launches serve Qwen3 handles");
+    if (c->prefill > MAX_B_DS) return fail(ETXMK_EINVAL, "prefill rows %d outside 0..%d", c->prefill, MAX_B_DS);
     return check_ds(c);
   }
   if (c->HD != HDIM) return fail(ETXMK_EINVAL, "head_dim %d unsupported (the attention phase is built for %d)", c->HD, HDIM);
@@ -575,7 +575,7 @@ int etxmk_bind(etxmk_handle* h, void* weights, void* kv, void* workspace) {
   HIPCHK(hipMemset(h->wsp + h->ws.x, 0, 4ull * c.H * rows_of(c)));
   HIPCHK(hipMemset(h->wsp + h->ws.x16, 0, 2ull * c.H * rows_of(c)));
   HIPCHK(hipMemset(h->wsp + h->ws.acnt, 0, acnt_bytes(c)));
-  if (ds) HIPCHK(hipMemset(h->wsp + h->ws.h16d, 0, 2ull * (c.first_dense > 0 ? ds_ip(c) : 8) * c.batch));  // zero pads
+  if (ds) HIPCHK(hipMemset(h->wsp + h->ws.h16d, 0, 2ull * (c.first_dense > 0 ? ds_ip(c) : 8) * rows_of(c)));  // zero pads
   h->bar_epoch = 0;
   return ETXMK_OK;
 }
@@ -973,13 +973,12 @@ int etxmk_step_batch(etxmk_handle* h, const int32_t* positions, int32_t write_ne
 int etxmk_prefill(etxmk_handle* h, int32_t seq, int32_t pos0, int32_t n, int32_t write_next, void* stream) {
   if (!h) return fail(ETXMK_EINVAL, "NULL handle");
   const etxmk_config& c = h->c;
-  if (is_ds(c)) return fail(ETXMK_EINVAL, "prefill launches serve Qwen3 handles");
   if (!h->fused) return fail(ETXMK_EINVAL, "prefill runs the persistent kernel only");
   if (seq < 0 || seq >= c.batch) return fail(ETXMK_EINVAL, "sequence %d outside 0..%d", seq, c.batch - 1);
   if (n < 1 || n > rows_of(c)) return fail(ETXMK_EINVAL, "%d prefill positions outside 1..%d", n, rows_of(c));
   if (pos0 < 0 || pos0 + n > c.max_ctx)
     return fail(ETXMK_EINVAL, "positions %d..%d outside 0..%d", pos0, pos0 + n - 1, c.max_ctx - 1);
-  if (!batch_kernel(c, n))
+  if (!is_ds(c) && !batch_kernel(c, n))
     return fail(ETXMK_EINVAL, "no batched persistent kernel for %d rows, H %d, NH*HD %d, %s %d", n, c.H, c.NH * c.HD,
                 c.moe ? "MI" : "I", c.moe ? c.MI : c.I);
   int32_t posv[MAX_B];

@@ -44,7 +44,6 @@ struct MlaTiles {
   alignas(16) float xo[MLA_KVL];          // P2c: o_c of the item, in the W_UV rows' stored order
   alignas(16) float p[MLA_G][2 * MAX_CHUNKS];  // chunk: exp(s - m) per position; merge: chunk weights, chunk sums
   float m[MLA_G];
-  alignas(16) float cn[MLA_CD];           // the sequence's new latent row
 };
 
 template <int B, int XC>
@@ -95,12 +94,17 @@ __device__ __forceinline__ void rope_ds_pair(float a, float b, float c, float s,
   hi = bfr(b * c + a * s);
 }
 
-// The new latent row of sequence b, one wave: c = kv_a_layernorm(kv_a) (reference_decode.py:231; the sum of
-// squares in dot order, then bfr(w * bfr(x * r))) and k_pe roped (:234), as fp32 (bf16 values) into cn; with
-// `append` also as bf16 into the latent cache at the sequence's position (:236-237)
-__device__ __forceinline__ void latent_row(const Params& p, const LayerW& Lw, int b, bool append, float* cn) {
-  const int lane = lane_id(), pos = p.posb[b], BS = p.BS;
+// The latent row of row b's QKV output at position q, one wave: c = kv_a_layernorm(kv_a) (reference_decode.py:231;
+// the sum of squares in dot order, then bfr(w * bfr(x * r))) and k_pe roped at q (:234), as fp32 (bf16 values) in
+// registers: lane l holds c[l + 64e] in c[e], and lanes < 32 the roped pair (lo, hi) = dims 512 + l, 544 + l.
+struct LatentRow {
+  float c[MLA_KVL / 64];
+  float lo, hi;
+};
+__device__ __forceinline__ LatentRow latent_row(const Params& p, const LayerW& Lw, int b, int q) {
+  const int lane = lane_id();
   const float* kva = p.qkv + (size_t)b * p.nqkv + p.NH * MLA_QD;
+  LatentRow r;
   float x[MLA_KVL / 64];
 #pragma unroll
   for (int e = 0; e < MLA_KVL / 64; ++e) x[e] = ld_ag(kva + lane + 64 * e);
@@ -110,28 +114,26 @@ __device__ __forceinline__ void latent_row(const Params& p, const LayerW& Lw, in
 #pragma unroll
   for (int e = 0; e < MLA_KVL / 64; ++e) acc = __builtin_fmaf(x[e], x[e], acc);
   acc = wave_sum(acc);
-  const float r = 1.0f / __builtin_sqrtf(acc / (float)MLA_KVL + p.eps);
-  const int blk = ld_i(p.btab + (size_t)b * p.nbps + pos / BS), off = pos % BS;
-  uint16_t* row = Lw.kc + (size_t)blk * MLA_CG * BS * 8 + off * 8;   // dim k at row + (k / 8) * BS * 8 + k % 8
+  const float rs = 1.0f / __builtin_sqrtf(acc / (float)MLA_KVL + p.eps);
 #pragma unroll
-  for (int e = 0; e < MLA_KVL / 64; ++e) {
-    const int k = lane + 64 * e;
-    const float c = bfr(bf2f(ld_u16(Lw.kn + k)) * bfr(x[e] * r));
-    if (append) st_u16(row + (size_t)(k / 8) * BS * 8 + k % 8, f2bf(c));
-    cn[k] = c;
-  }
+  for (int e = 0; e < MLA_KVL / 64; ++e) r.c[e] = bfr(bf2f(ld_u16(Lw.kn + lane + 64 * e)) * bfr(x[e] * rs));
+  r.lo = r.hi = 0.0f;
   if (lane < MLA_R / 2) {
-    const float cs = ld_f(p.rope_cos + (size_t)pos * (MLA_R / 2) + lane);
-    const float sn = ld_f(p.rope_sin + (size_t)pos * (MLA_R / 2) + lane);
-    float lo, hi;
-    rope_ds_pair(a0, a1, cs, sn, lo, hi);
-    const int k0 = MLA_KVL + lane, k1 = MLA_KVL + MLA_R / 2 + lane;
-    if (append) {
-      st_u16(row + (size_t)(k0 / 8) * BS * 8 + k0 % 8, f2bf(lo));
-      st_u16(row + (size_t)(k1 / 8) * BS * 8 + k1 % 8, f2bf(hi));
-    }
-    cn[k0] = lo;
-    cn[k1] = hi;
+    const float cs = ld_f(p.rope_cos + (size_t)q * (MLA_R / 2) + lane);
+    const float sn = ld_f(p.rope_sin + (size_t)q * (MLA_R / 2) + lane);
+    rope_ds_pair(a0, a1, cs, sn, r.lo, r.hi);
+  }
+  return r;
+}
+// visit (dim, value) of a latent row held as above
+template <class F>
+__device__ __forceinline__ void latent_dims(const LatentRow& r, F f) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int e = 0; e < MLA_KVL / 64; ++e) f(lane + 64 * e, r.c[e]);
+  if (lane < MLA_R / 2) {
+    f(MLA_KVL + lane, r.lo);
+    f(MLA_KVL + MLA_R / 2 + lane, r.hi);
   }
 }
 
@@ -201,13 +203,16 @@ __device__ __forceinline__ void phase_mla_attn(const Params& p, int layer, S& s,
   // the chunk's cached latent rows, HBM -> LDS (global_load_lds, 16 bytes per lane): wave w copies groups w, w+8, ...
   // (the rows do not depend on this step, so the first item's copies are issued before the wait; the current
   // position's row is computed here instead)
+  // positions from first_new(pos) on are this launch's (the row's own, and in prefill the earlier rows'): built
+  // from the rows' QKV outputs, not read from the cache
+  auto first_new = [&](int pos) { return p.pf ? p.posb[0] : pos; };
   auto load_tile = [&](const MlaItem& it) {
-    const int t0 = it.c * CHUNK, n = it.pos + 1;
+    const int t0 = it.c * CHUNK, n = it.pos + 1, fp = first_new(it.pos);
     const int g16 = t0 + (lane & ~15);                   // the swizzle permutes inside 16 positions: one block
     const int blk = g16 < n ? ld_i(p.btab + (size_t)it.b * p.nbps + g16 / BS) : 0;
     for (int j = wave; j < MLA_CG; j += NWAVE) {
       const int T = t0 + (lane ^ (j & 15));
-      if (T < n && T != it.pos)
+      if (T < n && T < fp)
         __builtin_amdgcn_global_load_lds((const MK_G void*)(Lw.kc + (((size_t)blk * MLA_CG + j) * BS + T % BS) * 8),
                                          (__attribute__((address_space(3))) void*)&s.a.t[j][0], 16, 0, 0);
     }
@@ -218,7 +223,8 @@ __device__ __forceinline__ void phase_mla_attn(const Params& p, int layer, S& s,
     const MlaItem it = mla_item(p, item, NHG);
     const int b = it.b, c = it.c, pos = it.pos, n = pos + 1;
     const int t0 = c * CHUNK, len = min(CHUNK, n - t0);
-    const bool has_new = pos < t0 + len;
+    // this launch's positions in the chunk: [nlo, nhi] (decode: pos alone, in the chunk holding it)
+    const int nlo = max(first_new(pos), t0), nhi = min(pos, t0 + CHUNK - 1);
     if (item != (int)blockIdx.x) load_tile(it);
     // queries of head hg*GH + wave, in registers: q_c dims lane + 64e (agent-scope loads: written by P1b), and q_pe
     // roped (reference_decode.py:235): lane i < 32 holds dims i (lo) and i + 32 (hi).  The score loop takes each
@@ -237,16 +243,25 @@ __device__ __forceinline__ void phase_mla_attn(const Params& p, int layer, S& s,
         rope_ds_pair(a0, a1, cs, sn, qlo, qhi);
       }
     }
-    // the chunk holding the current position builds its latent row (the first head group appends it to the cache)
-    if (has_new && wave == NWAVE - 1) latent_row(p, Lw, b, it.hg == 0, s.a.cn);
+    // the launch's positions in this chunk: wave NWAVE-1-w builds the latent row of position nlo + w from the QKV
+    // output of its row, b - (pos - q) (a launch has at most MAX_B_DS <= NWAVE rows), writes it into the tile slots
+    // once the cached rows have landed, and the first head group's item appends the row's own position to the cache
+    const int q = nlo + (NWAVE - 1 - wave);
+    LatentRow lr;
+    if (q <= nhi) lr = latent_row(p, Lw, b - (pos - q), q);
     __builtin_amdgcn_s_waitcnt(0);                        // this wave's tile copies have landed in LDS
     __syncthreads();
-    if (has_new && (int)threadIdx.x < MLA_CG) {           // the current position's row into its slots
-      const int jj = threadIdx.x, tn = pos - t0;
-      uint32_t o[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) o[e] = (uint32_t)f2bf(s.a.cn[8 * jj + 2 * e]) | ((uint32_t)f2bf(s.a.cn[8 * jj + 2 * e + 1]) << 16);
-      s.a.t[jj][tn ^ (jj & 15)] = u32x4{o[0], o[1], o[2], o[3]};
+    if (q <= nhi) {
+      const int tn = q - t0;
+      latent_dims(lr, [&](int k, float v) {
+        const int jj = k / 8;
+        ((uint16_t*)&s.a.t[jj][tn ^ (jj & 15)])[k % 8] = f2bf(v);
+      });
+      if (q == pos && it.hg == 0) {                       // the cache append (reference_decode.py:236-237)
+        const int blk = ld_i(p.btab + (size_t)b * p.nbps + pos / BS), off = pos % BS;
+        uint16_t* row = Lw.kc + (size_t)blk * MLA_CG * BS * 8 + off * 8;   // dim k at row + (k / 8) * BS * 8 + k % 8
+        latent_dims(lr, [&](int k, float v) { st_u16(row + (size_t)(k / 8) * BS * 8 + k % 8, f2bf(v)); });
+      }
     }
     __syncthreads();
     // scores: wave = head, lane = position

@@ -411,7 +411,7 @@ class Decoder:
     def prefill_rows(self) -> int:
         """Positions one prefill launch takes (0: this handle reads prompts token by token)."""
         c = self.cfg
-        if c.arch != ARCH_QWEN3 or not self.fused:
+        if not self.fused:
             return 0
         return max(c.batch, c.prefill) if (c.batch > 1 or c.prefill > 0) else 0
 

@@ -117,7 +117,7 @@ def test_deepseek_v2_lite_sizes():
 
 
 @pytest.mark.parametrize("bad", [dict(wdtype=1), dict(batch=5), dict(kv_lora=256), dict(block_size=8),
-                                 dict(HD=128), dict(NH=12), dict(MI=1024), dict(prefill=4)])
+                                 dict(HD=128), dict(NH=12), dict(MI=1024), dict(prefill=5)])
 def test_deepseek_config_refused(bad):
     d = configs.DEEPSEEK_V2_LITE.as_dict()
     d.update(bad)

@@ -107,7 +107,7 @@ def test_tiny_batch_prompts_mixed_lengths(gpu):
     dec = N.Decoder(cfg)
     dec.init_weights(SEED, 0.02)
     prompts = [O.gen_tokens(SEED + b, 3 + 5 * b, cfg.V) for b in range(4)]
-    got = dec.generate_batch(prompts, 6)
+    got = dec.generate_batch(prompts, 6, prefill=False)
     orc = O.OracleModel(configs.TINY_MOE.as_dict(), SEED, 0.02)
     for b, p in enumerate(prompts):
         o = O.OracleModel(configs.TINY_MOE.as_dict(), SEED, 0.02)

@@ -110,7 +110,7 @@ def test_tiny_mla_prompts_mixed_lengths(gpu):
     dec = N.Decoder(cfg)
     dec.init_weights(SEED, 0.02)
     prompts = [O.gen_tokens(SEED + b, 3 + 7 * b, cfg.V) for b in range(4)]
-    got = dec.generate_batch(prompts, 5)
+    got = dec.generate_batch(prompts, 5, prefill=False)
     for b, p in enumerate(prompts):
         o = O.OracleModel(configs.TINY_MLA.as_dict(), SEED, 0.02)
         toks = list(p)

@@ -115,3 +115,63 @@ def test_qwen3_30b_a3b_prefill_two_layers(gpu):
 def test_qwen3_8b_prefill_two_layers(gpu):
     """Qwen3-8B shapes (two dense layers, 12288-long down rows): 4 positions per launch of its batch-4 kernel."""
     run_prefill(configs.with_layers(configs.QWEN3_8B, 2, prefill=4), 22, n_new=4, rows=4)
+
+
+def run_prefill_mla(cfg, prompt_len, n_new, rows):
+    """DeepSeek-V2: the prompt in launches of `rows` positions, then n_new - 1 decode steps (a batch-1 handle runs
+    its batched kernel as a batch of one); the latent cache and every position's greedy token against the oracle."""
+    t0 = time.time()
+    say(f"[gpu] prefill {cfg.name}: {prompt_len} prompt positions, {rows} per launch, {n_new} new")
+    dec = N.Decoder(cfg)
+    dec.init_weights(SEED, 0.02)
+    orc = O.OracleModel(cfg.as_dict(), SEED, 0.02)
+    prompt = O.gen_tokens(SEED, prompt_len, cfg.V)
+    dec.set_tokens(prompt)
+    dec.feed_prompt(prompt_len, rows=rows)
+    for pos in range(prompt_len, prompt_len + n_new - 1):
+        dec.step(pos, write_next=True)
+    dec.sync()
+    seq, greedy = list(prompt), []
+    for pos in range(prompt_len + n_new - 1):
+        t = orc.step(seq[pos], pos)
+        greedy.append(t)
+        if pos + 1 >= prompt_len:
+            seq.append(t)
+    say(f"[gpu]   device and oracle done ({time.time() - t0:.1f}s)")
+    got = dec.read_tokens(prompt_len + n_new - 1)
+    bad = [i for i in range(len(greedy)) if got[i] != greedy[i]]
+    assert not bad, f"greedy tokens differ at positions {bad[:10]}"
+    for L in range(cfg.L):
+        assert np.array_equal(dec.kv_layer(L)[0], orc.kv(L)[0]), f"layer {L}: latent cache differs"
+    orc.close()
+    dec.close()
+
+
+@pytest.mark.parametrize("rows,plen", [(4, 90), (3, 70)], ids=["rows4", "rows3"])
+def test_tiny_mla_prefill_bit_exact(gpu, rows, plen):
+    """Launches of 3 positions straddle the 64-position chunk boundary; the last launch is ragged."""
+    run_prefill_mla(configs.with_layers(configs.TINY_MLA, configs.TINY_MLA.L, prefill=4), plen, n_new=5, rows=rows)
+
+
+def test_tiny_mla_batched_handle_prefill(gpu):
+    cfg = configs.with_layers(configs.TINY_MLA, configs.TINY_MLA.L, batch=4)
+    say(f"[gpu] mla prefill per sequence, batch-4 handle {cfg.name}")
+    dec = N.Decoder(cfg)
+    dec.init_weights(SEED, 0.02)
+    prompts = [O.gen_tokens(SEED + b, 6 + 11 * b, cfg.V) for b in range(4)]
+    got = dec.generate_batch(prompts, 5, prefill=True)
+    for b, p in enumerate(prompts):
+        o = O.OracleModel(configs.TINY_MLA.as_dict(), SEED, 0.02)
+        toks = list(p)
+        for q in range(len(p) + 4):
+            t = o.step(toks[q], q)
+            if q + 1 >= len(p):
+                toks.append(t)
+        assert list(got[b]) == toks[len(p):], f"sequence {b}"
+        o.close()
+    dec.close()
+
+
+def test_deepseek_v2_lite_prefill_two_layers(gpu):
+    """DeepSeek-V2-Lite shapes (the dense layer 0 and one MoE layer): 4 positions per launch."""
+    run_prefill_mla(configs.with_layers(configs.DEEPSEEK_V2_LITE, 2, prefill=4), 26, n_new=4, rows=4)
