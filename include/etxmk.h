@@ -67,7 +67,8 @@ typedef struct etxmk_config {
   int32_t n_shared, first_dense, dense_I;
   float routed_scale, rope_factor, rope_mscale, rope_mscale_all, beta_fast, beta_slow;
   int32_t rope_orig_max;
-  /* rows of etxmk_prefill launches (0..16; Qwen3): the workspace holds max(batch, prefill) rows of activations */
+  /* rows of etxmk_prefill launches (0..16; DeepSeek-V2 0..4): the workspace holds max(batch, prefill) rows of
+   * activations */
   int32_t prefill;
 } etxmk_config;
 
@@ -157,7 +158,7 @@ int etxmk_step(etxmk_handle* h, int32_t pos, int32_t write_next, void* stream);
 int etxmk_step_batch(etxmk_handle* h, const int32_t* positions, int32_t write_next_mask, void* stream);
 
 /* Batched prefill: positions pos0 .. pos0 + n - 1 of sequence seq (their tokens set beforehand) in one launch of
- * the batched persistent kernel, one row per position (fused mode, Qwen3, n <= max(batch, prefill)).  Each row
+ * the batched persistent kernel, one row per position (fused mode, n <= max(batch, prefill)).  Each row
  * computes what etxmk_step computes at its position, bit for bit: its K/V row goes to the cache, its greedy token
  * to out_tokens[pos], and, when write_next != 0, the last row's also to tokens[pos0 + n].  The rows attend to the
  * cache below pos0 and to the launch's own K/V rows (taken from their QKV outputs inside the launch).  Other
