@@ -94,7 +94,7 @@ class ModelConfig:
     beta_fast: float = 32.0
     beta_slow: float = 1.0
     rope_orig_max: int = 4096
-    prefill: int = 0              # positions per prefill launch (Qwen3): 0 reads prompts token by token
+    prefill: int = 0              # rows per prefill launch (<= 16; DeepSeek-V2 <= 4); 0: prompts token by token
     name: str = field(default="custom", compare=False)
 
     def as_struct(self) -> EtxmkConfig:
