@@ -208,14 +208,15 @@ const char* kernel_symbol(const etxmk_config& c, int* cap) {
   return best;
 }
 
-// grid barriers of a step over layers [l0, l1) (plus the head): one per phase
-int barriers_of(const etxmk_config& c, int l0, int l1, int head) {
+// grid barriers of a launch over layers [l0, l1) (plus the head), one per phase; `batched`: the batched kernel
+// (Qwen3: the attention merge is a phase of its own)
+int barriers_of(const etxmk_config& c, int l0, int l1, int head, bool batched) {
   if (c.arch == ETXMK_ARCH_DSV2) {                         // 5 attention phases, then 2 dense or 3 MoE phases
     int n = 0;
     for (int l = l0; l < l1; ++l) n += l < c.first_dense ? 7 : 8;
     return n + (head ? 1 : 0);
   }
-  return (c.moe ? 6 : 5) * (l1 - l0) + (head ? 1 : 0);
+  return ((c.moe ? 6 : 5) + (batched ? 1 : 0)) * (l1 - l0) + (head ? 1 : 0);
 }
 
 int check_config(const etxmk_config* c) {
@@ -439,7 +440,7 @@ struct etxmk_handle {
     const TensorSlot* s = slot(kind, layer);
     return s ? (const uint8_t*)(w + s->off) : nullptr;
   }
-  int barriers(int l0, int l1, int head) const { return barriers_of(c, l0, l1, head); }
+  int barriers(int l0, int l1, int head, bool batched) const { return barriers_of(c, l0, l1, head, batched); }
 };
 
 extern "C" {
@@ -479,7 +480,7 @@ int etxmk_plan(const etxmk_config* cfg, int32_t fused, etxmk_plan_info* out) {
   const char* sym = fused ? kernel_symbol(c, &cap) : "unfused";
   if (!sym) return fail(ETXMK_EINVAL, "no persistent kernel for this shape (use the unfused mode)");
   snprintf(out->kernel, sizeof out->kernel, "%s", sym);
-  out->barriers_per_step = barriers_of(c, 0, c.L, 1);
+  out->barriers_per_step = barriers_of(c, 0, c.L, 1, c.batch > 1);
   out->threads = NT;
   out->batch_capacity = cap;
   weight_layout(cfg, &out->weight_bytes);
@@ -812,7 +813,7 @@ int etxmk_set_trace(etxmk_handle* h, uint64_t* stamps) {
 
 int etxmk_barriers_per_step(etxmk_handle* h, int32_t* n) {
   if (!h || !n) return fail(ETXMK_EINVAL, "NULL argument");
-  *n = h->barriers(0, h->c.L, 1);
+  *n = h->barriers(0, h->c.L, 1, h->c.batch > 1);
   return ETXMK_OK;
 }
 
@@ -877,7 +878,7 @@ static int launch(etxmk_handle* h, const int32_t* posv, int pos, int write_next,
   if (!pf) {                               // the dump buffers hold `batch` rows; prefill rows are not dumped
     p.dump_x = h->dump_x; p.dump_ids = h->dump_ids; p.dump_wts = h->dump_wts; p.dump_logits = h->dump_logits;
   }
-  p.trace = h->fused ? h->trace : nullptr;
+  p.trace = h->fused && !pf ? h->trace : nullptr;   // the stamp buffer is sized for the handle's step kernel
   p.pos = batched ? 0 : pos; p.write_next = write_next; p.l0 = l0; p.l1 = l1; p.do_embed = embed; p.do_head = head;
   p.nwg = h->nwg;
   p.spin_ticks = 200000000ull;            // 2 s of the 100 MHz s_memrealtime clock
@@ -927,7 +928,7 @@ static int launch(etxmk_handle* h, const int32_t* posv, int pos, int write_next,
     p.bar_base = h->bar_epoch;
     void* args[] = {&p};
     HIPCHK(hipLaunchCooperativeKernel(fn, dim3(h->nwg), dim3(NT), args, 0, st));
-    h->bar_epoch += (uint32_t)h->barriers(l0, l1, head);
+    h->bar_epoch += (uint32_t)h->barriers(l0, l1, head, batched);
   } else {
     auto ph = [&](int phase, int layer) -> int {
       static void (*const kern[])(Params, int) = {etxmk_p_qkv, etxmk_p_attn, etxmk_p_oproj, etxmk_p_router,

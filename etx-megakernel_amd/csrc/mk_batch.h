@@ -24,7 +24,17 @@ namespace mk {
 constexpr int RES_ROWS = 64;            // residual rows per workgroup and sequence held for the epilogues
 constexpr int MAX_PAIRS = MAX_B * MAX_TOPK;
 constexpr int KEY_WORDS = MAX_E * MAX_B / 32;  // routed-pair keys expert * MAX_B + sequence, one bit each
-constexpr int ATTN_CPI_B = 2;           // chunks per attention item in batched kernels (one arrival per two chunks)
+constexpr int ATTN_CPI_B = 2;           // chunks per attention item in batched kernels
+
+// LDS of the batched attention phase: two buffers of ATTN_CPI_B chunk tile pairs (the next item's K and V stream in
+// while this item computes); the merge phase's per-wave chunk weights and sums
+struct AttnTilesB {
+  u32x4 kt[2][ATTN_CPI_B][HDIM / 8][CHUNK];         // [buffer][chunk][8-dim group][position]
+  u32x4 vt[2][ATTN_CPI_B][CHUNK / 8][2][CHUNK];     // [buffer][chunk][8-position group][dim half][dim in half]
+};
+struct AttnMergeB {
+  float p[NWAVE][2 * MAX_CHUNKS];
+};
 
 template <int B>
 struct SmemB {
@@ -40,7 +50,8 @@ struct SmemB {
       float xres[B][RES_ROWS];          // residual of this workgroup's output rows
       float acc[B][RES_ROWS];           // expert combine carried from one pass over the pairs to the next
     } v;
-    AttnTilesT<ATTN_CPI_B> a;
+    AttnTilesB a;
+    AttnMergeB m;
   };
   float rs[B];                          // 1/rms per sequence
   int32_t rids[B][MAX_TOPK];            // routing per sequence, slot order
@@ -373,6 +384,290 @@ __device__ __forceinline__ void phase_qkv_b(const Params& p, int layer, S& s, Wa
         return true;
       },
       p.nwg, p.trace, s.phase);
+}
+
+// P2 (batched): chunk partials per item (sequence b, kv head g, ATTN_CPI_B consecutive chunks), the single-sequence
+// phase's numerics (ref_numpy.py:116-129 in chunked form) with a pipelined schedule: the item's K and V tiles were
+// issued one item earlier into the other LDS buffer, so after the wait for them the next item's tiles are issued and
+// stream in while this item computes; the two chunks' score chains (ascending d) and P.V chains (ascending t) are
+// interleaved, with the tile reads a block ahead.  The partials go to global memory and the merge is the next phase
+// (no counter: nothing in the item loop waits for a store).
+template <int B, class S, class Wait>
+__device__ __forceinline__ void phase_attn_b(const Params& p, int layer, S& s, Wait wait) {
+  constexpr int CPI = ATTN_CPI_B;
+  static_assert(CPI == 2, "the score and P.V loops interleave two chunks");
+  const int NKV = p.NKV, NH = p.NH, G = NH / NKV, HD = HDIM, BS = p.BS;
+  const int NQKV = (NH + 2 * NKV) * HD;
+  const int nitems = p.ibase[p.B];
+  const LayerW Lw = layer_w(p, layer);
+  const int lane = lane_id(), wave = wave_u();
+  // positions from first_new(pos) on are this launch's (the row's own, and in prefill the earlier rows'): patched
+  // into the tiles from the QKV rows, not read from the cache
+  auto first_new = [&](int pos) { return p.pf ? p.posb[0] : pos; };
+  // wave w copies K dim-groups 2w, 2w+1 (lane = position) and the V position-group w (lane = dim, both halves) of
+  // every chunk of the item, HBM -> LDS buffer `buf` (global_load_lds, 16 bytes per lane)
+  auto load_kv = [&](int item, int buf) {
+    const AttnItem it = attn_item<B, CPI>(p, item);
+    const int g = it.g, pos = it.pos, n = pos + 1, nch = (n + CHUNK - 1) / CHUNK, fp = first_new(pos);
+    const int32_t* btab = p.btab + (size_t)it.b * p.nbps;
+#pragma unroll
+    for (int ci = 0; ci < CPI; ++ci) {
+      const int c = it.cp * CPI + ci;
+      if (c < nch) {
+        const int t0 = c * CHUNK, len = min(CHUNK, n - t0);
+        const int t = t0 + lane;
+        if (lane < len && t < fp) {
+          const int blk = ld_i(btab + t / BS), off = t % BS;
+          const uint16_t* kp = Lw.kc + (((size_t)blk * NKV + g) * (HD / 8)) * BS * 8 + off * 8;
+#pragma unroll
+          for (int jj = 2 * wave; jj < 2 * wave + 2; ++jj)
+            __builtin_amdgcn_global_load_lds((const MK_G void*)(kp + (size_t)jj * BS * 8),
+                                             (__attribute__((address_space(3))) void*)&s.a.kt[buf][ci][jj][0], 16, 0, 0);
+        }
+        const int tb = t0 + wave * 8;                     // 8 positions per 16-byte load
+        if (tb < t0 + len && tb < fp) {
+          const int blk = ld_i(btab + tb / BS), off = tb % BS;
+          const uint16_t* vp = Lw.vc + ((size_t)blk * NKV + g) * HD * BS + off;
+          __builtin_amdgcn_global_load_lds((const MK_G void*)(vp + (size_t)lane * BS),
+                                           (__attribute__((address_space(3))) void*)&s.a.vt[buf][ci][wave][0][0], 16, 0, 0);
+          __builtin_amdgcn_global_load_lds((const MK_G void*)(vp + (size_t)(lane + 64) * BS),
+                                           (__attribute__((address_space(3))) void*)&s.a.vt[buf][ci][wave][1][0], 16, 0, 0);
+        }
+      }
+    }
+  };
+  const float qn0 = bf2f(ld_u16(Lw.qn + lane)), qn1 = bf2f(ld_u16(Lw.qn + lane + 64));
+  const float kn0 = bf2f(ld_u16(Lw.kn + lane)), kn1 = bf2f(ld_u16(Lw.kn + lane + 64));
+  if ((int)blockIdx.x < nitems) load_kv(blockIdx.x, 0);
+  if (!wait()) return;
+  auto bcast = [](float v, int l) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l)); };
+  int k = 0;
+  for (int item = blockIdx.x; item < nitems; item += p.nwg, ++k) {
+    const int buf = k & 1;
+    const AttnItem it = attn_item<B, CPI>(p, item);
+    const int g = it.g, pos = it.pos, n = pos + 1, nch = (n + CHUNK - 1) / CHUNK;
+    const int c0 = it.cp * CPI, nc = min(CPI, nch - c0);   // chunks c0 .. c0 + nc - 1
+    const int32_t* btab = p.btab + (size_t)it.b * p.nbps;
+    const float* qkv = p.qkv + (size_t)it.b * NQKV;
+    float* apart = p.apart + (size_t)it.b * NH * MAX_CHUNKS * PART;
+    // this launch's positions in the item's chunks: [qlo, qhi] (decode: pos alone, in the item of the last chunk)
+    const int qlo = max(first_new(pos), c0 * CHUNK), qhi = min(pos, (c0 + nc) * CHUNK - 1);
+    const float rc = ld_f(p.rope_cos + (size_t)pos * (HD / 2) + lane), rs = ld_f(p.rope_sin + (size_t)pos * (HD / 2) + lane);
+    // wave j: head g*G + j, its roped q in registers (dims lane, lane + 64), broadcast with v_readlane below
+    const int j = wave;
+    float q0 = 0.0f, q1 = 0.0f;
+    if (j < G) {
+      const float* src = qkv + (size_t)(g * G + j) * HD;
+      float a0 = ld_ag(src + lane), a1 = ld_ag(src + lane + 64);
+      if (p.qk_norm) qk_norm(a0, a1, qn0, qn1, p.eps);
+      q0 = bfr(bfr(a0 * rc) + bfr(-a1 * rs));
+      q1 = bfr(bfr(a1 * rc) + bfr(a0 * rs));
+    }
+    // k (normed, roped at its position) and v of the launch's positions: position q from QKV row it.b - (pos - q);
+    // wave NWAVE-1-w takes positions qlo + w and qlo + w + NWAVE (a launch has <= 2*NWAVE rows)
+    float kn[2][2], vn[2][2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int q = qlo + (NWAVE - 1 - wave) + u * NWAVE;
+      if (q <= qhi) {
+        const float* row = p.qkv + (size_t)(it.b - (pos - q)) * NQKV;
+        float a0 = ld_ag(row + (size_t)(NH + g) * HD + lane), a1 = ld_ag(row + (size_t)(NH + g) * HD + lane + 64);
+        vn[u][0] = ld_ag(row + (size_t)(NH + NKV + g) * HD + lane);
+        vn[u][1] = ld_ag(row + (size_t)(NH + NKV + g) * HD + lane + 64);
+        float cq = rc, sq = rs;
+        if (q != pos) {
+          cq = ld_f(p.rope_cos + (size_t)q * (HD / 2) + lane);
+          sq = ld_f(p.rope_sin + (size_t)q * (HD / 2) + lane);
+        }
+        if (p.qk_norm) qk_norm(a0, a1, kn0, kn1, p.eps);
+        kn[u][0] = bfr(bfr(a0 * cq) + bfr(-a1 * sq));
+        kn[u][1] = bfr(bfr(a1 * cq) + bfr(a0 * sq));
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0);                        // this item's tiles (and this wave's loads) have landed
+    __syncthreads();                                      // ... in every wave; the other buffer is free
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {                         // the new positions' bf16 k, v into the tiles
+      const int q = qlo + (NWAVE - 1 - wave) + u * NWAVE;
+      if (q <= qhi) {
+        const int ci = q / CHUNK - c0, tn = q % CHUNK;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int d = lane + 64 * h;
+          ((uint16_t*)&s.a.kt[buf][ci][d / 8][tn])[d % 8] = f2bf(kn[u][h]);
+          ((uint16_t*)&s.a.vt[buf][ci][tn / 8][h][lane])[tn % 8] = f2bf(vn[u][h]);
+        }
+        if (q == pos) {                                   // paged append (:121): K [blk][NKV][HD/8][BS][8], V [blk][NKV][HD][BS]
+          const int blk = ld_i(btab + pos / BS), off = pos % BS;
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const int d = lane + 64 * h;
+            st_u16(Lw.kc + ((((size_t)blk * NKV + g) * (HD / 8) + d / 8) * BS + off) * 8 + d % 8, f2bf(kn[u][h]));
+            st_u16(Lw.vc + (((size_t)blk * NKV + g) * HD + d) * BS + off, f2bf(vn[u][h]));
+          }
+        }
+      }
+    }
+    __syncthreads();
+    if (item + p.nwg < nitems) load_kv(item + p.nwg, buf ^ 1);
+    if (j < G) {
+      // scores (:126), lane = position: both chunks' chains over ascending d, each broadcast q value feeding both;
+      // the K reads run a block of GB dim groups ahead.  With one chunk the second chain reads stale LDS, unused.
+      constexpr int GB = 2, NB = HDIM / 8 / GB;
+      float acc0 = 0.0f, acc1 = 0.0f;
+      u32x4 kA[2][GB], kB[2][GB];
+      auto ldk = [&](u32x4(&kk)[2][GB], int blk) {
+#pragma unroll
+        for (int u = 0; u < GB; ++u) {
+          kk[0][u] = s.a.kt[buf][0][blk * GB + u][lane];
+          kk[1][u] = s.a.kt[buf][1][blk * GB + u][lane];
+        }
+      };
+      auto fmk = [&](const u32x4(&kk)[2][GB], int blk) {
+#pragma unroll
+        for (int u = 0; u < GB; ++u) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int d = 8 * (blk * GB + u) + 2 * e;
+            const float qa = bcast(d < 64 ? q0 : q1, d & 63), qb = bcast(d + 1 < 64 ? q0 : q1, (d + 1) & 63);
+            acc0 = __builtin_fmaf(qa, bf_lo(kk[0][u][e]), acc0);
+            acc1 = __builtin_fmaf(qa, bf_lo(kk[1][u][e]), acc1);
+            acc0 = __builtin_fmaf(qb, bf_hi(kk[0][u][e]), acc0);
+            acc1 = __builtin_fmaf(qb, bf_hi(kk[1][u][e]), acc1);
+          }
+        }
+      };
+      ldk(kA, 0);
+#pragma unroll
+      for (int blk = 0; blk < NB; blk += 2) {
+        ldk(kB, blk + 1);
+        fmk(kA, blk);
+        if (blk + 2 < NB) ldk(kA, blk + 2);
+        fmk(kB, blk + 1);
+      }
+      const int len0 = min(CHUNK, n - c0 * CHUNK), len1 = nc > 1 ? min(CHUNK, n - (c0 + 1) * CHUNK) : 0;
+      const float sc0 = lane < len0 ? acc0 * p.attn_scale : -__builtin_huge_valf();
+      const float sc1 = lane < len1 ? acc1 * p.attn_scale : -__builtin_huge_valf();
+      const float m0 = wave_max(sc0), m1 = wave_max(sc1);
+      const float pr0 = lane < len0 ? expf_mk(sc0 - m0) : 0.0f;
+      const float pr1 = lane < len1 ? expf_mk(sc1 - m1) : 0.0f;
+      // V (:127-128), lanes = dims (lane, lane + 64): a = sum_t p_t v_t[d] and l = sum_t p_t over ascending t
+      float a[2][2] = {{0.0f, 0.0f}, {0.0f, 0.0f}}, l[2] = {0.0f, 0.0f};
+      auto vat = [](const u32x4& w, int e) { return (e & 1) ? bf_hi(w[e >> 1]) : bf_lo(w[e >> 1]); };
+      if (len1 == CHUNK) {                                // two full chunks: both chains together, reads ahead
+        u32x4 vA[4], vB[4];
+        auto ldv = [&](u32x4(&v)[4], int hb) {
+          v[0] = s.a.vt[buf][0][hb][0][lane];
+          v[1] = s.a.vt[buf][0][hb][1][lane];
+          v[2] = s.a.vt[buf][1][hb][0][lane];
+          v[3] = s.a.vt[buf][1][hb][1][lane];
+        };
+        auto fmv = [&](const u32x4(&v)[4], int hb) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float p0 = bcast(pr0, hb * 8 + e), p1 = bcast(pr1, hb * 8 + e);
+            a[0][0] = __builtin_fmaf(p0, vat(v[0], e), a[0][0]);
+            a[0][1] = __builtin_fmaf(p0, vat(v[1], e), a[0][1]);
+            l[0] = l[0] + p0;
+            a[1][0] = __builtin_fmaf(p1, vat(v[2], e), a[1][0]);
+            a[1][1] = __builtin_fmaf(p1, vat(v[3], e), a[1][1]);
+            l[1] = l[1] + p1;
+          }
+        };
+        ldv(vA, 0);
+#pragma unroll
+        for (int hb = 0; hb < CHUNK / 8; hb += 2) {
+          ldv(vB, hb + 1);
+          fmv(vA, hb);
+          if (hb + 2 < CHUNK / 8) ldv(vA, hb + 2);
+          fmv(vB, hb + 1);
+        }
+      } else {                                            // a partial last chunk: one chunk at a time
+#pragma unroll
+        for (int ci = 0; ci < CPI; ++ci) {
+          const int len = ci == 0 ? len0 : len1;
+          const float pr = ci == 0 ? pr0 : pr1;
+          for (int hb = 0; hb < CHUNK / 8 && hb * 8 < len; ++hb) {
+            const u32x4 w0 = s.a.vt[buf][ci][hb][0][lane], w1 = s.a.vt[buf][ci][hb][1][lane];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              if (hb * 8 + e < len) {
+                const float pt = bcast(pr, hb * 8 + e);
+                a[ci][0] = __builtin_fmaf(pt, vat(w0, e), a[ci][0]);
+                a[ci][1] = __builtin_fmaf(pt, vat(w1, e), a[ci][1]);
+                l[ci] = l[ci] + pt;
+              }
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int ci = 0; ci < CPI; ++ci) {
+        if (ci < nc) {
+          float* part = apart + ((size_t)(g * G + j) * MAX_CHUNKS + c0 + ci) * PART;
+          st_ag(part + lane, a[ci][0]);
+          st_ag(part + lane + 64, a[ci][1]);
+          if (lane == 0) { st_ag(part + HD, ci == 0 ? m0 : m1); st_ag(part + HD + 1, l[ci]); }
+        }
+      }
+    }
+    if (p.trace && threadIdx.x == 0)                      // slot 2 of the attention phase: chunk partials issued
+      *(MK_G uint64_t*)(p.trace + ((size_t)s.phase * p.nwg + blockIdx.x) * 3 + 2) = __builtin_amdgcn_s_memrealtime();
+  }
+}
+
+// P2b (batched): per (sequence b, head h), one wave: the merge of the head's chunk partials in ascending chunk order
+// (M = max m_c, w_c = exp(m_c - M), L = sum w_c l_c, A[d] = sum w_c a_c[d], o = bf16(A / L)), written as the O
+// projection's lane-permuted bf16 row, where dims lane and lane + 64 of a head are adjacent (NH*HD a multiple of 512,
+// HD = 128): one 4-byte store per lane.  The waves of the grid take the merges in turn across the workgroups.
+template <int B, class S, class Wait>
+__device__ __forceinline__ void phase_attn_merge_b(const Params& p, S& s, Wait wait) {
+  const int NH = p.NH, HD = HDIM, KA = NH * HD;
+  const int lane = lane_id(), wave = wave_u();
+  if (!wait()) return;
+  for (int m = wave * p.nwg + (int)blockIdx.x; m < p.B * NH; m += p.nwg * NWAVE) {
+    const int b = m / NH, h = m - b * NH, nch = p.posb[b] / CHUNK + 1;
+    const float* part = p.apart + ((size_t)b * NH + h) * MAX_CHUNKS * PART;
+    float* wl = s.m.p[wave];
+    // lane cc holds chunks cc and cc + 64's (m, l); the chunk weights go through LDS for the ordered sums.  The
+    // first MB chunks' a[] are loaded together with (m, l) (they do not depend on the maximum): one round trip.
+    constexpr int MB = 18;
+    float av0[MB], av1[MB];
+    auto load_a = [&](int cb) {
+#pragma unroll
+      for (int u = 0; u < MB; ++u) {
+        const int c = min(cb + u, nch - 1);               // past the last chunk: a repeat, never used
+        av0[u] = ld_ag(part + (size_t)c * PART + lane);
+        av1[u] = ld_ag(part + (size_t)c * PART + lane + 64);
+      }
+    };
+    float mloc = -__builtin_huge_valf(), lloc = 0.0f, mhi = -__builtin_huge_valf(), lhi = 0.0f;
+    if (lane < nch) { mloc = ld_ag(part + (size_t)lane * PART + HD); lloc = ld_ag(part + (size_t)lane * PART + HD + 1); }
+    if (lane + 64 < nch) {
+      mhi = ld_ag(part + (size_t)(lane + 64) * PART + HD);
+      lhi = ld_ag(part + (size_t)(lane + 64) * PART + HD + 1);
+    }
+    load_a(0);
+    const float M = wave_max(fmaxf(mloc, mhi));
+    wl[lane] = lane < nch ? expf_mk(mloc - M) : 0.0f;
+    wl[64 + lane] = lane + 64 < nch ? expf_mk(mhi - M) : 0.0f;
+    wl[MAX_CHUNKS + lane] = lloc;
+    wl[MAX_CHUNKS + 64 + lane] = lhi;
+    float Ls = 0.0f, A0 = 0.0f, A1 = 0.0f;
+    for (int cb = 0; cb < nch; cb += MB) {
+      if (cb > 0) load_a(cb);
+#pragma unroll
+      for (int u = 0; u < MB; ++u)
+        if (cb + u < nch) {
+          const float wc = wl[cb + u];
+          Ls = __builtin_fmaf(wc, wl[MAX_CHUNKS + cb + u], Ls);
+          A0 = __builtin_fmaf(wc, av0[u], A0);
+          A1 = __builtin_fmaf(wc, av1[u], A1);
+        }
+    }
+    const int st = perm_stored(h * HD + lane, KA);
+    st_ag_u32((uint32_t*)(p.o16 + (size_t)b * KA + st), (uint32_t)f2bf(A0 / Ls) | ((uint32_t)f2bf(A1 / Ls) << 16));
+  }
 }
 
 // P3: O projection + residual per sequence (ref_numpy.py:130)
@@ -731,7 +1026,10 @@ __device__ __forceinline__ void fused_body_b(const Params& p) {
     phase_qkv_b<RowOf<FP8, H>, B>(p, layer, s, wait);
     if (s.abort) return;
     grid_arrive(p, k, s);
-    phase_attn<B>(p, layer, s, wait);
+    phase_attn_b<B>(p, layer, s, wait);
+    if (s.abort) return;
+    grid_arrive(p, k, s);
+    phase_attn_merge_b<B>(p, s, wait);
     if (s.abort) return;
     grid_arrive(p, k, s);
     phase_oproj_b<RowOf<FP8, KA>, B>(p, layer, s, wait);

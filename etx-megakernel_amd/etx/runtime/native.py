@@ -219,10 +219,10 @@ def phase_names(cfg: ModelConfig) -> list[list[str]]:
         att = ["qkv", "absorb", "attn", "wuv", "oproj"]
         layers = [att + (["gateup", "down"] if l < cfg.first_dense else ["router_shared", "expert_up", "expert_down"])
                   for l in range(cfg.L)]
-    elif cfg.moe:
-        layers = [["qkv", "attn", "oproj", "router", "expert_up", "expert_down"] for _ in range(cfg.L)]
-    else:
-        layers = [["qkv", "attn", "oproj", "gateup", "down"] for _ in range(cfg.L)]
+    else:                                   # batched kernels merge the attention partials in a phase of its own
+        att = ["qkv", "attn"] + (["attn_merge"] if cfg.batch > 1 else []) + ["oproj"]
+        mlp = ["router", "expert_up", "expert_down"] if cfg.moe else ["gateup", "down"]
+        layers = [att + mlp for _ in range(cfg.L)]
     return layers + [["head"]]
 
 

@@ -135,6 +135,12 @@ def test_qwen3_30b_a3b_batch16_two_layers(gpu):
     run_contexts(cfg, ctx, n_steps=2, pool=False)
 
 
+def test_qwen3_8b_batch4_two_layers(gpu):
+    """Qwen3-8B shapes at batch 4 (two dense layers, H 4096, 12288-long down rows in the long-row batched GEMV)."""
+    cfg = configs.with_layers(configs.QWEN3_8B, 2, batch=4)
+    run_contexts(cfg, [300, 64, 1000, 7], n_steps=3, shuffle=True)
+
+
 @pytest.mark.timeout(900)
 def test_qwen3_30b_a3b_batch4_full_depth(gpu):
     """48 layers at batch 4 with per-sequence contexts: 8 greedy steps of every sequence identical to the oracle,
