@@ -234,7 +234,8 @@ int check_config(const etxmk_config* c) {
   if (c->H > MAX_H || !k_in(c->H, {MK_K_HIDDEN})) return fail(ETXMK_EINVAL, "hidden size %d unsupported", c->H);
   if (!k_in(c->NH * c->HD, {MK_K_ATTN})) return fail(ETXMK_EINVAL, "NH*HD %d unsupported", c->NH * c->HD);
   if (c->batch < 1 || c->batch > MAX_B) return fail(ETXMK_EINVAL, "batch %d outside 1..%d", c->batch, MAX_B);
-  if (c->block_size <= 0 || CHUNK % c->block_size) return fail(ETXMK_EINVAL, "block size %d must divide %d", c->block_size, CHUNK);
+  if (c->block_size != 16)                 // the attention tiles copy whole 16-position blocks (etx/importer/spec.py:274-281)
+    return fail(ETXMK_EINVAL, "block size %d unsupported (the paged KV cache is built for 16-position blocks)", c->block_size);
   if (c->max_ctx <= 0 || c->max_ctx > MAX_CTX) return fail(ETXMK_EINVAL, "max_ctx %d outside 1..%d", c->max_ctx, MAX_CTX);
   if (c->moe) {
     if (c->E <= 0 || c->E > MAX_E || c->E % 4 || c->TOPK <= 0 || c->TOPK > MAX_TOPK || c->TOPK > c->E)

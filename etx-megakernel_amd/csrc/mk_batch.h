@@ -405,11 +405,27 @@ __device__ __forceinline__ void phase_attn_b(const Params& p, int layer, S& s, W
   // into the tiles from the QKV rows, not read from the cache
   auto first_new = [&](int pos) { return p.pf ? p.posb[0] : pos; };
   // wave w copies K dim-groups 2w, 2w+1 (lane = position) and the V position-group w (lane = dim, both halves) of
-  // every chunk of the item, HBM -> LDS buffer `buf` (global_load_lds, 16 bytes per lane)
-  auto load_kv = [&](int item, int buf) {
+  // every chunk of the item, HBM -> LDS buffer `buf` (global_load_lds, 16 bytes per lane).  The block-table entries
+  // they need are read one item ahead (kv_blocks), so issuing the copies waits on nothing.
+  struct KvBlocks {
+    int k[CPI], v[CPI];                                   // block of the lane's K position, of the wave's V group
+  };
+  auto kv_blocks = [&](int item) {
+    const AttnItem it = attn_item<B, CPI>(p, item);
+    const int n = it.pos + 1, fp = first_new(it.pos);
+    const int32_t* btab = p.btab + (size_t)it.b * p.nbps;
+    KvBlocks r;
+#pragma unroll
+    for (int ci = 0; ci < CPI; ++ci) {
+      const int t0 = (it.cp * CPI + ci) * CHUNK, t = t0 + lane, tb = t0 + wave * 8;
+      r.k[ci] = t < n && t < fp ? ld_i(btab + t / BS) : 0;
+      r.v[ci] = tb < n && tb < fp ? ld_i(btab + tb / BS) : 0;
+    }
+    return r;
+  };
+  auto load_kv = [&](int item, int buf, const KvBlocks& kb) {
     const AttnItem it = attn_item<B, CPI>(p, item);
     const int g = it.g, pos = it.pos, n = pos + 1, nch = (n + CHUNK - 1) / CHUNK, fp = first_new(pos);
-    const int32_t* btab = p.btab + (size_t)it.b * p.nbps;
 #pragma unroll
     for (int ci = 0; ci < CPI; ++ci) {
       const int c = it.cp * CPI + ci;
@@ -417,8 +433,7 @@ __device__ __forceinline__ void phase_attn_b(const Params& p, int layer, S& s, W
         const int t0 = c * CHUNK, len = min(CHUNK, n - t0);
         const int t = t0 + lane;
         if (lane < len && t < fp) {
-          const int blk = ld_i(btab + t / BS), off = t % BS;
-          const uint16_t* kp = Lw.kc + (((size_t)blk * NKV + g) * (HD / 8)) * BS * 8 + off * 8;
+          const uint16_t* kp = Lw.kc + (((size_t)kb.k[ci] * NKV + g) * (HD / 8)) * BS * 8 + (t % BS) * 8;
 #pragma unroll
           for (int jj = 2 * wave; jj < 2 * wave + 2; ++jj)
             __builtin_amdgcn_global_load_lds((const MK_G void*)(kp + (size_t)jj * BS * 8),
@@ -426,8 +441,7 @@ __device__ __forceinline__ void phase_attn_b(const Params& p, int layer, S& s, W
         }
         const int tb = t0 + wave * 8;                     // 8 positions per 16-byte load
         if (tb < t0 + len && tb < fp) {
-          const int blk = ld_i(btab + tb / BS), off = tb % BS;
-          const uint16_t* vp = Lw.vc + ((size_t)blk * NKV + g) * HD * BS + off;
+          const uint16_t* vp = Lw.vc + ((size_t)kb.v[ci] * NKV + g) * HD * BS + tb % BS;
           __builtin_amdgcn_global_load_lds((const MK_G void*)(vp + (size_t)lane * BS),
                                            (__attribute__((address_space(3))) void*)&s.a.vt[buf][ci][wave][0][0], 16, 0, 0);
           __builtin_amdgcn_global_load_lds((const MK_G void*)(vp + (size_t)(lane + 64) * BS),
@@ -438,7 +452,7 @@ __device__ __forceinline__ void phase_attn_b(const Params& p, int layer, S& s, W
   };
   const float qn0 = bf2f(ld_u16(Lw.qn + lane)), qn1 = bf2f(ld_u16(Lw.qn + lane + 64));
   const float kn0 = bf2f(ld_u16(Lw.kn + lane)), kn1 = bf2f(ld_u16(Lw.kn + lane + 64));
-  if ((int)blockIdx.x < nitems) load_kv(blockIdx.x, 0);
+  if ((int)blockIdx.x < nitems) load_kv(blockIdx.x, 0, kv_blocks(blockIdx.x));
   if (!wait()) return;
   auto bcast = [](float v, int l) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l)); };
   int k = 0;
@@ -453,6 +467,9 @@ __device__ __forceinline__ void phase_attn_b(const Params& p, int layer, S& s, W
     // this launch's positions in the item's chunks: [qlo, qhi] (decode: pos alone, in the item of the last chunk)
     const int qlo = max(first_new(pos), c0 * CHUNK), qhi = min(pos, (c0 + nc) * CHUNK - 1);
     const float rc = ld_f(p.rope_cos + (size_t)pos * (HD / 2) + lane), rs = ld_f(p.rope_sin + (size_t)pos * (HD / 2) + lane);
+    const bool more = item + p.nwg < nitems;
+    KvBlocks nkb;                                         // the next item's blocks, read with this item's inputs
+    if (more) nkb = kv_blocks(item + p.nwg);
     // wave j: head g*G + j, its roped q in registers (dims lane, lane + 64), broadcast with v_readlane below
     const int j = wave;
     float q0 = 0.0f, q1 = 0.0f;
@@ -509,7 +526,7 @@ __device__ __forceinline__ void phase_attn_b(const Params& p, int layer, S& s, W
       }
     }
     __syncthreads();
-    if (item + p.nwg < nitems) load_kv(item + p.nwg, buf ^ 1);
+    if (more) load_kv(item + p.nwg, buf ^ 1, nkb);
     if (j < G) {
       // scores (:126), lane = position: both chunks' chains over ascending d, each broadcast q value feeding both;
       // the K reads run a block of GB dim groups ahead.  With one chunk the second chain reads stale LDS, unused.

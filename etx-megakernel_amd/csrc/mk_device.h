@@ -883,10 +883,16 @@ __device__ __forceinline__ void phase_attn(const Params& p, int layer, S& s, Wai
     // p_t = exp(s_t - m) in lane t.  Then V (:127-128): lanes = dims (lane, lane + 64); a = sum_t p_t v_t[d] and
     // l = sum_t p_t, ascending t, from one 16-byte read per dim half (8 positions of this lane's dim).  Full chunks
     // take the loop without position tests; only a head's last chunk is partial.
+    // (the V reads run one 8-position group ahead of the chains)
     auto pv = [&](int ci, int len, float pr, auto full, float& a0, float& a1, float& l) {
+      u32x4 wn0 = s.a.vt[ci][0][0][lane], wn1 = s.a.vt[ci][0][1][lane];
 #pragma unroll
       for (int hb = 0; hb < CHUNK / 8; ++hb) {
-        const u32x4 w0 = s.a.vt[ci][hb][0][lane], w1 = s.a.vt[ci][hb][1][lane];
+        const u32x4 w0 = wn0, w1 = wn1;
+        if (hb + 1 < CHUNK / 8 && (decltype(full)::value || (hb + 1) * 8 < len)) {
+          wn0 = s.a.vt[ci][hb + 1][0][lane];
+          wn1 = s.a.vt[ci][hb + 1][1][lane];
+        }
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           if (decltype(full)::value || hb * 8 + e < len) {
@@ -906,10 +912,15 @@ __device__ __forceinline__ void phase_attn(const Params& p, int layer, S& s, Wai
         if (ci < nc) {
           const int c = c0 + ci, len = min(CHUNK, n - c * CHUNK);
           const bool valid = lane < len;
+          // the K reads run two 8-dim groups ahead of the chain
           float acc = 0.0f;
+          u32x4 kr[HDIM / 8];
+          kr[0] = s.a.kt[ci][0][lane];
+          kr[1] = s.a.kt[ci][1][lane];
 #pragma unroll
-          for (int jj = 0; jj < HD / 8; ++jj) {
-            const u32x4 kw = s.a.kt[ci][jj][lane];
+          for (int jj = 0; jj < HDIM / 8; ++jj) {
+            if (jj + 2 < HDIM / 8) kr[jj + 2] = s.a.kt[ci][jj + 2][lane];
+            const u32x4 kw = kr[jj];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
               const int d = 8 * jj + 2 * e;

@@ -28,7 +28,7 @@ def test_sizes_of_real_configurations():
     assert 15.0e9 < s8["weights"] < 16.5e9
 
 
-@pytest.mark.parametrize("bad", [dict(HD=64), dict(H=3000), dict(batch=0), dict(batch=17), dict(block_size=48),
+@pytest.mark.parametrize("bad", [dict(HD=64), dict(H=3000), dict(batch=0), dict(batch=17), dict(block_size=48), dict(block_size=8), dict(block_size=32),
                                  dict(max_ctx=10**6), dict(TOPK=9), dict(E=0), dict(NKV=3), dict(prefill=17),
                                  dict(prefill=-1)])
 def test_config_refused(bad):
