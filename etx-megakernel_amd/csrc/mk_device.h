@@ -747,23 +747,23 @@ __device__ __forceinline__ AttnItem attn_item(const Params& p, int item) {
   return AttnItem{b, r % p.NKV, r / p.NKV, B > 1 ? p.posb[b] : p.pos};
 }
 
+// the single-sequence phase (the batched kernels run phase_attn_b and phase_attn_merge_b)
 template <int B, class S, class Wait>
 __device__ __forceinline__ void phase_attn(const Params& p, int layer, S& s, Wait wait) {
+  static_assert(B == 1, "single-sequence attention");
   constexpr int CPI = decltype(s.a)::cpi;
   const int NKV = p.NKV, NH = p.NH, G = NH / NKV, HD = HDIM, BS = p.BS;
   const int NQKV = (NH + 2 * NKV) * HD;
-  const int nitems = B > 1 ? p.ibase[p.B] : NKV * ((p.pos / CHUNK + CPI) / CPI);
+  const int nitems = NKV * ((p.pos / CHUNK + CPI) / CPI);
   const LayerW Lw = layer_w(p, layer);
   const int lane = lane_id(), wave = wave_u();
   // The chunks' cached K and V go straight from HBM into LDS tiles (global_load_lds, 16 bytes per lane); they do
   // not depend on this step, so the first item's copies are issued before the wait.  Wave w copies K dim-groups
   // 2w, 2w+1 (lane = position) and the V position-group w (lane = dim, both halves) of every chunk of the item.
-  // Positions from first_new(pos) on are this launch's (the row's own, and in prefill the earlier rows'): they are
-  // not read from the cache but patched into the tiles from the QKV rows.
-  auto first_new = [&](int pos) { return B > 1 && p.pf ? p.posb[0] : pos; };
+  // The current position is not read from the cache: it is patched into the tiles from the QKV row.
   auto load_kv = [&](int item) {
     const AttnItem it = attn_item<B, CPI>(p, item);
-    const int g = it.g, pos = it.pos, n = pos + 1, nch = (n + CHUNK - 1) / CHUNK, fp = first_new(pos);
+    const int g = it.g, pos = it.pos, n = pos + 1, nch = (n + CHUNK - 1) / CHUNK, fp = pos;
     const int32_t* btab = p.btab + (size_t)it.b * p.nbps;
 #pragma unroll
     for (int ci = 0; ci < CPI; ++ci) {
@@ -791,9 +791,8 @@ __device__ __forceinline__ void phase_attn(const Params& p, int layer, S& s, Wai
       }
     }
   };
-  // RoPE factors of the position (ref_numpy.py:76-81 tables), reloaded when an item's sequence has another
-  int rpos = (int)blockIdx.x < nitems ? attn_item<B, CPI>(p, blockIdx.x).pos : 0;
-  float rc = ld_f(p.rope_cos + (size_t)rpos * (HD / 2) + lane), rs = ld_f(p.rope_sin + (size_t)rpos * (HD / 2) + lane);
+  // RoPE factors of the position (ref_numpy.py:76-81 tables)
+  const float rc = ld_f(p.rope_cos + (size_t)p.pos * (HD / 2) + lane), rs = ld_f(p.rope_sin + (size_t)p.pos * (HD / 2) + lane);
   const float qn0 = bf2f(ld_u16(Lw.qn + lane)), qn1 = bf2f(ld_u16(Lw.qn + lane + 64));
   const float kn0 = bf2f(ld_u16(Lw.kn + lane)), kn1 = bf2f(ld_u16(Lw.kn + lane + 64));
   if ((int)blockIdx.x < nitems) load_kv(blockIdx.x);
@@ -807,16 +806,9 @@ __device__ __forceinline__ void phase_attn(const Params& p, int layer, S& s, Wai
     float* apart = p.apart + (size_t)it.b * NH * MAX_CHUNKS * PART;
     uint32_t* acnt = p.acnt + (size_t)it.b * NKV * 64;
     float* o = p.o + (size_t)it.b * NH * HD;
-    // this launch's positions in the item's chunks: [qlo, qhi] (decode: pos alone, in the item of the last chunk)
-    const int qlo = max(first_new(pos), c0 * CHUNK), qhi = min(pos, (c0 + nc) * CHUNK - 1);
+    // the current position, when it lies in the item's chunks: [qlo, qhi] is it or empty
+    const int qlo = max(pos, c0 * CHUNK), qhi = min(pos, (c0 + nc) * CHUNK - 1);
     if (item != (int)blockIdx.x) load_kv(item);
-    if constexpr (B > 1) {
-      if (pos != rpos) {
-        rpos = pos;
-        rc = ld_f(p.rope_cos + (size_t)pos * (HD / 2) + lane);
-        rs = ld_f(p.rope_sin + (size_t)pos * (HD / 2) + lane);
-      }
-    }
     // wave j computes head g*G + j (G <= 8, checked by the host): its roped q stays in registers, dims lane (q0)
     // and lane + 64 (q1) (ref_numpy.py:116-120); the score and P.V loops take each dim's or position's value from its
     // lane with v_readlane (wave-uniform operands, no LDS traffic for q or p)
@@ -829,9 +821,8 @@ __device__ __forceinline__ void phase_attn(const Params& p, int layer, S& s, Wai
       q0 = bfr(bfr(a0 * rc) + bfr(-a1 * rs));
       q1 = bfr(bfr(a1 * rc) + bfr(a0 * rs));
     }
-    // k (normed, roped at its position) and v of position q come from the QKV row of that position, row
-    // it.b - (pos - q); wave NWAVE-1-w takes positions qlo + w and qlo + w + NWAVE (a launch has <= 2*NWAVE rows)
-    constexpr int PQ = B > 1 ? 2 : 1;
+    // k (normed and roped) and v of the current position come from its QKV row; wave NWAVE-1 takes it
+    constexpr int PQ = 1;
     float kn[PQ][2], vn[PQ][2];
 #pragma unroll
     for (int u = 0; u < PQ; ++u) {
@@ -991,17 +982,8 @@ __device__ __forceinline__ void phase_attn(const Params& p, int layer, S& s, Wai
               A1 = __builtin_fmaf(wc, av1[u], A1);
             }
         }
-        if constexpr (B > 1) {
-          // batched: o goes out as the O projection's lane-permuted bf16 row, where dims lane and lane + 64 of a
-          // head are adjacent (NH*HD a multiple of 512, HD = 128), so one 4-byte store per lane
-          const int KA = NH * HD;
-          const int st = perm_stored((g * G + j) * HD + lane, KA);
-          st_ag_u32((uint32_t*)(p.o16 + (size_t)it.b * KA + st),
-                    (uint32_t)f2bf(A0 / Ls) | ((uint32_t)f2bf(A1 / Ls) << 16));
-        } else {
-          st_ag(o + (size_t)(g * G + j) * HD + lane, bfr(A0 / Ls));
-          st_ag(o + (size_t)(g * G + j) * HD + lane + 64, bfr(A1 / Ls));
-        }
+        st_ag(o + (size_t)(g * G + j) * HD + lane, bfr(A0 / Ls));
+        st_ag(o + (size_t)(g * G + j) * HD + lane + 64, bfr(A1 / Ls));
       }
       if (threadIdx.x == 0) __hip_atomic_store(acnt + 64 * g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
