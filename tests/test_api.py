@@ -74,6 +74,9 @@ def test_plan_records_kernel_grid_and_phases():
     assert ds["kernel"].startswith("etxmk_ds_b4") and ds["batch_capacity"] == 4
     assert ds["barriers_per_step"] == 7 + 8 * 26 + 1 == sum(len(x) for x in ds["phases"])
     assert ds["phases"][0][-2:] == ["gateup", "down"] and ds["phases"][1][-3:] == ["router_shared", "expert_up", "expert_down"]
+    b16 = api.plan(_wl(configs.with_layers(configs.QWEN3_30B_A3B, 48, batch=16))).record.to_dict()
+    assert b16["barriers_per_step"] == 7 * 48 + 1 == sum(len(x) for x in b16["phases"])   # the merge phase
+    assert b16["phases"][0][:4] == ["qkv", "attn", "attn_merge", "oproj"]
     f8 = api.plan(_wl(configs.with_layers(configs.QWEN3_30B_A3B, 48, batch=16, wdtype=1))).record.to_dict()
     assert f8["kernel"] == "etxmk_fused_fp8_b16_h2048_a4096_moe768_e128" and any("fp8" in d for d in f8["decisions"])
     un = api.plan(_wl(configs.TINY_MOE, fused=False)).record.to_dict()

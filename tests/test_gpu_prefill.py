@@ -175,3 +175,21 @@ def test_tiny_mla_batched_handle_prefill(gpu):
 def test_deepseek_v2_lite_prefill_two_layers(gpu):
     """DeepSeek-V2-Lite shapes (the dense layer 0 and one MoE layer): 4 positions per launch."""
     run_prefill_mla(configs.with_layers(configs.DEEPSEEK_V2_LITE, 2, prefill=4), 26, n_new=4, rows=4)
+
+
+def test_prefill_refusals(gpu):
+    """Rows beyond the handle's prefill rows, positions past max_ctx, a sequence outside the batch and the unfused
+    mode are refused before anything is launched."""
+    cfg = configs.with_layers(configs.TINY_MOE, configs.TINY_MOE.L, prefill=4)
+    dec = N.Decoder(cfg)
+    dec.init_weights(SEED, 0.02)
+    for args, kw, msg in [((0, 5), {}, "prefill positions"), ((0, 0), {}, "prefill positions"),
+                          ((cfg.max_ctx - 2, 4), {}, "outside"), ((0, 2), {"seq": 1}, "sequence")]:
+        with pytest.raises(N.EtxmkError, match=msg):
+            dec.prefill(*args, **kw)
+    dec.close()
+    unf = N.Decoder(cfg, fused=False)
+    with pytest.raises(N.EtxmkError, match="persistent kernel"):
+        unf.prefill(0, 2)
+    assert unf.prefill_rows == 0
+    unf.close()
