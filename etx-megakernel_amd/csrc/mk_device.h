@@ -127,6 +127,7 @@ struct Smem {
   int32_t ids[NWAVE][MAX_TOPK];         // routing, one private copy per wave (no workgroup barrier needed)
   float wts[NWAVE][MAX_TOPK];
   int32_t order[NWAVE][MAX_TOPK];
+  float lg[MAX_E];                      // the router logits, read once per workgroup
   int32_t abort;
   int32_t last;
   int32_t phase;                        // arrivals so far (the current phase index), for trace stamps
@@ -1137,10 +1138,23 @@ __device__ __forceinline__ void route_topk_into(const Params& p, const float* lo
   route_load<EC>(p, logits, r);
   route_topk_from<EC>(p, r, ids_out, wts_out, order_out);
 }
+// every wave routes on its own from the logits, which one wave reads (agent-scope) into LDS for the workgroup:
+// the grid's reads of the one logits row are one per workgroup, not one per wave
 template <int EC = 0>
 __device__ __forceinline__ void route_topk(const Params& p, Smem& s) {
-  const int wave = wave_u();
-  route_topk_into<EC>(p, p.logits, s.ids[wave], s.wts[wave], s.order[wave]);
+  const int wave = wave_u(), lane = lane_id(), E = EC > 0 ? EC : p.E;
+  if (wave == 0) {
+    RouteLogits<EC> r;
+    route_load<EC>(p, p.logits, r);
+#pragma unroll
+    for (int w = 0; w < RouteLogits<EC>::NW; ++w)
+      if (lane + 64 * w < E) s.lg[lane + 64 * w] = r.v[w];
+  }
+  __syncthreads();
+  RouteLogits<EC> r;
+#pragma unroll
+  for (int w = 0; w < RouteLogits<EC>::NW; ++w) r.v[w] = lane + 64 * w < E ? s.lg[lane + 64 * w] : -__builtin_huge_valf();
+  route_topk_from<EC>(p, r, s.ids[wave], s.wts[wave], s.order[wave]);
 }
 
 // P5: experts gate/up + SiLU*up for the top-k slots (ref_numpy.py:142-145).  The normed input depends only on x
