@@ -32,6 +32,8 @@ for _p in (str(ROOT), str(ROOT / "etx-megakernel_amd")):
 METRIC = "decode ms/token at batch 1, Qwen3-30B-A3B shape; achieved HBM GB/s vs peak"
 HBM_PEAK_GBPS = 8000.0
 REFERENCE_MI300X_MS = 4.087415          # docs/qwen/QWEN-BATCH-BASELINE-2026-10-18.md:17 (MI300X, not comparable hardware)
+METRIC_8B = "decode ms/token at batch 1, Qwen3-8B shape; achieved HBM GB/s vs peak"
+REFERENCE_MI300X_8B_TILES_MS = 10.07    # README.md:140-146: the generic hand-written tiles at context 1024 (MI300X)
 
 
 def log(*a):
@@ -295,8 +297,9 @@ def main():
     ap.add_argument("--ctx-hi", type=int, default=0,
                     help="batched contexts' upper bound (default 4096; 2048 for deepseek-v2-lite, BASELINE configs[3])")
     ap.add_argument("--fp8", action="store_true", help="fp8 e4m3 weights with per-row scales (BASELINE.json configs[4])")
-    ap.add_argument("--model", default="qwen3-30b-a3b", choices=["qwen3-30b-a3b", "deepseek-v2-lite"],
-                    help="deepseek-v2-lite: the batched multi-head latent attention step (BASELINE.json configs[3])")
+    ap.add_argument("--model", default="qwen3-30b-a3b", choices=["qwen3-30b-a3b", "qwen3-8b", "deepseek-v2-lite"],
+                    help="qwen3-8b: the dense model of BASELINE.json configs[1] at batch 1; deepseek-v2-lite: the "
+                         "batched multi-head latent attention step (configs[3])")
     a = ap.parse_args()
     if a.ctx_hi <= 0:
         a.ctx_hi = 2048 if a.model == "deepseek-v2-lite" else 4096
@@ -304,6 +307,8 @@ def main():
         print(f"bench.py: this build runs on exactly one GPU (asked for {a.gpus}); multi-GPU sharding is a design "
               f"note only", file=sys.stderr)
         sys.exit(2)
+    if a.model == "qwen3-8b" and a.batch > 1:
+        raise SystemExit("the Qwen3-8B workload (BASELINE.json configs[1]) is batch 1")
     if a.batch > 1 or a.model == "deepseek-v2-lite":
         return main_batch(a)
 
@@ -312,10 +317,15 @@ def main():
     from etx.runtime import native as N
     from etx.models import configs
 
-    cfg = configs.QWEN3_30B_A3B
+    dense = a.model == "qwen3-8b"
+    cfg = configs.QWEN3_8B if dense else configs.QWEN3_30B_A3B
     if a.fp8:
+        if dense:
+            raise SystemExit("fp8 weights are built for the Qwen3-30B-A3B shape (BASELINE.json configs[4])")
         cfg = configs.with_layers(cfg, cfg.L, wdtype=N.W_FP8)
     rows = a.prefill_rows if a.prefill_rows > 1 and not a.unfused else 0
+    if dense:
+        rows = min(rows, 4)                               # the Qwen3-8B batched kernel holds 4 rows
     if rows:
         cfg = configs.with_layers(cfg, cfg.L, prefill=rows)
     if a.ctx + a.warmup + a.steps + 1 > cfg.max_ctx:
@@ -408,7 +418,8 @@ def main():
             np.save(a.trace_out, t)
         phase_us = trace_summary(t, cfg)
     out = {
-        "metric": METRIC, "value": round(ms, 4), "unit": "ms/token", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "metric": METRIC_8B if dense else METRIC, "value": round(ms, 4), "unit": "ms/token", "n_gpus": 1,
+        "steps": a.steps, "warmup": a.warmup,
         "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
         "dtype": "fp8-e4m3 weights x bf16 activations, fp32 accumulation" if a.fp8 else "bf16",
         "data": "synthetic: seeded random-init " + ("fp8 (quantised from bf16 N(0,0.02))" if a.fp8 else "bf16")
@@ -416,13 +427,14 @@ def main():
                 if a.kv_fill else "prompt of seeded uniform token ids, prefilled " +
                 (f"{rows} positions per launch (bit-identical to token by token)" if rows else "token by token")),
         "config": {"workload": f"{cfg.name} decode, batch 1, context {a.ctx} (+{a.warmup} warmup), greedy "
-                               f"(BASELINE.json configs[2])",
+                               f"(BASELINE.json configs[{1 if dense else 2}])",
                    "batch": 1, "context": a.ctx, "layers": cfg.L, "experts": cfg.E, "top_k": cfg.TOPK,
                    "vocab": cfg.V, "mode": "unfused" if a.unfused else "fused megakernel",
                    "workgroups": a.workgroups or "one per CU", "seed": a.seed},
         "tokens_per_s": round(1e3 / ms, 2), "host_wall_ms_per_token": round(wall / a.steps, 4),
         "bytes_per_token": b["total"], "achieved_GBps": round(gbps, 1),
-        "reference_mi300x_ms_per_token": REFERENCE_MI300X_MS,
+        ("reference_mi300x_generic_tiles_ms_per_token" if dense else "reference_mi300x_ms_per_token"):
+            REFERENCE_MI300X_8B_TILES_MS if dense else REFERENCE_MI300X_MS,
         "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
                      "kernel": "etxmk_fused" if not a.unfused else "etxmk_phase (all phases)"},
@@ -435,7 +447,7 @@ def main():
     # HBM bytes per launch from the committed counter passes (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of this
     # workload, each scaled by the same counter's reading for a 1 GiB copy)
     tf = ROOT / "profiles" / "etxmk_fused_qwen3-30b-a3b_b1_ctx1024_hbm_traffic.json"
-    if tf.exists() and not a.unfused:
+    if tf.exists() and not a.unfused and not dense and not a.fp8:
         t = json.loads(tf.read_text())
         out["roofline"]["traffic"] = t["traffic_bytes_per_launch"]
         out["roofline"]["traffic_source"] = f"profiles/{tf.name} (FETCH x{t['fetch_factor']}, WRITE x{t['write_factor']})"
