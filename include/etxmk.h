@@ -162,8 +162,10 @@ int etxmk_step_batch(etxmk_handle* h, const int32_t* positions, int32_t write_ne
  * computes what etxmk_step computes at its position, bit for bit: its K/V row goes to the cache, its greedy token
  * to out_tokens[pos], and, when write_next != 0, the last row's also to tokens[pos0 + n].  The rows attend to the
  * cache below pos0 and to the launch's own K/V rows (taken from their QKV outputs inside the launch).  Other
- * sequences are untouched.  Reference: the prompt loop of examples/llm/host.hip:203-213 (one decode step per
- * prompt token), which this replaces by ceil(prompt / n) launches. */
+ * sequences are untouched.  Prefill launches write no per-layer dumps (etxmk_set_dump buffers hold batch rows) and
+ * no trace stamps (the stamp buffer is sized for the handle's step kernel).  Reference: the prompt loop of
+ * examples/llm/host.hip:203-213 (one decode step per prompt token), which this replaces by ceil(prompt / n)
+ * launches. */
 int etxmk_prefill(etxmk_handle* h, int32_t seq, int32_t pos0, int32_t n, int32_t write_next, void* stream);
 
 /* Layers [l0, l1) only, on the residual already in the workspace (etxmk_set_residual), no embedding and
