@@ -883,10 +883,14 @@ static int launch(etxmk_handle* h, const int32_t* posv, int pos, int write_next,
   p.pos = batched ? 0 : pos; p.write_next = write_next; p.l0 = l0; p.l1 = l1; p.do_embed = embed; p.do_head = head;
   p.nwg = h->nwg;
   p.spin_ticks = 200000000ull;            // 2 s of the 100 MHz s_memrealtime clock
-  {                                        // QKV rows staged in LDS a layer ahead when a workgroup's share fits
+  {  // a workgroup's QKV rows: staged in LDS a layer ahead as far as the stage holds them, the rest (rows of 4096
+     // only, up to two per wave) loaded into registers before the QKV phase's wait
     const int rows = nqkv_of(c), R = (rows + h->nwg - 1) / h->nwg;
-    p.qkv_rows = (!batched && h->fused && c.wdtype == ETXMK_W_BF16 && c.H % 512 == 0 &&
-                  (uint64_t)R * c.H * 2 <= (uint64_t)QKVW_BYTES) ? R : 0;
+    const int S = R < (int)(QKVW_BYTES / (2 * c.H)) ? R : (int)(QKVW_BYTES / (2 * c.H));
+    const int regs = c.H >= 4096 ? 2 * NWAVE : 0;
+    const bool ok = !batched && h->fused && c.wdtype == ETXMK_W_BF16 && c.H % 512 == 0 && R - S <= regs;
+    p.qkv_rows = ok ? R : 0;
+    p.qkv_lds_rows = ok ? S : 0;
   }
   p.B = nrows;
   p.nbps = nbps_of(&c);

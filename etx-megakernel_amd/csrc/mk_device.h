@@ -79,7 +79,8 @@ struct Params {
   float* dump_logits;
   uint64_t* trace;                      // optional: [phase][workgroup][wait done, arrive, loads issued] stamps
   int pos, write_next, l0, l1, do_embed, do_head;
-  int qkv_rows;                         // > 0: QKV rows per workgroup staged in LDS one layer ahead (fused mode)
+  int qkv_rows;                         // > 0: QKV rows per workgroup, the first qkv_lds_rows of them staged in LDS
+  int qkv_lds_rows;                     // one layer ahead, the rest loaded before the QKV phase's wait (fused mode)
   uint32_t bar_base;
   int nwg;
   uint64_t spin_ticks;
@@ -640,17 +641,18 @@ __device__ __forceinline__ int token_of(const Params& p) {
   return (t >= 0 && t < p.V) ? t : 0;
 }
 
-// The QKV rows of layer `layer` that this workgroup computes ([b*R, b*R + R), R = p.qkv_rows), HBM -> LDS as
-// stored (lane-permuted), issued from the O projection of the layer before: that stream overlaps the attention,
-// router and expert phases, whose memory traffic leaves room, and the QKV phase then reads its weights from LDS.
-// Wave w copies rows w, w + 8, ...; each wave reads back only the rows it copied, after its own wait.
+// The QKV rows of layer `layer` that this workgroup computes are [b*R, b*R + R), R = p.qkv_rows; the first
+// S = p.qkv_lds_rows of them go HBM -> LDS as stored (lane-permuted), issued from the O projection of the layer
+// before: that stream overlaps the attention, router and MLP phases, whose memory traffic leaves room, and the QKV
+// phase then reads them from LDS.  Wave w copies rows w, w + 8, ...; each wave reads back only the rows it copied,
+// after its own wait.
 template <int KK>
 __device__ __forceinline__ void qkv_to_lds(const Params& p, int layer, Smem& s) {
   static_assert(KK % 512 == 0, "LDS-staged QKV rows are whole 512-element blocks");
   const LayerW Lw = layer_w(p, layer);
-  const int rows = p.nqkv, R = p.qkv_rows, r0 = (int)blockIdx.x * R;
+  const int rows = p.nqkv, R = p.qkv_rows, S = p.qkv_lds_rows, r0 = (int)blockIdx.x * R;
   const int lane = lane_id();
-  for (int i = wave_u(); i < R && r0 + i < rows; i += NWAVE) {
+  for (int i = wave_u(); i < S && r0 + i < rows; i += NWAVE) {
     const uint16_t* src = (const uint16_t*)Lw.wqkv + (size_t)(r0 + i) * KK + 8 * lane;
 #pragma unroll
     for (int b = 0; b < KK / 512; ++b)
@@ -659,19 +661,33 @@ __device__ __forceinline__ void qkv_to_lds(const Params& p, int layer, Smem& s) 
   }
 }
 
-// P1 with the weights in LDS (staged by qkv_to_lds one layer ahead): the same norm prologue, the same dot order.
+// rows per wave of a workgroup's QKV share beyond the LDS-staged ones (loaded into registers before the wait):
+// none for rows of up to 2048 (a share of Qwen3-30B-A3B fits the stage), two for longer rows
+template <int KK>
+constexpr int qkv_reg_rows() { return KK >= 4096 ? 2 : 0; }
+
+// P1 with the weights in LDS (staged by qkv_to_lds one layer ahead) and, past the stage, in registers (loaded
+// before the wait): the same norm prologue, the same dot order.
 template <int KK, class Wait>
 __device__ __forceinline__ void phase_qkv_lds(const Params& p, int layer, Smem& s, Wait wait) {
+  using WR = Bf16Row<KK>;
+  constexpr int RR = qkv_reg_rows<KK>();
   const LayerW Lw = layer_w(p, layer);
-  const int rows = p.nqkv, R = p.qkv_rows, r0 = (int)blockIdx.x * R;
-  const int lane = lane_id();
+  const int rows = p.nqkv, R = p.qkv_rows, S = p.qkv_lds_rows, r0 = (int)blockIdx.x * R;
+  const int lane = lane_id(), wave = wave_u();
   float* qkv = p.qkv;
+  typename WR::Regs Rr[RR > 0 ? RR : 1];
+#pragma unroll
+  for (int u = 0; u < RR; ++u) {                          // rows S + wave + 8u
+    const int i = S + wave + u * NWAVE;
+    if (i < R && r0 + i < rows) WR::load(Rr[u], mrow<WR>(Lw.wqkv, (size_t)(r0 + i)), lane);
+  }
   if (!wait()) return;
   build_norm_x<KK>(p, p.x, nullptr, Lw.ln1, s);
   if (blockIdx.x == 0 && p.dump_x && layer > p.l0)
     for (int i = threadIdx.x; i < KK; i += NT) st_f(p.dump_x + (size_t)(layer - 1) * KK + i, s.g.xf[i]);
   __builtin_amdgcn_s_waitcnt(0);                          // this wave's rows have landed in LDS (long since)
-  for (int i = wave_u(); i < R && r0 + i < rows; i += NWAVE) {
+  for (int i = wave; i < S && r0 + i < rows; i += NWAVE) {
     float acc = 0.0f;
 #pragma unroll
     for (int b = 0; b < KK / 512; ++b) {
@@ -685,6 +701,14 @@ __device__ __forceinline__ void phase_qkv_lds(const Params& p, int layer, Smem& 
     }
     acc = wave_sum(acc);
     if (lane == 0) st_ag(qkv + r0 + i, bfr(acc));
+  }
+#pragma unroll
+  for (int u = 0; u < RR; ++u) {
+    const int i = S + wave + u * NWAVE;
+    if (i < R && r0 + i < rows) {
+      const float acc = WR::dot(Rr[u], s.g.xs, lane);
+      if (lane == 0) st_ag(qkv + r0 + i, bfr(acc));
+    }
   }
 }
 
@@ -995,7 +1019,8 @@ __device__ __forceinline__ void phase_attn(const Params& p, int layer, S& s, Wai
 // P3: O projection and residual (ref_numpy.py:130): x = bfr(x + bfr(Wo . o)); the residual is read into LDS in
 // the prologue together with o, so the epilogue does not wait on memory.  HQ > 0 (persistent kernel): the next
 // layer's QKV rows of this workgroup start streaming into LDS right behind the O rows; the attention and router
-// phases around it leave the memory system room for them.
+// phases around it leave the memory system room for them (a dense model's O phase absorbs them less well, yet
+// better than its gate/up phase: 3.140 against 3.176 ms/token for Qwen3-8B).
 template <class WR, class Wait, int HQ = 0>
 __device__ __forceinline__ void phase_oproj(const Params& p, int layer, Smem& s, Wait wait) {
   constexpr int KK = WR::K;
