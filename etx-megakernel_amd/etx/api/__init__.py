@@ -105,8 +105,26 @@ def _checked(workload: WorkloadSpec):
     if bad:
         raise ValueError(f"unknown model keys {sorted(bad)}")
     run = cfg.get("run", {})
-    from etx.runtime.native import ModelConfig
-    return ModelConfig(name=workload.name, **model), run
+    from etx.runtime import native as N
+    mc = N.ModelConfig(name=workload.name, **model)
+    if "prefill" not in model and bool(run.get("fused", True)):
+        mc = _default_prefill(mc)
+    return mc, run
+
+
+def _default_prefill(mc):
+    """The prompt rows per prefill launch when the model leaves them open: the most the library accepts for this
+    shape (16, else 4), or none.  Prefill is bit-identical to reading the prompt token by token."""
+    import dataclasses
+    from etx.runtime import native as N
+    for rows in (16, 4):
+        cand = dataclasses.replace(mc, prefill=rows)
+        try:
+            N.sizes(cand)
+            return cand
+        except N.EtxmkError:
+            continue
+    return mc
 
 
 @dataclass(frozen=True)
@@ -154,12 +172,22 @@ def plan(workload: WorkloadSpec, workgroups: int = 256) -> PlannedWorkload:
         decisions.append("multi-head latent attention, absorbed: W_UK^T per head before the attention, W_UV after "
                          "the merge; chunk items of 8 heads x 64 positions over the latent cache")
     else:
-        rows = mc.nqkv
-        R = -(-rows // wg)
-        staged = fused and mc.batch == 1 and mc.wdtype == N.W_BF16 and mc.H % 512 == 0 and R * mc.H * 2 <= 81920
-        decisions.append(f"QKV rows staged in LDS a layer ahead ({R} rows per workgroup)" if staged
+        R = -(-mc.nqkv // wg)                             # a workgroup's QKV rows; the library's staging rule
+        S = min(R, 81920 // (2 * mc.H))
+        staged = (fused and mc.batch == 1 and mc.wdtype == N.W_BF16 and mc.H % 512 == 0
+                  and R - S <= (16 if mc.H >= 4096 else 0))
+        decisions.append((f"QKV rows staged in LDS a layer ahead ({R} rows per workgroup)" if S == R else
+                          f"QKV rows: {S} of each workgroup's {R} staged in LDS a layer ahead, {R - S} loaded into "
+                          f"registers before the QKV phase's wait") if staged
                          else "QKV rows streamed from HBM in the QKV phase")
-        decisions.append(f"attention items: {mc.NKV} kv heads x 64-position chunks per sequence, last-arriver merge")
+        if mc.batch > 1:
+            decisions.append(f"attention items: {mc.NKV} kv heads x two 64-position chunks per sequence, pipelined over "
+                             f"double-buffered tiles; the merge is a phase of its own")
+        else:
+            decisions.append(f"attention items: {mc.NKV} kv heads x 64-position chunks, last-arriver merge")
+    if fused and mc.prefill:
+        decisions.append(f"prompts: {max(mc.batch, mc.prefill)} positions per prefill launch of the batched kernel, "
+                         f"bit-identical to reading them token by token")
     lib = N.LIB_PATH
     record = {
         "schema_version": SCHEMA_VERSION, "workload": workload.identity, "kernel": info["kernel"], "fused": fused,

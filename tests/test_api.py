@@ -135,3 +135,18 @@ def test_trace_step_rows(gpu, tmp_path, base, B):
     wg = body["workers_per_domain"] * body["domains"]
     assert np.all(rows[wg:, 5] >= rows[:-wg, 7] - 1)     # a workgroup takes phase k after its arrival from k-1
     sess.close()
+
+
+def test_prompt_rows_default_to_library_limit():
+    """A workload whose model leaves `prefill` open reads prompts through the largest prefill launch the library
+    accepts for its shape (16 rows, 4 for Qwen3-8B and DeepSeek-V2-Lite); one that sets it, or runs unfused, keeps
+    its choice."""
+    def prompts_line(cfg, model=None, **run):
+        model = model if model is not None else {k: v for k, v in cfg.as_dict().items() if k != "prefill"}
+        ds = api.plan(api.decode_workload(cfg.name, model, **run)).record.to_dict()["decisions"]
+        return [d for d in ds if d.startswith("prompts:")]
+    assert prompts_line(configs.QWEN3_30B_A3B)[0].startswith("prompts: 16 positions")
+    assert prompts_line(configs.QWEN3_8B)[0].startswith("prompts: 4 positions")
+    assert prompts_line(configs.DEEPSEEK_V2_LITE)[0].startswith("prompts: 4 positions")
+    assert prompts_line(configs.QWEN3_30B_A3B, configs.QWEN3_30B_A3B.as_dict()) == []      # prefill 0 set
+    assert prompts_line(configs.QWEN3_30B_A3B, fused=False) == []
