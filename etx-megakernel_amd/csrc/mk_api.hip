@@ -334,7 +334,7 @@ int kv_pools(const etxmk_config* c) { return c->arch == ETXMK_ARCH_DSV2 ? 1 : 2;
 
 struct WsLayout {
   uint64_t x, x16, qkv, o, o16, logits, hbuf, h16, apart, acnt, amax, bar, abort_w, tokens, out_tokens, btab, rcos, rsin,
-      layers, h16d, qc, h16s, total;
+      layers, h16d, qc, h16s, sink, total;
 };
 
 WsLayout ws_layout(const etxmk_config* c) {
@@ -372,6 +372,7 @@ WsLayout ws_layout(const etxmk_config* c) {
   } else {
     w.h16d = w.h16;
   }
+  w.sink = take(4ull * SINK_WAVES * 64);
   w.total = off;
   return w;
 }
@@ -909,6 +910,7 @@ static int launch(etxmk_handle* h, const int32_t* posv, int pos, int write_next,
   p.nqkv = nqkv_of(c);
   p.Ip = ds ? ds_ip(c) : c.I;
   p.h16d = h->wsptr<uint16_t>(h->ws.h16d);
+  p.sink = h->wsptr<float>(h->ws.sink);
   p.arch = c.arch;
   if (ds) {
     p.I = c.dense_I;

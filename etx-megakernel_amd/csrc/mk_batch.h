@@ -230,15 +230,24 @@ __device__ __forceinline__ void dot_row_long_b(const uint16_t* row, XP xp, int n
   for (int b = 0; b < B; ++b) v[b] = b < nv ? wave_sum(acc[b]) : 0.0f;
 }
 
-// gemv_run with B input rows per group: groups of NR rows dealt round-robin to the grid's waves; two register
-// buffers alternate, so one group's weights stream while the other group is reduced (a batched group carries
-// B x NR dots, which covers the latency of the next group's loads).  The first group is issued before `prologue`
-// (which waits for the inputs).  nvec(g) is the number of input rows of group g, xvec(g, b) the LDS address of
-// its b-th; epi(g, nv, v) consumes v[NR][B].
-template <class WR, int NR, int B, class RowF, class NVF, class XF, class EpiF, class Pro>
+// the wave's store sink: the target of epilogue lanes that have no value to store.  All of them write the same
+// word (one of the values lands; the line written is one per store, not four); waves are 256 bytes apart.
+__device__ __forceinline__ float* sink_of(const Params& p) {
+  return p.sink + (size_t)((blockIdx.x * NWAVE + wave_u()) & (SINK_WAVES - 1)) * 64;
+}
+
+// gemv_run with B input rows per group: groups of NR rows dealt round-robin to the grid's waves.  D register buffers
+// form a ring: the next D - 1 groups' weights stream while one group is reduced, the first D - 1 issued before
+// `prologue` (which waits for the inputs).  Every issue is the same run of loads: a missing row (nullptr) reloads
+// the group's first row, and past the wave's last group the issues reload that group (cache hits); with epilogues of
+// one store per lane (the sink for lanes with nothing to store) the compiler's wait before a buffer's dots counts
+// exactly the loads and stores issued after it, so it never waits for groups still streaming.  nvec(g) is the number
+// of input rows of group g, xvec(g, b) the LDS address of its b-th; epi(g, nv, v) consumes v[NR][B].
+template <class WR, int NR, int B, int D = 2, class RowF, class NVF, class XF, class EpiF, class Pro>
 __device__ __forceinline__ bool gemv_run_b(int ngroups, RowF rowf, NVF nvec, XF xvec, EpiF epi, Pro prologue, int nwg,
                                            uint64_t* trace, int s_phase) {
   using Regs = typename WR::Regs;
+  static_assert(D >= 2, "a ring of at least two buffers");
   const int lane = lane_id();
   const int gw = blockIdx.x * NWAVE + wave_u(), nw = nwg * NWAVE;
   if constexpr (WR::LONG) {                               // rows streamed in segments (dot_row_long_b)
@@ -258,35 +267,56 @@ __device__ __forceinline__ bool gemv_run_b(int ngroups, RowF rowf, NVF nvec, XF 
     }
     return true;
   } else {
-    Regs RA[NR], RB[NR];
-    auto issue = [&](Regs(&R)[NR], int g) {
+    Regs R[D][NR];
+    const bool any = gw < ngroups;
+    const int last = any ? gw + (ngroups - 1 - gw) / nw * nw : 0;
+    auto issue = [&](Regs(&Rb)[NR], int g) {
+      const int gc = g <= last ? g : last;
+      const uint8_t* r0 = rowf(gc, 0);
 #pragma unroll
       for (int i = 0; i < NR; ++i) {
-        const uint8_t* rp = rowf(g, i);
-        if (rp) WR::load(R[i], rp, lane);
+        const uint8_t* rp = i == 0 ? r0 : rowf(gc, i);
+        WR::load(Rb[i], rp ? rp : r0, lane);
       }
     };
-    auto compute = [&](const Regs(&R)[NR], int g) {
+    auto compute = [&](const Regs(&Rb)[NR], int g) {
       const int nv = nvec(g);
       float v[NR][B];
-      dot_rows_any<WR, NR, B>(R, [&](int b) { return xvec(g, b); }, nv, lane, v);
+      dot_rows_any<WR, NR, B>(Rb, [&](int b) { return xvec(g, b); }, nv, lane, v);
       epi(g, nv, v);
     };
-    int g = gw;
-    if (g < ngroups) issue(RA, g);
-    if (trace && threadIdx.x == 0)
-      *(MK_G uint64_t*)(trace + ((size_t)s_phase * nwg + blockIdx.x) * 3 + 2) = __builtin_amdgcn_s_memrealtime();
-    if (!prologue()) return false;
-    while (g < ngroups) {
-      const int g1 = g + nw;
-      if (g1 < ngroups) issue(RB, g1);
-      compute(RA, g);
-      if (g1 >= ngroups) break;
-      const int g2 = g1 + nw;
-      if (g2 < ngroups) issue(RA, g2);
-      compute(RB, g1);
-      g = g2;
+    auto stamp = [&]() {
+      if (trace && threadIdx.x == 0)
+        *(MK_G uint64_t*)(trace + ((size_t)s_phase * nwg + blockIdx.x) * 3 + 2) = __builtin_amdgcn_s_memrealtime();
+    };
+    const int n = any ? (last - gw) / nw + 1 : 0;        // this wave's groups
+    if (n == 1 || n == 2) {                               // one or two groups: no ring, no reloads
+      issue(R[0], gw);
+      stamp();
+      if (!prologue()) return false;
+      if (n == 2) issue(R[1], gw + nw);
+      compute(R[0], gw);
+      if (n == 2) compute(R[1], gw + nw);
+      return true;
     }
+    if (any)
+#pragma unroll
+      for (int j = 0; j + 1 < D; ++j) issue(R[j], gw + j * nw);
+    stamp();
+    if (!prologue()) return false;
+    if (!any) return true;
+    issue(R[D - 1], gw + (D - 1) * nw);                   // the last slot after the wait: more loads in flight
+    int g = gw;                                           // during the grid barrier slow the barrier down
+    for (;;) {                                            // a buffer is refilled right after its dots: the issue's
+#pragma unroll                                            // address temporaries alias no load still in flight
+      for (int j = 0; j < D; ++j) {
+        compute(R[j], g);
+        if (g >= last) goto done;
+        issue(R[j], g + D * nw);
+        g += nw;
+      }
+    }
+  done:
     return true;
   }
 }
@@ -343,13 +373,14 @@ __device__ __forceinline__ float lane_pick(const float (&v)[NR][B]) {
       if (i * B + b < 64) r = lane == i * B + b ? v[i][b] : r;
   return r;
 }
-// store NR x B values: lane i*B + b stores (i, b) for b < nv, one divergent call
+// store NR x B values: lane i*B + b holds (i, b), valid for i < NR and b < nv; f(i, b, val, ok) makes one store
+// from every lane, to the sink where !ok
 template <int NR, int B, class F>
 __device__ __forceinline__ void lane_store_b(const float (&v)[NR][B], int nv, F f) {
   static_assert(NR * B <= 64, "one lane per value");
   const int lane = lane_id(), i = lane / B, b = lane - i * B;
   const float val = lane_pick<NR, B>(v);
-  if (i < NR && b < nv) f(i, b, val);
+  f(i < NR ? i : 0, b, val, i < NR && b < nv);
 }
 
 // ---------------------------------------------------------------- phases (batched)
@@ -366,9 +397,9 @@ __device__ __forceinline__ void phase_qkv_b(const Params& p, int layer, S& s, Wa
       [&](int g, int i) -> const uint8_t* { const int r = 2 * g + i; return r < rows ? mrow<WR>(W, r) : nullptr; },
       [&](int) { return nb; }, [&](int, int b) { return (const uint16_t*)(s.n.xs + b * KK); },
       [&](int g, int nv, const float(&v)[2][B]) {
-        lane_store_b<2, B>(v, nv, [&](int i, int b, float val) {
+        lane_store_b<2, B>(v, nv, [&](int i, int b, float val, bool ok) {
           const int r = 2 * g + i;
-          if (r < rows) st_ag(p.qkv + (size_t)b * rows + r, bfr(val));
+          st_ag(ok && r < rows ? p.qkv + (size_t)b * rows + r : sink_of(p), bfr(val));
         });
       },
       [&]() {
@@ -701,8 +732,8 @@ __device__ __forceinline__ void phase_oproj_b(const Params& p, int layer, S& s, 
       [&](int, int b) { return (const uint16_t*)(s.v.xs + b * KK); },
       [&](int g, int nv, const float(&v)[1][B]) {
         const int r = res_slot(g, nw);
-        lane_store_b<1, B>(v, nv, [&](int, int b, float val) {
-          st_ag_u16(p.x16 + (size_t)b * H + g, f2bf(s.v.xres[b][r] + bfr(val)));
+        lane_store_b<1, B>(v, nv, [&](int, int b, float val, bool ok) {
+          st_ag_u16(ok ? p.x16 + (size_t)b * H + g : (uint16_t*)sink_of(p), f2bf(s.v.xres[b][r] + bfr(val)));
         });
       },
       [&]() {
@@ -727,7 +758,9 @@ __device__ __forceinline__ void phase_router_b(const Params& p, int layer, S& s,
       E, [&](int g, int) -> const uint8_t* { return mrow<WR>(W, g); }, [&](int) { return nb; },
       [&](int, int b) { return (const uint16_t*)(s.n.xs + b * KK); },
       [&](int g, int nv, const float(&v)[1][B]) {
-        lane_store_b<1, B>(v, nv, [&](int, int b, float val) { st_ag(p.logits + (size_t)b * E + g, bfr(val)); });
+        lane_store_b<1, B>(v, nv, [&](int, int b, float val, bool ok) {
+          st_ag(ok ? p.logits + (size_t)b * E + g : sink_of(p), bfr(val));
+        });
       },
       [&]() {
         if (!wait()) return false;
@@ -841,8 +874,8 @@ __device__ __forceinline__ void phase_expert_up_b(const Params& p, int layer, S&
       [&](int g, int nv, const float(&v)[2][B]) {
         const int u = g / MI, j = g - u * MI, lane = lane_id();
         const float gv = lane_pick<1, B>((const float(&)[1][B])v[0]), uv = lane_pick<1, B>((const float(&)[1][B])v[1]);
-        if (lane < nv)
-          st_ag_u16(p.h16 + (size_t)(s.ustart[u] + lane) * MI + perm_stored(j, MI), f2bf(bfr(bfr(silu(bfr(gv))) * bfr(uv))));
+        st_ag_u16(lane < nv ? p.h16 + (size_t)(s.ustart[u] + lane) * MI + perm_stored(j, MI) : (uint16_t*)sink_of(p),
+                  f2bf(bfr(bfr(silu(bfr(gv))) * bfr(uv))));
       },
       [&]() { return true; }, p.nwg, p.trace, s.phase);
 }
@@ -850,7 +883,10 @@ __device__ __forceinline__ void phase_expert_up_b(const Params& p, int layer, S&
 // P6: expert down, routing weight, combine per sequence in ascending expert id, residual (ref_numpy.py:146-148).
 // Each wave owns output rows; for its row it streams the rows of every distinct expert (D at a time, the next
 // batch in flight while the current one is reduced) and dots each with the h rows of that expert's pairs.  The
-// pairs' h rows are staged in LDS in passes of whole experts that fit; lane b carries sequence b's combine chain.
+// pairs' h rows are staged in LDS in passes of whole experts that fit; lane b carries sequence b's combine chain,
+// kept in LDS between batches and passes.  Every batch issue is the same run of loads (a batch short of D experts
+// reloads its last one; after a row's last batch the issue reloads it) and the outputs are stored after the last
+// pass, so the wait before a batch's dots counts exactly the loads issued after it.
 template <class WR, int B, class S, class Wait>
 __device__ __forceinline__ void phase_expert_down_b(const Params& p, int layer, S& s, Wait wait) {
   constexpr int KK = WR::K;
@@ -867,8 +903,10 @@ __device__ __forceinline__ void phase_expert_down_b(const Params& p, int layer, 
   Regs R[2][DE];
   auto issue = [&](Regs(&Rb)[DE], int g, int ub, int u1) {
 #pragma unroll
-    for (int d = 0; d < DE; ++d)
-      if (ub + d < u1) WR::load(Rb[d], mrow<WR>(W, (size_t)s.uexp[ub + d] * H + g), lane);
+    for (int d = 0; d < DE; ++d) {
+      const int u = ub + d < u1 ? ub + d : u1 - 1;
+      WR::load(Rb[d], mrow<WR>(W, (size_t)s.uexp[u] * H + g), lane);
+    }
   };
   int u0 = 0, u1 = 0;
   auto pass_end = [&](int a) {
@@ -890,11 +928,12 @@ __device__ __forceinline__ void phase_expert_down_b(const Params& p, int layer, 
     copy_rows_lds(p.h16 + (size_t)p0 * KK, (s.ustart[u1] - p0) * KK, s.v.xs);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    const bool last_pass = u1 >= U;
     float acc = 0.0f;
     auto compute = [&](Regs(&Rb)[DE], int t) {
       const int g = gw + (t / nbt) * nw, ub = u0 + (t % nbt) * DE, r = res_slot(g, nw);
       if (t % nbt == 0) acc = (!first_pass && lane < nb) ? s.v.acc[lane][r] : 0.0f;
+#pragma unroll
+      for (int d = 0; d < DE; ++d) settle(Rb[d]);
 #pragma unroll
       for (int d = 0; d < DE; ++d)
         if (ub + d < u1)
@@ -902,27 +941,32 @@ __device__ __forceinline__ void phase_expert_down_b(const Params& p, int layer, 
             const float y = bfr(bfr(WR::dot(Rb[d], s.v.xs + (pp - p0) * KK, lane)) * s.pw[pp]);
             if (lane == s.pseq[pp]) acc = bfr(acc + y);
           }
-      if (t % nbt == nbt - 1 && lane < nb) {
-        if (last_pass) st_ag_u16(p.x16 + (size_t)lane * H + g, f2bf(s.v.xres[lane][r] + acc));
-        else s.v.acc[lane][r] = acc;
-      }
+      if (t % nbt == nbt - 1 && lane < nb) s.v.acc[lane][r] = acc;
     };
     auto batch_g = [&](int t) { return gw + (t / nbt) * nw; };
     auto batch_u = [&](int t) { return u0 + (t % nbt) * DE; };
-    if (!first_pass && T > 0) issue(R[0], batch_g(0), batch_u(0), u1);
-    for (int t = 0; t < T; t += 2) {
-      if (t + 1 < T) issue(R[1], batch_g(t + 1), batch_u(t + 1), u1);
-      compute(R[0], t);
-      if (t + 2 < T) issue(R[0], batch_g(t + 2), batch_u(t + 2), u1);
-      if (t + 1 < T) compute(R[1], t + 1);
+    auto clamp_t = [&](int t) { return t < T ? t : T - 1; };
+    if (T > 0) {                                          // a buffer is refilled right after its dots
+      if (!first_pass) issue(R[0], batch_g(0), batch_u(0), u1);
+      issue(R[1], batch_g(clamp_t(1)), batch_u(clamp_t(1)), u1);
+      for (int t = 0;; t += 2) {
+        compute(R[0], t);
+        if (t + 1 >= T) break;
+        issue(R[0], batch_g(clamp_t(t + 2)), batch_u(clamp_t(t + 2)), u1);
+        compute(R[1], t + 1);
+        if (t + 2 >= T) break;
+        issue(R[1], batch_g(clamp_t(t + 3)), batch_u(clamp_t(t + 3)), u1);
+      }
     }
     first_pass = false;
     u0 = u1;
     if (u0 < U) u1 = pass_end(u0);
   }
-  if (U == 0)                                             // no expert (never with TOPK >= 1): the residual passes
-    for (int g = gw; g < H; g += nw)
-      if (lane < nb) st_ag_u16(p.x16 + (size_t)lane * H + g, f2bf(s.v.xres[lane][res_slot(g, nw)]));
+  for (int g = gw; g < H; g += nw)                        // residual + combine (no expert, never with TOPK >= 1:
+    if (lane < nb) {                                      // the residual alone)
+      const int r = res_slot(g, nw);
+      st_ag_u16(p.x16 + (size_t)lane * H + g, f2bf(U > 0 ? s.v.xres[lane][r] + s.v.acc[lane][r] : s.v.xres[lane][r]));
+    }
 }
 
 // dense MLP (ref_numpy.py:149-152): gate/up + SiLU*up per sequence into h16, then down + residual
@@ -938,8 +982,8 @@ __device__ __forceinline__ void phase_gateup_b(const Params& p, int layer, S& s,
       [&](int g, int nv, const float(&v)[2][B]) {
         const int lane = lane_id();
         const float gv = lane_pick<1, B>((const float(&)[1][B])v[0]), uv = lane_pick<1, B>((const float(&)[1][B])v[1]);
-        if (lane < nv)
-          st_ag_u16(p.h16d + (size_t)lane * IS + perm_stored(g, IS), f2bf(bfr(bfr(silu(bfr(gv))) * bfr(uv))));
+        st_ag_u16(lane < nv ? p.h16d + (size_t)lane * IS + perm_stored(g, IS) : (uint16_t*)sink_of(p),
+                  f2bf(bfr(bfr(silu(bfr(gv))) * bfr(uv))));
       },
       [&]() {
         if (!wait()) return false;
@@ -961,8 +1005,8 @@ __device__ __forceinline__ void phase_down_b(const Params& p, int layer, S& s, W
       [&](int, int b) { return (const uint16_t*)(s.v.xs + b * KK); },
       [&](int g, int nv, const float(&v)[1][B]) {
         const int r = res_slot(g, nw);
-        lane_store_b<1, B>(v, nv, [&](int, int b, float val) {
-          st_ag_u16(p.x16 + (size_t)b * H + g, f2bf(s.v.xres[b][r] + bfr(val)));
+        lane_store_b<1, B>(v, nv, [&](int, int b, float val, bool ok) {
+          st_ag_u16(ok ? p.x16 + (size_t)b * H + g : (uint16_t*)sink_of(p), f2bf(s.v.xres[b][r] + bfr(val)));
         });
       },
       [&]() {

@@ -40,6 +40,7 @@ constexpr int MAX_TOPK = 8;
 constexpr int PART = HDIM + 2;          // attention partial: a[HD], m, l
 constexpr int QKVW_BYTES = 81920;       // the workgroup's rows of the next layer's QKV matrix, staged in LDS
 constexpr int MAX_B = 16;               // sequences per batched step
+constexpr int SINK_WAVES = 2048;        // waves with a private store sink (more share them modulo)
 
 // one layer's tensors; matrices are byte addresses of rows in their format (Bf16Row / Fp8Row below)
 struct LayerW {
@@ -102,6 +103,9 @@ struct Params {
   float routed_scale;
   float* qc;                            // [L][B][NH][kv_lora] absorbed queries, fp32
   uint16_t* h16s;                       // [B][SI] shared experts' activations, bf16 lane-permuted
+  float* sink;                          // [SINK_WAVES][64]: where a batched GEMV's lanes with no value store (one
+                                        // word per wave, 256 bytes apart), so
+                                        // every epilogue is one store per lane and the load waits stay exact
 };
 
 // the attention phase's LDS (one (sequence, kv head, chunk) item at a time)
@@ -523,6 +527,25 @@ struct Bf16Row {
     else return 0.0f;
   }
 };
+// An empty asm reading every register of a row buffer: the compiler's wait for the buffer's loads lands here, on
+// every path.  Without it the first uses sit in conditional code, the skip path leaves the buffer pending, and
+// the next issue into neighbouring registers waits for loads still streaming.
+template <int K>
+__device__ __forceinline__ void settle(const RowRegs<K>& r) {
+#pragma unroll
+  for (int b = 0; b < KS<K>::KB; ++b) asm volatile("" ::"v"(r.w[b]));
+#pragma unroll
+  for (int t = 0; t < KS<K>::TW; ++t) asm volatile("" ::"v"(r.t[t]));
+}
+template <int K>
+__device__ __forceinline__ void settle(const RowRegs8<K>& r) {
+#pragma unroll
+  for (int b = 0; b < KS8<K>::KB; ++b) asm volatile("" ::"v"(r.w[b]));
+#pragma unroll
+  for (int t = 0; t < KS8<K>::TW; ++t) asm volatile("" ::"v"(r.t[t]));
+  asm volatile("" ::"v"(r.sc));
+}
+
 template <int K_>
 struct Fp8Row {
   static constexpr int K = K_;

@@ -156,7 +156,9 @@ __device__ __forceinline__ void phase_absorb_b(const Params& p, int layer, S& s,
       [&](int) { return nb; },
       [&](int g, int b) { return (const uint16_t*)(s.v.xs + (b * NH + (g * NR) / MLA_KVL) * MLA_NOPE); },
       [&](int g, int nv, const float(&v)[NR][B]) {
-        lane_store_b<NR, B>(v, nv, [&](int i, int b, float val) { st_ag(qc_of(p, layer, b, 0) + g * NR + i, val); });
+        lane_store_b<NR, B>(v, nv, [&](int i, int b, float val, bool ok) {
+          st_ag(ok ? qc_of(p, layer, b, 0) + g * NR + i : sink_of(p), val);
+        });
       },
       [&]() {
         if (!wait()) return false;
@@ -449,11 +451,14 @@ __device__ __forceinline__ void phase_router_shared_b(const Params& p, int layer
       [&](int) { return nb; }, [&](int, int b) { return (const uint16_t*)(s.n.xs + b * KK); },
       [&](int g, int nv, const float(&v)[2][B]) {
         if (g < E2) {
-          lane_store_b<2, B>(v, nv, [&](int i, int b, float val) { st_ag(p.logits + (size_t)b * E + 2 * g + i, val); });
+          lane_store_b<2, B>(v, nv, [&](int i, int b, float val, bool ok) {
+            st_ag(ok ? p.logits + (size_t)b * E + 2 * g + i : sink_of(p), val);
+          });
         } else {
           const int j = g - E2, lane = lane_id();
           const float gv = lane_pick<1, B>((const float(&)[1][B])v[0]), uv = lane_pick<1, B>((const float(&)[1][B])v[1]);
-          if (lane < nv) st_ag_u16(p.h16s + (size_t)lane * SI + perm_stored(j, SI), f2bf(bfr(bfr(silu(bfr(gv))) * bfr(uv))));
+          st_ag_u16(lane < nv ? p.h16s + (size_t)lane * SI + perm_stored(j, SI) : (uint16_t*)sink_of(p),
+                    f2bf(bfr(bfr(silu(bfr(gv))) * bfr(uv))));
         }
       },
       [&]() {
