@@ -43,6 +43,7 @@
 #include <stdlib.h>
 #include <string.h>
 #include <omp.h>
+#include <immintrin.h>
 
 #define EXPORT __attribute__((visibility("default")))
 
@@ -235,6 +236,12 @@ static inline uint8_t f32_to_e4m3(float f) {
   return (uint8_t)(sign | (uint8_t)((e + 7) << 3) | (uint8_t)qm);
 }
 EXPORT float orc_e4m3_to_f32(uint8_t c) { return e4m3_to_f32(c); }
+/* the 256 decoded values, filled from e4m3_to_f32 when the library loads (the dot loops read them from here) */
+static float e4m3_lut[256];
+static void __attribute__((constructor)) fill_e4m3_lut(void) {
+  for (int c = 0; c < 256; ++c) e4m3_lut[c] = e4m3_to_f32((uint8_t)c);
+}
+static inline float e4m3_f(uint8_t c) { return e4m3_lut[c]; }
 EXPORT uint8_t orc_f32_to_e4m3(float f) { return f32_to_e4m3(f); }
 
 /* per-row quantisation of R rows of K bf16 values */
@@ -255,7 +262,7 @@ static inline float dot64_q(const uint8_t* q, const float* x, int K) {
   float acc[64];
   for (int l = 0; l < 64; ++l) acc[l] = 0.0f;
   for (int k0 = 0; k0 < K; k0 += 64)
-    for (int l = 0; l < 64; ++l) acc[l] = fmaf(e4m3_to_f32(q[k0 + l]), x[k0 + l], acc[l]);
+    for (int l = 0; l < 64; ++l) acc[l] = fmaf(e4m3_f(q[k0 + l]), x[k0 + l], acc[l]);
   return butterfly64(acc);
 }
 /* canonical dot over dequantised bf16 weights bfr(e4m3 * s) (wdtype 2) */
@@ -263,7 +270,7 @@ static inline float dot64_deq(const uint8_t* q, float s, const float* x, int K) 
   float acc[64];
   for (int l = 0; l < 64; ++l) acc[l] = 0.0f;
   for (int k0 = 0; k0 < K; k0 += 64)
-    for (int l = 0; l < 64; ++l) acc[l] = fmaf(bfr(e4m3_to_f32(q[k0 + l]) * s), x[k0 + l], acc[l]);
+    for (int l = 0; l < 64; ++l) acc[l] = fmaf(bfr(e4m3_f(q[k0 + l]) * s), x[k0 + l], acc[l]);
   return butterfly64(acc);
 }
 EXPORT float orc_dot64_q(const uint8_t* q, const float* x, int K) { return dot64_q(q, x, K); }
@@ -653,6 +660,374 @@ static void layer_step(orc_model* m, int l, float* x, int pos, const int32_t* bt
   free(xs); free(qkv); free(o); free(t);
 }
 
+/* ------------------------------------------------------------------ many rows at once */
+/* A row is one decode step of one sequence: its token, position and block table.  orc_step_rows computes n rows
+ * with the loops turned round: every weight row is read once and dotted with the n rows' vectors, each in the
+ * canonical order of dot64; each layer writes the K/V of every row before any row attends, and row r attends to
+ * its own sequence's positions up to its own.  So n rows of distinct sequences are one batched step (each row what
+ * orc_step_seq computes), and n consecutive positions of one sequence are the prompt loop of
+ * examples/llm/host.hip:203-213 (each position what the decode step at that position computes, given the earlier
+ * positions' K/V).  tests/test_oracle_prefill.py checks both forms against orc_step_seq bit for bit. */
+typedef struct {
+  const int32_t* bt;   /* the row's sequence's block table */
+  int pos;             /* the row's position */
+} orc_row;
+
+/* row r of a matrix as fp32 weights, with the factor its dot is multiplied by (the fp8 row scale, else 1) */
+static inline float row_f32(const orc_mat* m, int wdtype, size_t r, int K, float* out) {
+  if (wdtype == 0) { for (int k = 0; k < K; ++k) out[k] = bf2f(m->w[r * K + k]); return 1.0f; }
+  if (wdtype == 1) { for (int k = 0; k < K; ++k) out[k] = e4m3_f(m->q[r * K + k]); return m->s[r]; }
+  for (int k = 0; k < K; ++k) out[k] = bfr(e4m3_f(m->q[r * K + k]) * m->s[r]);
+  return 1.0f;
+}
+/* dot64 with fp32 weights: the same fma chain per lane and the same lane reduction, in AVX2.  Lane l of the 64 is
+ * element l of ymm accumulator l / 8.  lanes_reduce() adds partners l^1, l^2, then the 8-lane and 16-lane mirrors and
+ * the rows pairwise: for the sum it returns (every step is one addition of two values, and a + b == b + a) that is
+ * the balanced pairwise tree over lanes 0..63 in order, ((a0 + a1) + (a2 + a3)) + ((a4 + a5) + (a6 + a7)) per eight,
+ * eights paired, then (R0 + R1) + (R2 + R3).  Two hadd rounds build the tree of each eight in a 128-bit half,
+ * adding the halves closes it.  tests/test_oracle_prefill.py compares this with dot64 on random rows. */
+static inline float tree64(const __m256 v[8]) {
+  const __m256 h01 = _mm256_hadd_ps(v[0], v[1]), h23 = _mm256_hadd_ps(v[2], v[3]);
+  const __m256 h45 = _mm256_hadd_ps(v[4], v[5]), h67 = _mm256_hadd_ps(v[6], v[7]);
+  const __m256 k0 = _mm256_hadd_ps(h01, h23), k1 = _mm256_hadd_ps(h45, h67);   /* [G0 G1 G2 G3 | G0' ...] halves */
+  const __m128 g03 = _mm_add_ps(_mm256_castps256_ps128(k0), _mm256_extractf128_ps(k0, 1));   /* G0..G3 */
+  const __m128 g47 = _mm_add_ps(_mm256_castps256_ps128(k1), _mm256_extractf128_ps(k1, 1));   /* G4..G7 */
+  float g[8];
+  _mm_storeu_ps(g, g03);
+  _mm_storeu_ps(g + 4, g47);
+  return ((g[0] + g[1]) + (g[2] + g[3])) + ((g[4] + g[5]) + (g[6] + g[7]));
+}
+static inline float dot64f(const float* w, const float* x, int K) {
+  __m256 a[8];
+  for (int j = 0; j < 8; ++j) a[j] = _mm256_setzero_ps();
+  for (int k0 = 0; k0 < K; k0 += 64)
+    for (int j = 0; j < 8; ++j)
+      a[j] = _mm256_fmadd_ps(_mm256_loadu_ps(w + k0 + 8 * j), _mm256_loadu_ps(x + k0 + 8 * j), a[j]);
+  return tree64(a);
+}
+EXPORT float orc_dot64f(const float* w, const float* x, int K) { return dot64f(w, x, K); }
+/* value of row r for vector x: mat_dot's result, from the row's fp32 image */
+static inline float row_dot(const float* wf, float sc, int wdtype, const float* x, int K) {
+  const float d = dot64f(wf, x, K);
+  return wdtype == 1 ? d * sc : d;
+}
+/* out[b * ldo + r] = bfr(row r . X[b * ldx ..]) for rows [0, R), vectors [0, n).  A thread takes 8 rows at a time
+ * (their fp32 images stay in its L2) and runs every vector against them (each vector stays in L1 for the 8). */
+#define ORC_TR 8
+static void gemv_rows_multi(const orc_mat* W, int wdtype, int R, int K, const float* X, int ldx, int n, float* out,
+                            int ldo) {
+#pragma omp parallel
+  {
+    float* wf = (float*)malloc(sizeof(float) * (size_t)K * ORC_TR);
+    float sc[ORC_TR];
+#pragma omp for schedule(dynamic, 1)
+    for (int r0 = 0; r0 < R; r0 += ORC_TR) {
+      const int nr = R - r0 < ORC_TR ? R - r0 : ORC_TR;
+      for (int i = 0; i < nr; ++i) sc[i] = row_f32(W, wdtype, (size_t)(r0 + i), K, wf + (size_t)i * K);
+      for (int b = 0; b < n; ++b)
+        for (int i = 0; i < nr; ++i)
+          out[(size_t)b * ldo + r0 + i] = bfr(row_dot(wf + (size_t)i * K, sc[i], wdtype, X + (size_t)b * ldx, K));
+    }
+    free(wf);
+  }
+}
+
+/* attention_head for every row's q heads (row r's at qkv + r * ldq).  Rows of one sequence share one gathered copy of
+ * that sequence's cache, fp32 K^T [h][d][t] and V [h][t][d] over positions 0 .. (largest position of its rows): the
+ * scores of eight positions are computed at a time (each one's fma chain over d ascending, as in attention_head),
+ * and a[d] for eight dims at a time (each one's chain over t ascending).  The chunk maxima, the exponentials, the
+ * chunk sums and the merge are attention_head's, in its order. */
+static void attention_rows(const uint16_t* kc, const uint16_t* vc, const orc_row* rows, int n, const float* qkv, int ldq,
+                           int NH, int NKV, int HD, int BS, float* o) {
+  const int G = NH / NKV;
+  const float scale = (float)(1.0 / sqrt((double)HD));
+  int* done = (int*)calloc((size_t)n, sizeof(int));
+  int* grp = (int*)malloc(sizeof(int) * (size_t)n);
+  for (int r0 = 0; r0 < n; ++r0) {
+    if (done[r0]) continue;
+    const int32_t* bt = rows[r0].bt;
+    int ng = 0, T = 0;
+    for (int r = r0; r < n; ++r)
+      if (!done[r] && rows[r].bt == bt) {
+        done[r] = 1;
+        grp[ng++] = r;
+        if (rows[r].pos + 1 > T) T = rows[r].pos + 1;
+      }
+    const int Tp = (T + 7) & ~7;
+    float* kt = (float*)malloc(sizeof(float) * (size_t)NKV * HD * Tp);
+    float* vt = (float*)malloc(sizeof(float) * (size_t)NKV * Tp * HD);
+#pragma omp parallel for schedule(static)
+    for (int t = 0; t < Tp; ++t)
+      for (int h = 0; h < NKV; ++h)
+        for (int d = 0; d < HD; ++d) {
+          float kv = 0.0f, vv = 0.0f;
+          if (t < T) {
+            const int blk = bt[t / BS], off = t % BS;
+            kv = bf2f(kc[kv_k_index(blk, off, h, d, NKV, HD, BS)]);
+            vv = bf2f(vc[kv_v_index(blk, off, h, d, NKV, HD, BS)]);
+          }
+          kt[((size_t)h * HD + d) * Tp + t] = kv;
+          vt[((size_t)h * Tp + t) * HD + d] = vv;
+        }
+#pragma omp parallel
+    {
+      float* sc = (float*)malloc(sizeof(float) * (size_t)Tp);
+      float A[512], a[512];
+#pragma omp for schedule(dynamic, 1)
+      for (int gh = 0; gh < ng * NH; ++gh) {
+        const int r = grp[gh / NH], hh = gh % NH, h = hh / G, nt = rows[r].pos + 1, ntp = (nt + 7) & ~7;
+        const float* q = qkv + (size_t)r * ldq + (size_t)hh * HD;
+        const float* K = kt + (size_t)h * HD * Tp;
+        const float* Vv = vt + (size_t)h * Tp * HD;
+        for (int t = 0; t < ntp; ++t) sc[t] = 0.0f;
+        for (int d = 0; d < HD; ++d) {
+          const float qd = q[d];
+          const float* kr = K + (size_t)d * Tp;
+          for (int t = 0; t < ntp; ++t) sc[t] = fmaf(qd, kr[t], sc[t]);
+        }
+        for (int t = 0; t < nt; ++t) sc[t] = sc[t] * scale;
+        const int nch = (nt + ATT_CHUNK - 1) / ATT_CHUNK;
+        float mc[256], M = -INFINITY, L = 0.0f;
+        for (int c = 0; c < nch; ++c) {
+          const int t0 = c * ATT_CHUNK, t1 = t0 + ATT_CHUNK < nt ? t0 + ATT_CHUNK : nt;
+          float m = -INFINITY;
+          for (int t = t0; t < t1; ++t) if (sc[t] > m) m = sc[t];
+          mc[c] = m;
+          if (m > M) M = m;
+        }
+        for (int d = 0; d < HD; ++d) A[d] = 0.0f;
+        for (int c = 0; c < nch; ++c) {
+          const int t0 = c * ATT_CHUNK, t1 = t0 + ATT_CHUNK < nt ? t0 + ATT_CHUNK : nt;
+          float l = 0.0f;
+          for (int d = 0; d < HD; ++d) a[d] = 0.0f;
+          for (int t = t0; t < t1; ++t) {
+            const float p = mk_expf(sc[t] - mc[c]);
+            l = l + p;
+            const float* vr = Vv + (size_t)t * HD;
+            for (int d = 0; d < HD; ++d) a[d] = fmaf(p, vr[d], a[d]);
+          }
+          const float w = mk_expf(mc[c] - M);
+          L = fmaf(w, l, L);
+          for (int d = 0; d < HD; ++d) A[d] = fmaf(w, a[d], A[d]);
+        }
+        float* ob = o + (size_t)r * NH * HD + (size_t)hh * HD;
+        for (int d = 0; d < HD; ++d) ob[d] = bfr(A[d] / L);
+      }
+      free(sc);
+    }
+    free(kt);
+    free(vt);
+  }
+  free(done);
+  free(grp);
+}
+
+/* layer l for n rows; X [n][H] residuals in place; ids_out / wts_out [n] rows of ldk (may be NULL) */
+static void layer_rows(orc_model* m, int l, float* X, int n, const orc_row* rows, int32_t* ids_out, float* wts_out,
+                       int ldk) {
+  const orc_config* c = &m->c;
+  orc_layer* y = &m->ly[l];
+  const int H = c->H, NH = c->NH, NKV = c->NKV, HD = c->HD, BS = c->block_size, wt = c->wdtype;
+  const int NQKV = (NH + 2 * NKV) * HD;
+  float* xs = (float*)malloc(sizeof(float) * (size_t)n * H);
+  float* qkv = (float*)malloc(sizeof(float) * (size_t)n * NQKV);
+  float* o = (float*)malloc(sizeof(float) * (size_t)n * NH * HD);
+  float* t = (float*)malloc(sizeof(float) * (size_t)n * H);
+  for (int b = 0; b < n; ++b) rmsnorm(X + (size_t)b * H, NULL, H, c->eps, xs + (size_t)b * H);
+  gemv_rows_multi(&y->wqkv, wt, NQKV, H, xs, H, n, qkv, NQKV);                /* :112-115 */
+#pragma omp parallel for schedule(static)
+  for (int b = 0; b < n; ++b) {                                                 /* :116-121 */
+    float* q = qkv + (size_t)b * NQKV;
+    const int pos = rows[b].pos;
+    const float* cs = m->rcos + (size_t)pos * (HD / 2);
+    const float* sn = m->rsin + (size_t)pos * (HD / 2);
+    float tmp[512];
+    for (int hh = 0; hh < NH + NKV; ++hh) {
+      float* v = q + (size_t)hh * HD;
+      if (c->qk_norm) { rmsnorm(v, NULL, HD, c->eps, tmp); memcpy(v, tmp, sizeof(float) * (size_t)HD); }
+      apply_rope(v, HD, cs, sn);
+    }
+    const int blk = rows[b].bt[pos / BS], off = pos % BS;
+    for (int hh = 0; hh < NKV; ++hh)
+      for (int d = 0; d < HD; ++d) {
+        y->kc[kv_k_index(blk, off, hh, d, NKV, HD, BS)] = f2bf(q[(size_t)(NH + hh) * HD + d]);
+        y->vc[kv_v_index(blk, off, hh, d, NKV, HD, BS)] = f2bf(q[(size_t)(NH + NKV + hh) * HD + d]);
+      }
+  }
+  attention_rows(y->kc, y->vc, rows, n, qkv, NQKV, NH, NKV, HD, BS, o);         /* :122-129 */
+  gemv_rows_multi(&y->wo, wt, H, NH * HD, o, NH * HD, n, t, H);                /* :130 */
+  for (size_t i = 0; i < (size_t)n * H; ++i) X[i] = bfr(X[i] + t[i]);
+  for (int b = 0; b < n; ++b) rmsnorm(X + (size_t)b * H, NULL, H, c->eps, xs + (size_t)b * H);  /* :131 */
+  if (c->moe) {
+    const int E = c->E, K = c->TOPK, MI = c->MI;
+    float* logits = (float*)malloc(sizeof(float) * (size_t)n * E);
+    const orc_mat wr = {y->wr, NULL, NULL};
+    gemv_rows_multi(&wr, 0, E, H, xs, H, n, logits, E);                          /* :134 */
+    int32_t* ids = (int32_t*)malloc(sizeof(int32_t) * (size_t)n * K);
+    float* wts = (float*)malloc(sizeof(float) * (size_t)n * K);
+    for (int b = 0; b < n; ++b) {
+      route(logits + (size_t)b * E, E, K, c->norm_topk, ids + (size_t)b * K, wts + (size_t)b * K);   /* :135-140 */
+      if (ids_out) memcpy(ids_out + (size_t)b * ldk, ids + (size_t)b * K, sizeof(int32_t) * (size_t)K);
+      if (wts_out) memcpy(wts_out + (size_t)b * ldk, wts + (size_t)b * K, sizeof(float) * (size_t)K);
+    }
+    /* the (row, slot) pairs grouped by expert: pairs of expert e are pr[pe[e] .. pe[e+1]) */
+    int* pe = (int*)calloc((size_t)E + 1, sizeof(int));
+    int* pr = (int*)malloc(sizeof(int) * (size_t)n * K);
+    for (int i = 0; i < n * K; ++i) pe[ids[i] + 1]++;
+    for (int e = 0; e < E; ++e) pe[e + 1] += pe[e];
+    int* fill = (int*)malloc(sizeof(int) * (size_t)E);
+    memcpy(fill, pe, sizeof(int) * (size_t)E);
+    for (int i = 0; i < n * K; ++i) pr[fill[ids[i]]++] = i;
+    int* used = (int*)malloc(sizeof(int) * (size_t)E);
+    int nu = 0;
+    for (int e = 0; e < E; ++e) if (pe[e + 1] > pe[e]) { ensure_expert(m, l, e); used[nu++] = e; }
+    float* hb = (float*)malloc(sizeof(float) * (size_t)n * K * MI);           /* h of pair i at hb + i * MI */
+    float* ys = (float*)malloc(sizeof(float) * (size_t)n * K * H);            /* y of pair i at ys + i * H */
+#pragma omp parallel
+    {
+      float* wg = (float*)malloc(sizeof(float) * (size_t)(H > MI ? H : MI) * 2);
+      float* wu = wg + (H > MI ? H : MI);
+#pragma omp for schedule(dynamic, 8)
+      for (int u = 0; u < nu * MI; ++u) {                                       /* :142-145 */
+        const int e = used[u / MI], j = u % MI;
+        const orc_mat* W13 = &y->w13[e];
+        const float sg = row_f32(W13, wt, (size_t)(2 * j), H, wg);
+        const float su = row_f32(W13, wt, (size_t)(2 * j + 1), H, wu);
+        for (int q = pe[e]; q < pe[e + 1]; ++q) {
+          const int i = pr[q];
+          const float* xb = xs + (size_t)(i / K) * H;
+          const float g = bfr(row_dot(wg, sg, wt, xb, H));
+          const float up = bfr(row_dot(wu, su, wt, xb, H));
+          hb[(size_t)i * MI + j] = bfr(bfr(silu(g)) * up);
+        }
+      }
+#pragma omp for schedule(dynamic, 16)
+      for (int u = 0; u < nu * H; ++u) {                                        /* :146 */
+        const int e = used[u / H], r = u % H;
+        const float sd = row_f32(&y->w2[e], wt, (size_t)r, MI, wg);
+        for (int q = pe[e]; q < pe[e + 1]; ++q) {
+          const int i = pr[q];
+          ys[(size_t)i * H + r] = bfr(bfr(row_dot(wg, sd, wt, hb + (size_t)i * MI, MI)) * wts[i]);
+        }
+      }
+      free(wg);
+    }
+    for (int b = 0; b < n; ++b) {                                               /* :146-148 ascending expert id */
+      const int32_t* id = ids + (size_t)b * K;
+      int order[64];
+      for (int k = 0; k < K; ++k) order[k] = k;
+      for (int a = 1; a < K; ++a)
+        for (int q = a; q > 0 && id[order[q]] < id[order[q - 1]]; --q) { int z = order[q]; order[q] = order[q - 1]; order[q - 1] = z; }
+      float* x = X + (size_t)b * H;
+      for (int i = 0; i < H; ++i) {
+        float acc = 0.0f;
+        for (int k = 0; k < K; ++k) acc = bfr(acc + ys[((size_t)b * K + order[k]) * H + i]);
+        x[i] = bfr(x[i] + acc);
+      }
+    }
+    free(logits); free(ids); free(wts); free(pe); free(pr); free(fill); free(used); free(hb); free(ys);
+  } else {                                                                      /* :149-152 */
+    const int I = c->I;
+    float* hb = (float*)malloc(sizeof(float) * (size_t)n * I);
+#pragma omp parallel
+    {
+      float* wg = (float*)malloc(sizeof(float) * (size_t)H * 2);
+      float* wu = wg + H;
+#pragma omp for schedule(dynamic, 8)
+      for (int j = 0; j < I; ++j) {
+        const float sg = row_f32(&y->wgu, wt, (size_t)(2 * j), H, wg);
+        const float su = row_f32(&y->wgu, wt, (size_t)(2 * j + 1), H, wu);
+        for (int b = 0; b < n; ++b) {
+          const float* xb = xs + (size_t)b * H;
+          const float g = bfr(row_dot(wg, sg, wt, xb, H));
+          const float up = bfr(row_dot(wu, su, wt, xb, H));
+          hb[(size_t)b * I + j] = bfr(bfr(silu(g)) * up);
+        }
+      }
+      free(wg);
+    }
+    gemv_rows_multi(&y->wd, wt, H, I, hb, I, n, t, H);
+    for (size_t i = 0; i < (size_t)n * H; ++i) X[i] = bfr(X[i] + t[i]);
+    free(hb);
+  }
+  free(xs); free(qkv); free(o); free(t);
+}
+
+/* n rows: row r is sequence seqs[r]'s step with input token toks[r] at position pos[r]; its greedy token into out[r]
+ * (each equal to orc_step_seq of that row given the cache its earlier positions left).  Rows of one sequence must hold
+ * distinct positions; a row attends to every position of its sequence up to its own, including the positions of the
+ * other rows.  dump_x [n][L][H] residual after each layer, dump_ids / dump_wts [n][L][TOPK]; each may be NULL. */
+EXPORT int orc_step_rows(void* h, int n, const int32_t* seqs, const int32_t* toks, const int32_t* pos, int32_t* out,
+                         float* dump_x, int32_t* dump_ids, float* dump_wts) {
+  orc_model* m = (orc_model*)h; const orc_config* c = &m->c;
+  if (c->arch != 0 || n < 1) return 1;
+  const int H = c->H, V = c->V, L = c->L, K = c->TOPK > 0 ? c->TOPK : 1;
+  orc_row* rows = (orc_row*)malloc(sizeof(orc_row) * (size_t)n);
+  for (int r = 0; r < n; ++r) {
+    if (seqs[r] < 0 || seqs[r] >= m->batch || pos[r] < 0 || pos[r] >= c->max_ctx || toks[r] < 0 || toks[r] >= V) {
+      free(rows);
+      return 1;
+    }
+    rows[r].bt = m->btab + (size_t)seqs[r] * m->nbps;
+    rows[r].pos = pos[r];
+  }
+  float* X = (float*)malloc(sizeof(float) * (size_t)n * H);
+  for (int b = 0; b < n; ++b)
+    for (int i = 0; i < H; ++i) X[(size_t)b * H + i] = bf2f(m->embed[(size_t)toks[b] * H + i]);
+  for (int l = 0; l < L; ++l) {
+    layer_rows(m, l, X, n, rows, dump_ids ? dump_ids + (size_t)l * K : NULL, dump_wts ? dump_wts + (size_t)l * K : NULL,
+               L * K);
+    if (dump_x)
+      for (int b = 0; b < n; ++b) memcpy(dump_x + ((size_t)b * L + l) * H, X + (size_t)b * H, sizeof(float) * (size_t)H);
+  }
+  float* xs = (float*)malloc(sizeof(float) * (size_t)n * H);
+  for (int b = 0; b < n; ++b) rmsnorm(X + (size_t)b * H, NULL, H, c->eps, xs + (size_t)b * H);   /* :155 */
+  /* lm_head rows against every row's vector, argmax (first maximum) per row, rows split over the threads */
+  const int nt = omp_get_max_threads();
+  float* bv = (float*)malloc(sizeof(float) * (size_t)nt * n);
+  int* bi = (int*)malloc(sizeof(int) * (size_t)nt * n);
+#pragma omp parallel
+  {
+    const int tid = omp_get_thread_num(), nth = omp_get_num_threads();
+    float* wf = (float*)malloc(sizeof(float) * (size_t)H * ORC_TR);
+    for (int b = 0; b < n; ++b) { bv[(size_t)tid * n + b] = -INFINITY; bi[(size_t)tid * n + b] = -1; }
+    const int r0 = (int)((int64_t)V * tid / nth), r1 = (int)((int64_t)V * (tid + 1) / nth);
+    const orc_mat lm = {m->lm_head, NULL, NULL};
+    for (int rt = r0; rt < r1; rt += ORC_TR) {                                  /* :157-158 */
+      const int nr = r1 - rt < ORC_TR ? r1 - rt : ORC_TR;
+      for (int i = 0; i < nr; ++i) row_f32(&lm, 0, (size_t)(rt + i), H, wf + (size_t)i * H);
+      for (int b = 0; b < n; ++b)
+        for (int i = 0; i < nr; ++i) {                /* rows ascending within the thread's range */
+          const float v = bfr(dot64f(wf + (size_t)i * H, xs + (size_t)b * H, H));
+          if (bi[(size_t)tid * n + b] < 0 || v > bv[(size_t)tid * n + b]) { bv[(size_t)tid * n + b] = v; bi[(size_t)tid * n + b] = rt + i; }
+        }
+    }
+    free(wf);
+  }
+  for (int b = 0; b < n; ++b) {                    /* threads hold ascending row ranges: the first maximum wins */
+    int best = -1; float v = -INFINITY;
+    for (int t = 0; t < nt; ++t) {
+      const int i = bi[(size_t)t * n + b];
+      if (i >= 0 && (best < 0 || bv[(size_t)t * n + b] > v)) { v = bv[(size_t)t * n + b]; best = i; }
+    }
+    out[b] = best < 0 ? 0 : best;
+  }
+  free(rows); free(X); free(xs); free(bv); free(bi);
+  return 0;
+}
+
+/* positions pos0 .. pos0+n-1 of sequence `seq` with input tokens toks[0..n): n rows of one sequence */
+EXPORT int orc_prefill_seq(void* h, int seq, const int32_t* toks, int pos0, int n, int32_t* out) {
+  if (n < 1) return 1;
+  int32_t* seqs = (int32_t*)malloc(sizeof(int32_t) * (size_t)n);
+  int32_t* pos = (int32_t*)malloc(sizeof(int32_t) * (size_t)n);
+  for (int b = 0; b < n; ++b) { seqs[b] = seq; pos[b] = pos0 + b; }
+  const int r = orc_step_rows(h, n, seqs, toks, pos, out, NULL, NULL, NULL);
+  free(seqs);
+  free(pos);
+  return r;
+}
+
 /* ref_numpy.py:105-158 Ref.step for sequence `seq` of the batch: token at position pos -> greedy next token.
  * The sequences of a batch share the weights and nothing else, so a batched step is this, once per sequence.
  * dump_x [L][H] residual after each layer; dump_ids/dump_wts [L][TOPK]; each may be NULL. */
@@ -835,7 +1210,7 @@ static inline float dot64_pad(const orc_mat* m, int wdtype, size_t r, const floa
   for (int l = 0; l < 64; ++l) acc[l] = 0.0f;
   for (int k0 = 0; k0 < K; k0 += 64)
     for (int l = 0; l < 64; ++l) {
-      const float w = wdtype == 0 ? bf2f(m->w[r * K + k0 + l]) : e4m3_to_f32(m->q[r * K + k0 + l]);
+      const float w = wdtype == 0 ? bf2f(m->w[r * K + k0 + l]) : e4m3_f(m->q[r * K + k0 + l]);
       acc[l] = fmaf(w, x[k0 + l], acc[l]);
     }
   for (int l = 0; l < 64; ++l) acc[l] = fmaf(0.0f, 0.0f, acc[l]);

@@ -101,6 +101,9 @@ def lib():
             "orc_weight": (C.POINTER(C.c_uint16), [C.c_void_p, C.c_int, C.c_int, C.c_int]),
             "orc_num_threads": (C.c_int, []),
             "orc_materialize_experts": (None, [C.c_void_p]),
+            "orc_prefill_seq": (C.c_int, [C.c_void_p, C.c_int, i32p, C.c_int, C.c_int, i32p]),
+            "orc_step_rows": (C.c_int, [C.c_void_p, C.c_int, i32p, i32p, i32p, i32p, C.c_void_p, C.c_void_p,
+                                        C.c_void_p]),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)
@@ -277,6 +280,38 @@ class OracleModel:
 
     def materialize_experts(self):
         lib().orc_materialize_experts(self._h)
+
+    def step_rows(self, seqs, tokens, positions, dump: bool = False):
+        """Rows of decode steps computed together, every weight row read once for all of them (Qwen3 architecture):
+        row r is sequence seqs[r]'s step with token tokens[r] at position positions[r].  Rows of distinct sequences
+        are one batched step; each row's result equals step(tokens[r], positions[r], seq=seqs[r]).  Returns the
+        greedy tokens [n], and with dump the residuals [n][L][H], top-k ids and weights [n][L][TOPK]."""
+        c = self.cfg
+        sq = np.ascontiguousarray(np.asarray(seqs, np.int32).reshape(-1))
+        tk = np.ascontiguousarray(np.asarray(tokens, np.int32).reshape(-1))
+        ps = np.ascontiguousarray(np.asarray(positions, np.int32).reshape(-1))
+        n = len(sq)
+        if len(tk) != n or len(ps) != n or n < 1:
+            raise ValueError("step_rows needs one sequence, token and position per row")
+        out = np.zeros(n, np.int32)
+        k = max(c["TOPK"], 1)
+        x = np.empty((n, c["L"], c["H"]), np.float32) if dump else None
+        ids = np.zeros((n, c["L"], k), np.int32) if dump else None
+        w = np.zeros((n, c["L"], k), np.float32) if dump else None
+        ptr = (lambda a: a.ctypes.data if a is not None else None)
+        if lib().orc_step_rows(self._h, n, sq, tk, ps, out, ptr(x), ptr(ids), ptr(w)) != 0:
+            raise ValueError("oracle step_rows refused (architecture, sequence, position or token out of range)")
+        return (out, x, ids, w) if dump else out
+
+    def prefill(self, tokens, pos0: int, seq: int = 0) -> np.ndarray:
+        """Positions pos0 .. pos0+n-1 of sequence `seq` with input tokens `tokens` (n of them), computed with every
+        weight row read once for the n positions: the KV cache afterwards and the returned greedy token of every
+        position equal n step() calls (Qwen3 architecture)."""
+        toks = np.ascontiguousarray(np.asarray(tokens, np.int32).reshape(-1))
+        out = np.zeros(len(toks), np.int32)
+        if lib().orc_prefill_seq(self._h, int(seq), toks, int(pos0), len(toks), out) != 0:
+            raise ValueError(f"oracle prefill of {len(toks)} positions at {pos0} refused")
+        return out
 
     def layer_step(self, layer: int, x: np.ndarray, pos: int, seq: int = 0):
         c = self.cfg

@@ -1,6 +1,7 @@
 """GPU parity of the batched step (etxmk_step_batch): B sequences at their own positions, with their own token rows
 and block-table rows into one paged-KV pool, decoded by one persistent launch per step.  Each sequence is compared
-with the CPU oracle's single-sequence step (a batched oracle holds the same pool): per-layer residuals bit for bit
+with the CPU oracle's step of that sequence (a batched oracle holds the same pool and computes the batch's rows in one
+pass over the weights, each row equal to its single-sequence step): per-layer residuals bit for bit
 (the 2e-2 gate reported), top-k ids and weights exactly, greedy tokens identical, and the whole pool's K and V
 caches bit for bit."""
 import sys
@@ -71,15 +72,15 @@ def run_contexts(cfg, ctx, n_steps, shuffle=False, check_every=1, pool=True):
         d = dec.dumps() if check else None
         if d is not None and B == 1:                        # single-sequence handles dump [layer][...]
             d = {k: v[:, None] for k, v in d.items()}
+        # the oracle's batched step: every sequence's row in one pass over the weights (each row equals the
+        # single-sequence step, tests/test_oracle_prefill.py)
+        r = orc.step_rows(list(range(B)), [toks[b][-1] for b in range(B)], pos, dump=check)
         for b in range(B):
             if check:
-                t, xo, ido, wo = orc.step(toks[b][-1], int(pos[b]), dump=True, seq=b)
-                check_layers(cfg, d, b, xo, ido, wo, f"step {s} sequence {b} (position {pos[b]})")
-            else:
-                t = orc.step(toks[b][-1], int(pos[b]), seq=b)
-            toks[b].append(t)
-            if cfg.L > 2:
-                say(f"[gpu]   step {s} sequence {b}: oracle token {t} ({time.time() - t0:.0f}s)")
+                check_layers(cfg, d, b, r[1][b], r[2][b], r[3][b], f"step {s} sequence {b} (position {pos[b]})")
+            toks[b].append(int(r[0][b] if check else r[b]))
+        if cfg.L > 2:
+            say(f"[gpu]   step {s}: oracle tokens {[tk[-1] for tk in toks]} ({time.time() - t0:.0f}s)")
         pos += 1
     dec.sync()
     for b in range(B):

@@ -168,51 +168,82 @@ def test_qwen3_30b_a3b_two_layers(gpu):
     run_and_compare(cfg, prompt_len=6, n_new=6, check_every=3)
 
 
-def _full_greedy(cfg, prompt_len, n_new, seed=SEED):
-    """Full-depth model: the prompt fed token by token, then greedy steps; every token and the last step's
-    per-layer residuals and top-k against the oracle."""
+def _full_prompt_decode(cfg, rows, prompt_len=1024, n_new=32, seed=SEED):
+    """The benchmarked workload at full depth: a seeded prompt of prompt_len token ids read through etxmk_prefill
+    launches of `rows` positions (what bench.py times before its decode steps), then n_new greedy tokens (31 decode
+    steps after the prompt's last position).  Against the oracle, which reads the same prompt with every position
+    computed as a decode step (examples/llm/host.hip:203-229 feeds the prompt token by token and gates on 32 tokens):
+    the greedy token of every prompt position, the n_new generated tokens, every layer's paged K/V cache, and the
+    first and last decode steps' per-layer residuals, top-k ids and weights."""
     import time
+    cfg = configs.with_layers(cfg, cfg.L, prefill=rows)
     t0 = time.time()
     dec, orc = make_pair(cfg, seed=seed)
+    dec.sync()
     say(f"[gpu]   weights ready in {time.time() - t0:.1f}s")
-    dec.enable_dumps(True)
     prompt = O.gen_tokens(seed, prompt_len, cfg.V)
-    got = dec.generate(prompt, n_new)
-    d = dec.dumps()
-    seq = list(prompt)
-    for pos in range(prompt_len + n_new - 1):
-        last = pos == prompt_len + n_new - 2
-        if last:
-            tok, xo, ido, wo = orc.step(seq[pos], pos, dump=True)
-        else:
-            tok = orc.step(seq[pos], pos)
-        if pos + 1 >= prompt_len:
-            seq.append(tok)
-    ref = seq[prompt_len:]
-    say(f"[gpu]   oracle done in {time.time() - t0:.1f}s; tokens {list(got)[:8]}...")
-    match = sum(int(a == b) for a, b in zip(got, ref))
-    worst = max(rel(d["x"][L], xo[L]) for L in range(cfg.L))
-    assert match == n_new, f"{match}/{n_new} greedy tokens identical"
-    assert worst < 2e-2, f"per-layer max rel {worst:.3e}"
-    for L in range(cfg.L):
-        assert np.array_equal(d["x"][L], xo[L]), f"layer {L}: residual differs (max rel {rel(d['x'][L], xo[L]):.3e})"
-        if cfg.moe:
-            assert np.array_equal(d["ids"][L], ido[L]), f"layer {L}: top-k ids differ"
-    orc.close()
+    P = prompt_len
+    dec.set_tokens(prompt)
+    dec.feed_prompt(P, rows=rows)
+    dec.sync()
+    g_prompt = dec.read_tokens(P)
+    dec.enable_dumps(True)
+    dec.step(P, write_next=True)
+    d_first = dec.dumps()
+    for pos in range(P + 1, P + n_new - 2):
+        dec.step(pos, write_next=True)
+    dec.step(P + n_new - 2, write_next=True)
+    d_last = dec.dumps()
+    got = dec.read_tokens(P + n_new - 1)[P - 1:]
+    kv_gpu = [dec.kv_layer(L) for L in range(cfg.L)]
     dec.close()
+    say(f"[gpu]   GPU done in {time.time() - t0:.1f}s; tokens {list(got)[:8]}...")
+    t1 = time.time()
+    o_prompt = np.concatenate([orc.prefill(prompt[p0:p0 + 256], p0) for p0 in range(0, P, 256)])
+    say(f"[gpu]   oracle prompt done in {time.time() - t1:.1f}s")
+    ref = [int(o_prompt[-1])]
+    dumps = {}
+    for pos in range(P, P + n_new - 1):
+        if pos in (P, P + n_new - 2):
+            tok, xo, ido, wo = orc.step(ref[-1], pos, dump=True)
+            dumps[pos] = (xo, ido, wo)
+        else:
+            tok = orc.step(ref[-1], pos)
+        ref.append(tok)
+    say(f"[gpu]   oracle done in {time.time() - t1:.1f}s")
+    bad = np.flatnonzero(g_prompt != o_prompt)
+    assert bad.size == 0, f"prompt positions {bad[:8]} ({bad.size} of {P}): greedy tokens differ"
+    match = sum(int(a == b) for a, b in zip(got, ref))
+    assert match == n_new, f"{match}/{n_new} greedy tokens identical"
+    for pos, d in ((P, d_first), (P + n_new - 2, d_last)):
+        xo, ido, wo = dumps[pos]
+        worst = max(rel(d["x"][L], xo[L]) for L in range(cfg.L))
+        assert worst < 2e-2, f"pos {pos}: per-layer max rel {worst:.3e}"
+        for L in range(cfg.L):
+            assert np.array_equal(d["x"][L], xo[L]), f"pos {pos} layer {L}: residual differs (max rel {rel(d['x'][L], xo[L]):.3e})"
+            if cfg.moe:
+                assert np.array_equal(d["ids"][L], ido[L]), f"pos {pos} layer {L}: top-k ids differ"
+                assert np.array_equal(d["w"][L], wo[L]), f"pos {pos} layer {L}: top-k weights differ"
+    for L in range(cfg.L):
+        ko, vo = orc.kv(L)
+        assert np.array_equal(kv_gpu[L][0], ko), f"layer {L}: paged K cache differs"
+        assert np.array_equal(kv_gpu[L][1], vo), f"layer {L}: paged V cache differs"
+    orc.close()
 
 
 @pytest.mark.timeout(900)
-def test_qwen3_30b_a3b_full_greedy_32(gpu):
-    """BASELINE configs[2] at full depth: 48 layers, 128 experts, vocab 151936; 32 greedy tokens identical."""
+def test_qwen3_30b_a3b_prompt1024_greedy_32(gpu):
+    """BASELINE configs[2], the headline workload at full depth: 48 layers, 128 experts top-8, vocab 151936; a
+    1024-token prompt through 16-position prefill launches, then 32 greedy tokens, all against the oracle."""
     cfg = configs.QWEN3_30B_A3B
-    say(f"[gpu] full {cfg.name}: 32-token prompt + 32 greedy")
-    _full_greedy(cfg, prompt_len=32, n_new=32)
+    say(f"[gpu] full {cfg.name}: 1024-token prompt (16-row prefill) + 32 greedy")
+    _full_prompt_decode(cfg, rows=16)
 
 
 @pytest.mark.timeout(900)
-def test_qwen3_8b_full_greedy_32(gpu):
-    """BASELINE configs[1] at full depth: 36 dense layers, vocab 151936; 32 greedy tokens identical."""
+def test_qwen3_8b_prompt1024_greedy_32(gpu):
+    """BASELINE configs[1] at full depth: 36 dense layers, vocab 151936; a 1024-token prompt through 4-position
+    prefill launches, then 32 greedy tokens, all against the oracle."""
     cfg = configs.QWEN3_8B
-    say(f"[gpu] full {cfg.name}: 32-token prompt + 32 greedy")
-    _full_greedy(cfg, prompt_len=32, n_new=32)
+    say(f"[gpu] full {cfg.name}: 1024-token prompt (4-row prefill) + 32 greedy")
+    _full_prompt_decode(cfg, rows=4)
