@@ -9,7 +9,9 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <chrono>
 #include <initializer_list>
+#include <thread>
 #include <vector>
 
 #include "etxmk.h"
@@ -58,6 +60,7 @@ int fail(int code, const char* fmt, ...) {
   } while (0)
 
 constexpr uint64_t ALIGN = 256;
+constexpr uint64_t SPIN_TICKS_DEFAULT = 200000000ull;   // 2 s of the 100 MHz s_memrealtime clock
 inline uint64_t align_up(uint64_t v) { return (v + ALIGN - 1) & ~(ALIGN - 1); }
 
 struct TensorSlot {
@@ -431,6 +434,10 @@ struct etxmk_handle {
   float* dump_logits = nullptr;
   uint64_t* trace = nullptr;
   std::vector<int32_t> btab_host;
+  int32_t* stop_host = nullptr;          // pinned, device-mapped host word: nonzero asks a running step to stop
+  int32_t* stop_dev = nullptr;           // its device address
+  uint64_t spin_ticks = SPIN_TICKS_DEFAULT;
+  uint32_t poll_mask = 255;
 
   const TensorSlot* slot(int kind, int layer) const {
     for (const auto& s : slots)
@@ -504,11 +511,22 @@ int etxmk_create(const etxmk_config* cfg, etxmk_handle** out) {
     return fail(ETXMK_EHIP, "no HIP device");
   }
   h->nwg = h->ncu;
+  // the host's stop word lives in pinned host memory mapped into the device's address space, so the host can set it
+  // with a plain store while a persistent launch holds every CU (a copy or fill would need a queue slot behind it)
+  if (hipHostMalloc((void**)&h->stop_host, 4, hipHostMallocMapped) != hipSuccess ||
+      hipHostGetDevicePointer((void**)&h->stop_dev, h->stop_host, 0) != hipSuccess) {
+    if (h->stop_host) (void)hipHostFree(h->stop_host);
+    delete h;
+    return fail(ETXMK_EHIP, "pinned stop word: %s", hipGetErrorString(hipGetLastError()));
+  }
+  __atomic_store_n(h->stop_host, 0, __ATOMIC_SEQ_CST);
   *out = h;
   return ETXMK_OK;
 }
 
 int etxmk_destroy(etxmk_handle* h) {
+  if (!h) return ETXMK_OK;
+  if (h->stop_host) (void)hipHostFree(h->stop_host);
   delete h;
   return ETXMK_OK;
 }
@@ -883,7 +901,9 @@ static int launch(etxmk_handle* h, const int32_t* posv, int pos, int write_next,
   p.trace = h->fused && !pf ? h->trace : nullptr;   // the stamp buffer is sized for the handle's step kernel
   p.pos = batched ? 0 : pos; p.write_next = write_next; p.l0 = l0; p.l1 = l1; p.do_embed = embed; p.do_head = head;
   p.nwg = h->nwg;
-  p.spin_ticks = 200000000ull;            // 2 s of the 100 MHz s_memrealtime clock
+  p.spin_ticks = h->spin_ticks;
+  p.poll_mask = h->poll_mask;
+  p.host_stop = h->stop_dev;
   {  // a workgroup's QKV rows: staged in LDS a layer ahead as far as the stage holds them, the rest (rows of 4096
      // only, up to two per wave) loaded into registers before the QKV phase's wait
     const int rows = nqkv_of(c), R = (rows + h->nwg - 1) / h->nwg;
@@ -1000,9 +1020,44 @@ int etxmk_step_layers(etxmk_handle* h, int32_t pos, int32_t l0, int32_t l1, void
   return launch(h, nullptr, pos, 0, l0, l1, 0, 0, (hipStream_t)stream);
 }
 
-int etxmk_sync(etxmk_handle* h, void* stream) {
+int etxmk_abort(etxmk_handle* h) {
+  if (!h) return fail(ETXMK_EINVAL, "NULL handle");
+  __atomic_store_n(h->stop_host, 1, __ATOMIC_SEQ_CST);
+  return ETXMK_OK;
+}
+
+int etxmk_set_spin_limit(etxmk_handle* h, uint64_t ticks, int32_t check_every) {
+  if (!h) return fail(ETXMK_EINVAL, "NULL handle");
+  if (check_every == 0) check_every = 256;
+  if (check_every < 1 || check_every > 256 || (check_every & (check_every - 1)))
+    return fail(ETXMK_EINVAL, "check_every %d is not a power of two in 1..256", check_every);
+  h->spin_ticks = ticks ? ticks : SPIN_TICKS_DEFAULT;
+  h->poll_mask = (uint32_t)check_every - 1u;
+  return ETXMK_OK;
+}
+
+int etxmk_sync_timeout(etxmk_handle* h, void* stream, int64_t timeout_ms) {
   if (!h || !h->wsp) return fail(ETXMK_EUNBOUND, "handle not bound");
-  HIPCHK(hipStreamSynchronize((hipStream_t)stream));
+  hipStream_t st = (hipStream_t)stream;
+  bool timed_out = false;
+  if (timeout_ms >= 0) {
+    // poll the stream; past the limit ask the running step to stop (its waits read the stop word) and let it drain
+    const auto t0 = std::chrono::steady_clock::now();
+    for (;;) {
+      const hipError_t q = hipStreamQuery(st);
+      if (q == hipSuccess) break;
+      if (q != hipErrorNotReady) return fail(ETXMK_EHIP, "hipStreamQuery: %s", hipGetErrorString(q));
+      if (std::chrono::steady_clock::now() - t0 >= std::chrono::milliseconds(timeout_ms)) {
+        timed_out = true;
+        __atomic_store_n(h->stop_host, 1, __ATOMIC_SEQ_CST);
+        break;
+      }
+      std::this_thread::yield();
+    }
+  }
+  const hipError_t e = hipStreamSynchronize(st);
+  __atomic_store_n(h->stop_host, 0, __ATOMIC_SEQ_CST);   // the stream has drained: no step can read it any more
+  if (e != hipSuccess) return fail(ETXMK_EHIP, "hipStreamSynchronize: %s", hipGetErrorString(e));
   int32_t ab = 0;
   HIPCHK(hipMemcpy(&ab, h->wsp + h->ws.abort_w, 4, hipMemcpyDeviceToHost));
   if (ab) {
@@ -1010,10 +1065,18 @@ int etxmk_sync(etxmk_handle* h, void* stream) {
     HIPCHK(hipMemset(h->wsp + h->ws.bar, 0, 4 * 64 * 17));
     HIPCHK(hipMemset(h->wsp + h->ws.acnt, 0, acnt_bytes(h->c)));
     h->bar_epoch = 0;
+    if (timed_out)
+      return fail(ETXMK_TIMEOUT, "the stream was still running after %lld ms; the step was stopped (abort word %d)",
+                  (long long)timeout_ms, ab);
     return fail(ETXMK_ABORTED, "device abort word %d (%s)", ab,
-                ab == 2 ? "a grid barrier wait exceeded its limit" : ab == 3 ? "no finite logit in the head" : "host abort");
+                ab == 2 ? "a grid barrier wait exceeded its limit" : ab == 3 ? "no finite logit in the head" : "host stop");
   }
+  if (timed_out)   // the step finished on its own before any wait saw the stop request: its results stand
+    return fail(ETXMK_TIMEOUT, "the stream was still running after %lld ms (it completed before the stop was seen)",
+                (long long)timeout_ms);
   return ETXMK_OK;
 }
+
+int etxmk_sync(etxmk_handle* h, void* stream) { return etxmk_sync_timeout(h, stream, -1); }
 
 }  // extern "C"

@@ -72,6 +72,7 @@ struct Params {
   uint64_t* amax;
   uint32_t* bar;
   int32_t* abort_word;
+  const int32_t* host_stop;             // the host's stop request (pinned host memory; etxmk_abort / a sync timeout)
   int32_t* tokens;
   int32_t* out_tokens;
   float* dump_x;
@@ -85,6 +86,7 @@ struct Params {
   uint32_t bar_base;
   int nwg;
   uint64_t spin_ticks;
+  uint32_t poll_mask;                   // a waiting workgroup checks the abort and stop words when (polls & mask) == 0
   // batched steps: per-sequence activations are [B][...] rows of the buffers above; tokens / out_tokens rows are
   // tok_stride long; btab rows nbps long; amax entries 256 bytes apart
   int B, nbps, tok_stride;
@@ -161,7 +163,9 @@ __device__ __forceinline__ int wave_u() { return __builtin_amdgcn_readfirstlane(
 // Visibility: every value another workgroup reads is written with an agent-scope (sc1) store and read with an
 // agent-scope load; each wave waits for its own stores to complete (s_waitcnt 0) before the workgroup barrier
 // that precedes the arrival, so no L2 write-back or invalidate is needed.  The wait is bounded by a wall-clock
-// limit; on expiry the abort word is set and every workgroup leaves.
+// limit; on expiry the abort word is set and every workgroup leaves.  Every 256 polls (poll_mask + 1) a waiting
+// workgroup also checks the clock, the abort word and the host's stop word: either makes it leave, and a stop request is copied into the abort word so
+// the rest of the grid leaves at its next check.
 template <class S>
 __device__ __forceinline__ void grid_arrive(const Params& p, int& k, S& s) {
   __builtin_amdgcn_s_waitcnt(0);
@@ -194,8 +198,13 @@ __device__ __forceinline__ bool grid_wait(const Params& p, int k, S& s) {
     uint32_t polls = 0;
     while ((int32_t)(__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - gen) < 0) {
       __builtin_amdgcn_s_sleep(1);
-      if ((++polls & 255u) == 0) {
+      if ((++polls & p.poll_mask) == 0) {
         if (ld_ag_i(p.abort_word) != 0) { ab = 1; break; }
+        if (p.host_stop && ld_sys_i(p.host_stop) != 0) {   // the host asked the step to stop: tell the grid
+          st_ag_i(p.abort_word, 1);
+          ab = 1;
+          break;
+        }
         if (__builtin_amdgcn_s_memrealtime() - t0 > p.spin_ticks) {
           st_ag_i(p.abort_word, 2);
           ab = 1;

@@ -202,6 +202,10 @@ __device__ __forceinline__ int32_t ld_ag_i(const int32_t* p) {
 __device__ __forceinline__ void st_ag_i(int32_t* p, int32_t v) {
   __hip_atomic_store((MK_G int32_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// system-scope load of a word the host writes (pinned, device-mapped host memory)
+__device__ __forceinline__ int32_t ld_sys_i(const int32_t* p) {
+  return __hip_atomic_load((const MK_G int32_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
 __device__ __forceinline__ uint16_t ld_ag_u16(const uint16_t* p) {
   return __hip_atomic_load((const MK_G uint16_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }

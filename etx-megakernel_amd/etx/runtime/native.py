@@ -19,8 +19,8 @@ PKG = Path(__file__).resolve().parents[2]
 LIB_PATH = PKG / "lib" / "libetxmk.so"
 HEADER = PKG.parent / "include" / "etxmk.h"
 
-ABI_VERSION = 2
-OK, EINVAL, EHIP, ABORTED, EUNBOUND = 0, 1, 2, 3, 4
+ABI_VERSION = 3
+OK, EINVAL, EHIP, ABORTED, EUNBOUND, TIMEOUT = 0, 1, 2, 3, 4, 5
 T_EMBED, T_LMHEAD, T_WQKV, T_WO, T_ROUTER, T_W13, T_W2, T_WGU, T_WD = 1, 2, 3, 4, 5, 6, 7, 8, 9
 T_LN1, T_LN2, T_QNORM, T_KNORM, T_FINAL_NORM = 20, 21, 22, 23, 24
 T_WKVB, T_WSGU, T_WSD = 14, 15, 16             # DeepSeek-V2: kv_b_proj, shared experts' gate/up and down
@@ -34,6 +34,10 @@ class EtxmkError(RuntimeError):
 
 class DeviceAbort(EtxmkError):
     pass
+
+
+class StepTimeout(EtxmkError):
+    """etxmk_sync_timeout: the stream outlived the limit; a stopped step's outputs are void."""
 
 
 class EtxmkConfig(C.Structure):
@@ -127,10 +131,8 @@ def load(path: Path | None = None):
     global _lib
     if _lib is not None and path is None:
         return _lib
-    # ETXMK_LIB names another build of the same library (for instance an instrumented one)
     import torch  # noqa: F401  (binds libamdhip64 before the library resolves it)
-    import os
-    p = Path(path or os.environ.get("ETXMK_LIB") or LIB_PATH)
+    p = Path(path or LIB_PATH)
     if not p.exists():
         raise FileNotFoundError(f"{p} is not built; run etx-megakernel_amd/build_lib.py (no fallback path exists)")
     L = C.CDLL(str(p))
@@ -162,6 +164,9 @@ def load(path: Path | None = None):
         "etxmk_set_residual": [vp, C.POINTER(C.c_float), vp],
         "etxmk_read_residual": [vp, C.POINTER(C.c_float), vp],
         "etxmk_sync": [vp, vp],
+        "etxmk_sync_timeout": [vp, vp, C.c_int64],
+        "etxmk_abort": [vp],
+        "etxmk_set_spin_limit": [vp, u64, i32],
         "etxmk_set_fused": [vp, i32],
         "etxmk_set_dump": [vp, vp, vp, vp, vp],
         "etxmk_set_grid": [vp, i32],
@@ -185,6 +190,8 @@ def _check(L, rc: int):
         msg = L.etxmk_last_error().decode(errors="replace")
         if rc == ABORTED:
             raise DeviceAbort(rc, msg)
+        if rc == TIMEOUT:
+            raise StepTimeout(rc, msg)
         raise EtxmkError(rc, msg)
 
 
@@ -440,8 +447,20 @@ class Decoder:
         _check(self.L, self.L.etxmk_read_residual(self.h, x.ctypes.data_as(C.POINTER(C.c_float)), self._stream()))
         return x
 
-    def sync(self):
-        _check(self.L, self.L.etxmk_sync(self.h, self._stream()))
+    def sync(self, timeout_ms: int | None = None):
+        """Wait for the handle's work; with timeout_ms, stop a step still running past it (StepTimeout)."""
+        if timeout_ms is None:
+            _check(self.L, self.L.etxmk_sync(self.h, self._stream()))
+        else:
+            _check(self.L, self.L.etxmk_sync_timeout(self.h, self._stream(), int(timeout_ms)))
+
+    def abort(self):
+        """Ask the running (or next) step to stop; the next sync raises DeviceAbort."""
+        _check(self.L, self.L.etxmk_abort(self.h))
+
+    def set_spin_limit(self, ticks: int = 0, check_every: int = 0):
+        """Bounds of the kernel's barrier waits (100 MHz ticks, 0 = default 2 s; check cadence in polls)."""
+        _check(self.L, self.L.etxmk_set_spin_limit(self.h, int(ticks), int(check_every)))
 
     def enable_trace(self, on: bool = True):
         """Per-phase, per-workgroup s_memrealtime stamps of the fused kernel; read with trace()."""

@@ -17,7 +17,7 @@
 extern "C" {
 #endif
 
-#define ETXMK_ABI_VERSION 2
+#define ETXMK_ABI_VERSION 3
 
 /* status codes */
 #define ETXMK_OK 0
@@ -25,6 +25,7 @@ extern "C" {
 #define ETXMK_EHIP 2            /* a HIP runtime call failed */
 #define ETXMK_ABORTED 3         /* the device spin limit fired or the host set the abort word */
 #define ETXMK_EUNBOUND 4        /* buffers not bound yet */
+#define ETXMK_TIMEOUT 5         /* etxmk_sync_timeout: the stream outlived the limit (the step was asked to stop) */
 
 /* tensor kinds (also the seeded generator's stream kinds: stream = kind << 48 | (layer + 1) << 24 | expert) */
 #define ETXMK_T_EMBED 1
@@ -176,8 +177,28 @@ int etxmk_set_residual(etxmk_handle* h, const float* x, void* stream);
 int etxmk_read_residual(etxmk_handle* h, float* x, void* stream);
 
 /* Wait for the stream and check the abort word (reference: etx_host::wait + after_wait,
- * etx/runtime/include/etx/host.h:351-417).  Returns ETXMK_ABORTED if the device gave up. */
+ * etx/runtime/include/etx/host.h:351-417).  Returns ETXMK_ABORTED if the device gave up; after an abort the
+ * barrier and attention counters are reset, so the next step runs normally (re-run the aborted position). */
 int etxmk_sync(etxmk_handle* h, void* stream);
+
+/* The host watchdog (reference: etx_host::wait_stream's poll loop, which writes ctrl_abort on timeout,
+ * etx/runtime/include/etx/host.h:351-376): polls the stream for up to timeout_ms (< 0: no limit); past the limit it
+ * sets the handle's stop word, which every grid-barrier wait of a running step reads (see etxmk_set_spin_limit), waits
+ * for the stream to drain and returns ETXMK_TIMEOUT (the stopped step's outputs are void; counters are reset as after
+ * an abort).  A step that is not stuck finishes before its waits look at the stop word: its results then stand, and
+ * the call still reports ETXMK_TIMEOUT for the missed limit.  Otherwise as etxmk_sync. */
+int etxmk_sync_timeout(etxmk_handle* h, void* stream, int64_t timeout_ms);
+
+/* Ask the running (or next) step of this handle to stop: sets the stop word in pinned host memory that its waits
+ * read; the step ends with ETXMK_ABORTED at the next etxmk_sync, which clears the word.  Reference: the host's write of
+ * ctrl_abort (etx/runtime/include/etx/host.h:366). */
+int etxmk_abort(etxmk_handle* h);
+
+/* Bounds of every grid-barrier wait (reference: etx_params.spin_limit, etx/runtime/include/etx/abi.h:102, set at
+ * etx/runtime/include/etx/host.h:199): a wait gives up after `ticks` of the 100 MHz clock (0: the default 2 s) and sets
+ * the abort word; it checks the clock, the abort word and the stop word once every `check_every` polls (a power of two
+ * up to 256; 0: 256).  Small values force the abort path on purpose (tests of the error handling). */
+int etxmk_set_spin_limit(etxmk_handle* h, uint64_t ticks, int32_t check_every);
 
 /* Execution mode: 1 = one persistent cooperative launch per step (the fused megakernel), 0 = one launch per
  * phase with the same device functions (reference: run_unfused, etx/runtime/include/etx/host.h:418-457). */

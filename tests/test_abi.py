@@ -14,7 +14,7 @@ def test_library_exports_every_declared_symbol():
     assert len(names) >= 20
     missing = [n for n in names if not hasattr(L, n)]
     assert not missing
-    assert L.etxmk_abi_version() == N.ABI_VERSION == 2
+    assert L.etxmk_abi_version() == N.ABI_VERSION == 3
 
 
 def test_sizes_of_real_configurations():
