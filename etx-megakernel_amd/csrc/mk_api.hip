@@ -11,6 +11,7 @@
 
 #include <chrono>
 #include <initializer_list>
+#include <mutex>
 #include <thread>
 #include <vector>
 
@@ -414,6 +415,44 @@ void yarn_tables(const etxmk_config& c, float* cs, float* sn) {
     }
 }
 
+// ---------------------------------------------------------------- allocation-free step (etxmk_step_static)
+// The scratch of a single-sequence step (activations, attention chunk partials, attention arrival counters, the argmax
+// key, the grid-barrier words) in one file-scope device array instead of the caller's workspace.  Each GPU the library
+// runs on holds its own copy until the process ends; its device address comes from hipGetSymbolAddress, taken once per
+// device with that device current (host code never uses the array's name as an address).
+constexpr uint64_t STATIC_SCRATCH_BYTES = 4ull << 20;
+constexpr int MAX_DEVICES = 64;
+
+struct StaticLayout {
+  uint64_t bar, acnt, amax, zero_end;     // counters first: [0, zero_end) is cleared by every call
+  uint64_t x, qkv, o, logits, hbuf, apart, total;
+};
+
+StaticLayout static_layout(const etxmk_config& c) {
+  StaticLayout w{};
+  uint64_t off = 0;
+  auto take = [&](uint64_t bytes) { const uint64_t o = off; off = align_up(off + bytes); return o; };
+  w.bar = take(4 * 64 * 17);
+  w.acnt = take(4ull * 64 * c.NKV);
+  w.amax = take(256);
+  w.zero_end = off;
+  const int hb = c.moe ? c.TOPK * c.MI : c.I;
+  w.x = take(4ull * c.H);
+  w.qkv = take(4ull * nqkv_of(c));
+  w.o = take(4ull * c.NH * c.HD);
+  w.logits = take(4ull * (c.E > 0 ? c.E : 1));
+  w.hbuf = take(4ull * (hb > 0 ? hb : 1));
+  w.apart = take(4ull * c.NH * MAX_CHUNKS * PART);
+  w.total = off;
+  return w;
+}
+
+// pointers of the step's scratch buffers when they do not come from the workspace
+struct ScratchView {
+  uint8_t* base;
+  StaticLayout lay;
+};
+
 }  // namespace
 
 struct etxmk_handle {
@@ -451,6 +490,28 @@ struct etxmk_handle {
   }
   int barriers(int l0, int l1, int head, bool batched) const { return barriers_of(c, l0, l1, head, batched); }
 };
+
+static __device__ __align__(256) uint8_t scratch[STATIC_SCRATCH_BYTES];
+
+namespace {
+std::mutex g_scratch_mu;
+uint8_t* g_scratch_ptr[MAX_DEVICES];
+
+// the calling thread's current device's copy of `scratch` (resolved on the first call on that device)
+int scratch_ptr(uint8_t** out) {
+  int dev = 0;
+  HIPCHK(hipGetDevice(&dev));
+  if (dev < 0 || dev >= MAX_DEVICES) return fail(ETXMK_EINVAL, "device %d outside 0..%d", dev, MAX_DEVICES - 1);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    HIPCHK(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+    g_scratch_ptr[dev] = (uint8_t*)ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return ETXMK_OK;
+}
+}  // namespace
 
 extern "C" {
 
@@ -838,8 +899,9 @@ int etxmk_barriers_per_step(etxmk_handle* h, int32_t* n) {
 }
 
 // pseq >= 0: prefill of sequence pseq, rows b = positions posv[0] + b (nrows of them)
+// sv: the step's scratch buffers come from sv (etxmk_step_static) instead of the workspace
 static int launch(etxmk_handle* h, const int32_t* posv, int pos, int write_next, int l0, int l1, int embed, int head,
-                  hipStream_t st, int pseq = -1, int nrows = 0) {
+                  hipStream_t st, int pseq = -1, int nrows = 0, const ScratchView* sv = nullptr) {
   if (!h || !h->wsp) return fail(ETXMK_EUNBOUND, "handle not bound");
   const etxmk_config& c = h->c;
   const bool ds = is_ds(c), pf = pseq >= 0;
@@ -953,9 +1015,21 @@ static int launch(etxmk_handle* h, const int32_t* posv, int pos, int write_next,
     if (!fn) return fail(ETXMK_EINVAL, "no persistent kernel for H %d, NH*HD %d, %s %d (use the unfused mode)", c.H,
                          c.NH * c.HD, c.moe ? "MI" : "I", c.moe ? c.MI : c.I);
     p.bar_base = h->bar_epoch;
+    if (sv) {                              // scratch outside the workspace; its counters were cleared just before
+      p.x = (float*)(sv->base + sv->lay.x);
+      p.qkv = (float*)(sv->base + sv->lay.qkv);
+      p.o = (float*)(sv->base + sv->lay.o);
+      p.logits = (float*)(sv->base + sv->lay.logits);
+      p.hbuf = (float*)(sv->base + sv->lay.hbuf);
+      p.apart = (float*)(sv->base + sv->lay.apart);
+      p.acnt = (uint32_t*)(sv->base + sv->lay.acnt);
+      p.amax = (uint64_t*)(sv->base + sv->lay.amax);
+      p.bar = (uint32_t*)(sv->base + sv->lay.bar);
+      p.bar_base = 0;
+    }
     void* args[] = {&p};
     HIPCHK(hipLaunchCooperativeKernel(fn, dim3(h->nwg), dim3(NT), args, 0, st));
-    h->bar_epoch += (uint32_t)h->barriers(l0, l1, head, batched);
+    if (!sv) h->bar_epoch += (uint32_t)h->barriers(l0, l1, head, batched);
   } else {
     auto ph = [&](int phase, int layer) -> int {
       static void (*const kern[])(Params, int) = {etxmk_p_qkv, etxmk_p_attn, etxmk_p_oproj, etxmk_p_router,
@@ -990,6 +1064,26 @@ static int launch(etxmk_handle* h, const int32_t* posv, int pos, int write_next,
 int etxmk_step(etxmk_handle* h, int32_t pos, int32_t write_next, void* stream) {
   if (!h) return fail(ETXMK_EINVAL, "NULL handle");
   return launch(h, nullptr, pos, write_next, 0, h->c.L, 1, 1, (hipStream_t)stream);
+}
+
+int etxmk_step_static(etxmk_handle* h, int32_t pos, int32_t write_next, void* stream) {
+  if (!h || !h->wsp) return fail(ETXMK_EUNBOUND, "handle not bound");
+  const etxmk_config& c = h->c;
+  if (c.batch != 1 || is_ds(c) || !h->fused)
+    return fail(ETXMK_EINVAL, "etxmk_step_static runs single-sequence Qwen3 handles in fused mode");
+  if (!fused_kernel(c)) return fail(ETXMK_EINVAL, "no persistent kernel for this shape");
+  ScratchView sv{};
+  sv.lay = static_layout(c);
+  if (sv.lay.total > STATIC_SCRATCH_BYTES)
+    return fail(ETXMK_EINVAL, "the step needs %llu bytes of scratch, above the %llu-byte static buffer",
+                (unsigned long long)sv.lay.total, (unsigned long long)STATIC_SCRATCH_BYTES);
+  if (int r = scratch_ptr(&sv.base)) return r;
+  hipStream_t st = (hipStream_t)stream;
+  // the counters must start at zero: a fill kernel (capturable), not a memset
+  const size_t n16 = sv.lay.zero_end / 2;
+  hipLaunchKernelGGL(etxmk_fill_u16, dim3(8), dim3(256), 0, st, (uint16_t*)(sv.base + sv.lay.bar), n16, (uint16_t)0);
+  HIPCHK(hipGetLastError());
+  return launch(h, nullptr, pos, write_next, 0, c.L, 1, 1, st, -1, 0, &sv);
 }
 
 int etxmk_step_batch(etxmk_handle* h, const int32_t* positions, int32_t write_next_mask, void* stream) {

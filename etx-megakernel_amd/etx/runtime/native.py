@@ -159,6 +159,7 @@ def load(path: Path | None = None):
         "etxmk_read_tokens_seq": [vp, i32, C.POINTER(i32), i32, vp],
         "etxmk_step": [vp, i32, i32, vp],
         "etxmk_step_batch": [vp, C.POINTER(i32), i32, vp],
+        "etxmk_step_static": [vp, i32, i32, vp],
         "etxmk_prefill": [vp, i32, i32, i32, i32, vp],
         "etxmk_step_layers": [vp, i32, i32, i32, vp],
         "etxmk_set_residual": [vp, C.POINTER(C.c_float), vp],
@@ -400,6 +401,10 @@ class Decoder:
 
     def step(self, pos: int, write_next: bool = True):
         _check(self.L, self.L.etxmk_step(self.h, pos, int(write_next), self._stream()))
+
+    def step_static(self, pos: int, write_next: bool = True):
+        """etxmk_step with its scratch in the library's static device array (no workspace scratch, no allocation)."""
+        _check(self.L, self.L.etxmk_step_static(self.h, pos, int(write_next), self._stream()))
 
     def step_batch(self, positions, write_next=True):
         """One step of every sequence; write_next: one flag for all, or one per sequence."""

@@ -152,6 +152,17 @@ int etxmk_read_tokens(etxmk_handle* h, int32_t* out_tokens, int32_t n, void* str
  * etx_megakernel_d0 (etx/codegen/kernel.py:471-605), after llm_set_params (examples/llm/tiles.hip:16-19). */
 int etxmk_step(etxmk_handle* h, int32_t pos, int32_t write_next, void* stream);
 
+/* etxmk_step without the workspace's scratch: no counterpart in the reference; for callers that cannot allocate or
+ * cannot hand the library a workspace's worth of scratch per handle (code under HIP graph capture, tight serving
+ * loops).  The step's scratch (activations, attention chunk partials and arrival counters, the argmax key, the
+ * grid-barrier words) lives in a static device array of at most 4 MiB per GPU, held until the process ends; the
+ * handle's bound buffers still provide the weights, the KV cache, the token rows (inputs and outputs), block table,
+ * RoPE tables and abort word.  Every call clears the array's counters with a fill kernel on `stream` first and calls no
+ * allocator.  Calls on one GPU share the array: calls that overlap on one GPU (other streams, other handles) race and
+ * must be ordered by the caller.  Single-sequence Qwen3 handles in fused mode; a shape whose scratch exceeds the
+ * array is refused with ETXMK_EINVAL.  Results are those of etxmk_step, bit for bit. */
+int etxmk_step_static(etxmk_handle* h, int32_t pos, int32_t write_next, void* stream);
+
 /* One decode step of every sequence of a batched handle, sequence b at position positions[b] (host array of
  * `batch` entries), in one persistent launch (fused mode only).  Bit b of write_next_mask: sequence b's greedy
  * token also goes to its tokens[positions[b] + 1] (clear while the sequence is still reading its prompt).
