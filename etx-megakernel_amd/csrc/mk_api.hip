@@ -358,7 +358,7 @@ WsLayout ws_layout(const etxmk_config* c) {
   w.hbuf = take(4ull * (hb > 0 ? hb : 1) * B);
   w.h16 = take(2ull * (hb > 0 ? hb : 1) * B);
   w.apart = take(4ull * c->NH * MAX_CHUNKS * (ds ? MLA_PART : PART) * B);
-  w.acnt = take(4ull * 64 * (ds ? ds_nhg(*c) : c->NKV) * B); // one 256-byte line per (sequence, kv head / head group)
+  w.acnt = take(4ull * 64 * 2 * (ds ? ds_nhg(*c) : c->NKV) * B); // one 256-byte line per (sequence, kv head / head group, half)
   w.amax = take(256ull * B);             // one 256-byte line per sequence
   w.bar = take(4 * 64 * 17);          // 8 group counters, 1 global counter, 8 release flags; 256 B apart
   w.abort_w = take(4);
@@ -381,7 +381,7 @@ WsLayout ws_layout(const etxmk_config* c) {
   return w;
 }
 
-uint64_t acnt_bytes(const etxmk_config& c) { return 4ull * 64 * (is_ds(c) ? ds_nhg(c) : c.NKV) * rows_of(c); }
+uint64_t acnt_bytes(const etxmk_config& c) { return 4ull * 64 * 2 * (is_ds(c) ? ds_nhg(c) : c.NKV) * rows_of(c); }
 
 // DeepseekV2YarnRotaryEmbedding tables (reference_decode.py:85-118) in the steps the reference's numpy takes in
 // float32: the correction range in double, the ramp, mask and inverse frequencies in float, then cos and sin of
@@ -433,7 +433,7 @@ StaticLayout static_layout(const etxmk_config& c) {
   uint64_t off = 0;
   auto take = [&](uint64_t bytes) { const uint64_t o = off; off = align_up(off + bytes); return o; };
   w.bar = take(4 * 64 * 17);
-  w.acnt = take(4ull * 64 * c.NKV);
+  w.acnt = take(4ull * 64 * 2 * c.NKV);
   w.amax = take(256);
   w.zero_end = off;
   const int hb = c.moe ? c.TOPK * c.MI : c.I;

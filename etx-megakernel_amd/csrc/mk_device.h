@@ -775,10 +775,11 @@ __device__ __forceinline__ void phase_qkv(const Params& p, int layer, Smem& s, W
       p.nwg, p.trace, s.phase);
 }
 
-// P2: per (kv head, 64-position chunk): q/k RMSNorm and neox RoPE of the group's heads (ref_numpy.py:116-120),
-// paged KV append by the chunk holding `pos` (:121), then per q head the chunk's scores, max, exp, sum and
-// probability-weighted V (:122-129 in chunked form).  The chunk partials (a[HD], m, l) go to global memory; the
-// last chunk of a kv head to arrive merges them in ascending chunk order and writes o.
+// P2: per (kv head, 64-position chunk, half of the group's q heads): q/k RMSNorm and neox RoPE of the item's heads
+// (ref_numpy.py:116-120), paged KV append by the first half's item of the chunk holding `pos` (:121), then per q
+// head the chunk's scores, max, exp, sum and probability-weighted V (:122-129 in chunked form).  The chunk partials
+// (a[HD], m, l) go to global memory; the last chunk of a (kv head, half) to arrive merges them in ascending chunk
+// order and writes o.
 // per-head RMSNorm of (a0, a1) = dims (lane, lane + 64) with weights (w0, w1)
 __device__ __forceinline__ void qk_norm(float& a0, float& a1, float w0, float w1, float eps) {
   float acc = __builtin_fmaf(a0, a0, 0.0f);
@@ -811,7 +812,12 @@ __device__ __forceinline__ void phase_attn(const Params& p, int layer, S& s, Wai
   constexpr int CPI = decltype(s.a)::cpi;
   const int NKV = p.NKV, NH = p.NH, G = NH / NKV, HD = HDIM, BS = p.BS;
   const int NQKV = (NH + 2 * NKV) * HD;
-  const int nitems = NKV * ((p.pos / CHUNK + CPI) / CPI);
+  // Items (kv head, chunk, half of the kv head's q heads): twice the workgroups of one item per (kv head, chunk),
+  // each computing on one wave per SIMD (the score and P.V chains are VALU-bound; with a whole group's heads two
+  // waves shared each SIMD), and half of the grid still free to stream the O projection's rows during the phase.
+  // Quarters (every workgroup an item at context 1024) left no workgroup to do that and were slower.
+  const int HS = (G % 2 == 0) ? 2 : 1, GH = G / HS;
+  const int nitems = HS * NKV * ((p.pos / CHUNK + CPI) / CPI);
   const LayerW Lw = layer_w(p, layer);
   const int lane = lane_id(), wave = wave_u();
   // The chunks' cached K and V go straight from HBM into LDS tiles (global_load_lds, 16 bytes per lane); they do
@@ -819,7 +825,7 @@ __device__ __forceinline__ void phase_attn(const Params& p, int layer, S& s, Wai
   // 2w, 2w+1 (lane = position) and the V position-group w (lane = dim, both halves) of every chunk of the item.
   // The current position is not read from the cache: it is patched into the tiles from the QKV row.
   auto load_kv = [&](int item) {
-    const AttnItem it = attn_item<B, CPI>(p, item);
+    const AttnItem it = attn_item<B, CPI>(p, item / HS);
     const int g = it.g, pos = it.pos, n = pos + 1, nch = (n + CHUNK - 1) / CHUNK, fp = pos;
     const int32_t* btab = p.btab + (size_t)it.b * p.nbps;
 #pragma unroll
@@ -855,7 +861,8 @@ __device__ __forceinline__ void phase_attn(const Params& p, int layer, S& s, Wai
   if ((int)blockIdx.x < nitems) load_kv(blockIdx.x);
   if (!wait()) return;
   for (int item = blockIdx.x; item < nitems; item += p.nwg) {
-    const AttnItem it = attn_item<B, CPI>(p, item);
+    const AttnItem it = attn_item<B, CPI>(p, item / HS);
+    const int half = item % HS, h0 = it.g * G + half * GH;   // this item's q heads h0 .. h0 + GH - 1
     const int g = it.g, pos = it.pos, n = pos + 1, nch = (n + CHUNK - 1) / CHUNK;
     const int c0 = it.cp * CPI, nc = min(CPI, nch - c0);   // chunks c0 .. c0 + nc - 1
     const int32_t* btab = p.btab + (size_t)it.b * p.nbps;
@@ -871,8 +878,8 @@ __device__ __forceinline__ void phase_attn(const Params& p, int layer, S& s, Wai
     // lane with v_readlane (wave-uniform operands, no LDS traffic for q or p)
     const int j = wave;
     float q0 = 0.0f, q1 = 0.0f;
-    if (j < G) {
-      const float* src = qkv + (size_t)(g * G + j) * HD;
+    if (j < GH) {
+      const float* src = qkv + (size_t)(h0 + j) * HD;
       float a0 = ld_ag(src + lane), a1 = ld_ag(src + lane + 64);
       if (p.qk_norm) qk_norm(a0, a1, qn0, qn1, p.eps);
       q0 = bfr(bfr(a0 * rc) + bfr(-a1 * rs));
@@ -914,7 +921,7 @@ __device__ __forceinline__ void phase_attn(const Params& p, int layer, S& s, Wai
           ((uint16_t*)&s.a.kt[ci][d / 8][tn])[d % 8] = f2bf(kn[u][h]);
           ((uint16_t*)&s.a.vt[ci][tn / 8][h][lane])[tn % 8] = f2bf(vn[u][h]);
         }
-        if (q == pos) {                                   // paged append (:121): K [blk][NKV][HD/8][BS][8], V [blk][NKV][HD][BS]
+        if (q == pos && half == 0) {                      // paged append (:121): K [blk][NKV][HD/8][BS][8], V [blk][NKV][HD][BS]
           const int blk = ld_i(btab + pos / BS), off = pos % BS;
 #pragma unroll
           for (int h = 0; h < 2; ++h) {
@@ -954,7 +961,7 @@ __device__ __forceinline__ void phase_attn(const Params& p, int layer, S& s, Wai
         }
       }
     };
-    if (j < G) {
+    if (j < GH) {
 #pragma unroll
       for (int ci = 0; ci < CPI; ++ci) {
         if (ci < nc) {
@@ -982,7 +989,7 @@ __device__ __forceinline__ void phase_attn(const Params& p, int layer, S& s, Wai
           float a0 = 0.0f, a1 = 0.0f, l = 0.0f;
           if (len == CHUNK) pv(ci, len, pr, std::true_type{}, a0, a1, l);
           else pv(ci, len, pr, std::false_type{}, a0, a1, l);
-          float* part = apart + ((size_t)(g * G + j) * MAX_CHUNKS + c) * PART;
+          float* part = apart + ((size_t)(h0 + j) * MAX_CHUNKS + c) * PART;
           st_ag(part + lane, a0);
           st_ag(part + lane + 64, a1);
           if (lane == 0) { st_ag(part + HD, m); st_ag(part + HD + 1, l); }
@@ -996,13 +1003,13 @@ __device__ __forceinline__ void phase_attn(const Params& p, int layer, S& s, Wai
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (threadIdx.x == 0) {
-      const uint32_t old = __hip_atomic_fetch_add(acnt + 64 * g, (uint32_t)nc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const uint32_t old = __hip_atomic_fetch_add(acnt + 64 * (g * HS + half), (uint32_t)nc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       s.last = (old + (uint32_t)nc == (uint32_t)nch);
     }
     __syncthreads();
     if (s.last) {
-      for (int j = wave; j < G; j += NWAVE) {
-        const float* part = apart + (size_t)(g * G + j) * MAX_CHUNKS * PART;
+      for (int j = wave; j < GH; j += NWAVE) {
+        const float* part = apart + (size_t)(h0 + j) * MAX_CHUNKS * PART;
         // lane cc holds chunks cc and cc + 64's (m, l); the chunk weights go through LDS for the ordered sums.  The
         // first MB chunks' a[] are loaded together with (m, l) (they do not depend on the maximum): one round trip.
         constexpr int MB = 18;
@@ -1039,10 +1046,10 @@ __device__ __forceinline__ void phase_attn(const Params& p, int layer, S& s, Wai
               A1 = __builtin_fmaf(wc, av1[u], A1);
             }
         }
-        st_ag(o + (size_t)(g * G + j) * HD + lane, bfr(A0 / Ls));
-        st_ag(o + (size_t)(g * G + j) * HD + lane + 64, bfr(A1 / Ls));
+        st_ag(o + (size_t)(h0 + j) * HD + lane, bfr(A0 / Ls));
+        st_ag(o + (size_t)(h0 + j) * HD + lane + 64, bfr(A1 / Ls));
       }
-      if (threadIdx.x == 0) __hip_atomic_store(acnt + 64 * g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (threadIdx.x == 0) __hip_atomic_store(acnt + 64 * (g * HS + half), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
   }
