@@ -182,10 +182,10 @@ def main_batch(a):
         f"{gbps:.1f} GB/s = {gbps / HBM_PEAK_GBPS:.3f} of 8 TB/s; expert union per MoE layer mean {umean:.1f}")
     shape = "DeepSeek-V2-Lite" if ds else "Qwen3-30B-A3B"
     if ds:
-        workload = (f"{cfg.name} decode, batch {B}, bf16 weights, multi-head latent attention over a paged latent "
+        workload = (f"{a.model} decode, batch {B}, bf16 weights, multi-head latent attention over a paged latent "
                     f"cache, contexts uniform in [{a.ctx_lo}, {a.ctx_hi}], greedy (BASELINE.json configs[3])")
     else:
-        workload = (f"{cfg.name} decode, batch {B}, {wname} weights, contexts uniform in [{a.ctx_lo}, {a.ctx_hi}], "
+        workload = (f"{a.model} decode, batch {B}, {wname} weights, contexts uniform in [{a.ctx_lo}, {a.ctx_hi}], "
                     f"greedy" + (" (BASELINE.json configs[4])" if a.fp8 else " (configs[4] shape with bf16 weights)"))
     out = {
         "metric": f"decode ms/step at batch {B}, {shape} shape; tokens/s; achieved HBM GB/s vs peak",
@@ -211,6 +211,15 @@ def main_batch(a):
             attach_traffic(out, "etxmk_ds_b4_deepseek-v2-lite_ctx512-2048_hbm_traffic.json")
         elif not ds and B == 16 and a.fp8 and a.ctx_hi == 4096:
             attach_traffic(out, "etxmk_fused_fp8_b16_qwen3-30b-a3b_ctx512-4096_hbm_traffic.json")
+    dec.close()                                           # release the handle before the CPU leg and the exit
+    del dec
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    if not a.no_cpu:
+        try:
+            out["cpu_baseline"] = cpu_baseline_batch(cfg, ctx, a.seed)
+        except Exception as e:  # the baseline is reported, never gating
+            log(f"[cpu] baseline failed: {e!r}")
     print(json.dumps(out), flush=True)
 
 
@@ -225,6 +234,47 @@ def calib_copy(dev):
     log("[gpu] calibration copy: 1 GiB read + 1 GiB written")
 
 
+def calibrate(dev) -> dict:
+    """The machine figures a decode step is built from, measured with the decode kernels' own code: the grid
+    barrier (grid_arrive / grid_wait, one 512-thread workgroup per CU, 2000 back to back per cooperative launch,
+    best of 3 launches) and the streaming read (non-temporal 1 KiB-per-wave loads over 4 GiB, 1 or 2 workgroups
+    per CU, 1 to 16 loads in flight per wave, best of 3).  Every barrier launch is checked (no wait gave up, every
+    counter at its final generation) and one stream pass is checked against a sum of the words it read."""
+    import torch
+    from etx.runtime import calib
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    iters = 2000
+    calib.barrier(cus, 100, dev)                           # warm
+    best = None
+    for _ in range(3):
+        us, bar, ab = calib.barrier(cus, iters, dev)
+        if ab != 0 or int(bar[64 * 8]) != 8 * iters or any(int(bar[64 * (9 + j)]) != iters for j in range(8)):
+            raise RuntimeError(f"barrier calibration: abort word {ab}, counters {bar[64 * 8]} / {bar[64 * 9]}")
+        best = us if best is None else min(best, us)
+    log(f"[gpu] grid barrier: {best:.3f} us ({cus} workgroups, {iters} per launch)")
+    gib = 4
+    src = torch.randint(-2**31, 2**31 - 1, (gib << 28,), dtype=torch.int32, device=dev)
+    nbytes = src.numel() * 4
+    want = calib.word_sum(src)
+    rows = []
+    for per_cu in (1, 2):
+        for inflight in (1, 2, 4, 8, 16):
+            calib.stream(src, inflight, per_cu * cus)
+            t = min(calib.stream(src, inflight, per_cu * cus)[0] for _ in range(3))
+            rows.append({"workgroups_per_cu": per_cu, "loads_in_flight_per_wave": inflight,
+                         "GBps": round(nbytes / t / 1e9, 1)})
+            log(f"[gpu] stream {per_cu} WG/CU, {inflight:2d} x 1 KiB per wave in flight: {rows[-1]['GBps']} GB/s")
+    _, sink = calib.stream(src, 4, cus)
+    got = calib.word_sum(sink)
+    if got != want:
+        raise RuntimeError(f"stream calibration read {got:#x}, words sum to {want:#x}")
+    del src, sink
+    return {"calibration": "gfx950 grid barrier and streaming read", "cus": cus,
+            "barrier_us": round(best, 3), "barriers_per_launch": iters, "stream_bytes": nbytes,
+            "stream": rows, "stream_checksum_ok": True,
+            "kernels": "etx-megakernel_amd/csrc/mk_calib.hip (grid_arrive/grid_wait of mk_device.h)"}
+
+
 def attach_traffic(out, name):
     """HBM bytes per launch of this workload from its committed counter passes (rocprofv3 --pmc FETCH_SIZE and
     WRITE_SIZE of the same command, each scaled by that counter's reading for the calibration copy), if present."""
@@ -235,37 +285,73 @@ def attach_traffic(out, name):
         out["roofline"]["traffic_source"] = f"profiles/{tf.name} (FETCH x{t['fetch_factor']}, WRITE x{t['write_factor']})"
 
 
-def cpu_baseline(cfg, ctx: int, seed: int) -> dict:
-    """The CPU oracle on a bounded sample of the same workload: two real-shape layers plus the full head at
-    context `ctx`, scaled to the model's layer count."""
+def cpu_baseline(cfg, ctx: int, seed: int, reps: int = 5) -> dict:
+    """The CPU oracle on a bounded sample of the same workload: the full-depth model (every layer, lm_head) with a
+    seeded KV cache of `ctx` positions; one untimed step at position ctx generates the experts it routes to, then
+    `reps` timed repeats of that step (each a whole decode step of the oracle: same token, same position, same
+    routing)."""
     import numpy as np
     from oracle import oracle as O
-    from etx.models.configs import with_layers
-    sample = with_layers(cfg, 2)
     t0 = time.time()
-    m = O.OracleModel(sample.as_dict(), seed, 0.02)
-    m.materialize_experts()
+    m = O.OracleModel(cfg.as_dict(), seed, 0.02)
     m.fill_kv_random(ctx)
-    log(f"[cpu] oracle sample built in {time.time() - t0:.1f}s ({O.num_threads()} threads)")
-    x = O.bf16_bits_to_f32(O.gen_normal_bf16(seed, O.stream_id(O.S_XIN, -1), cfg.H, scale=1.0))
-    reps = 3
+    tok = int(O.gen_tokens(seed, 1, cfg.V)[0])
+    m.step(tok, ctx)
+    log(f"[cpu] oracle model ({cfg.L} layers) and its first step ready in {time.time() - t0:.1f}s "
+        f"({O.num_threads()} threads)")
     t1 = time.time()
-    for r in range(reps):
-        for l in range(2):
-            x, _, _, _ = m.layer_step(l, x, ctx + r)
-    t_layers = (time.time() - t1) / reps                     # two layers
-    t2 = time.time()
-    for r in range(reps):
-        m.step(int(r), ctx + reps + r)
-    t_step = (time.time() - t2) / reps                       # embed + two layers + head
-    t_head = max(t_step - t_layers, 0.0)
-    ms = (t_head + t_layers * cfg.L / 2) * 1e3
+    for _ in range(reps):
+        m.step(tok, ctx)
+    ms = (time.time() - t1) / reps * 1e3
     m.close()
     import platform
     return {"value": round(ms, 3), "unit": "ms/token", "cores": O.num_threads(), "kind": "port",
-            "sample": f"CPU oracle (C, OpenMP), {reps} decode steps of 2 real-shape layers + lm_head at context {ctx}; "
-                      f"ms/token = head + {cfg.L}/2 x two-layer time ({platform.processor() or platform.machine()})",
+            "sample": f"CPU oracle (C, OpenMP): {reps} full-depth decode steps ({cfg.L} layers + lm_head) at context "
+                      f"{ctx}, timed after one untimed step of the same token and position "
+                      f"({platform.processor() or platform.machine()})",
             "tokens_per_s": round(1e3 / ms, 3), "effective_GBps": round(bytes_per_token(cfg, ctx)["total"] / ms / 1e6, 2)}
+
+
+def cpu_baseline_batch(cfg, contexts, seed: int, reps: int = 2) -> dict:
+    """The CPU oracle's batched step on a bounded sample: the batch's rows (each sequence at its context, seeded KV)
+    through slices of 2 and 4 layers plus lm_head (DeepSeek-V2: 2 and 3 layers, the dense layer first, one
+    sequence at a time); per layer = the difference / the extra layers, head = the rest; ms/step = head + L x per
+    layer."""
+    import numpy as np
+    from oracle import oracle as O
+    from etx.models.configs import with_layers
+    from etx.runtime import native as N
+    ds = cfg.arch == N.ARCH_DSV2
+    B = len(contexts)
+    lo, hi = (2, 3) if ds else (2, 4)
+    toks = [int(t) for t in O.gen_tokens(seed + 1, B, cfg.V)]
+    times = {}
+    for L in (lo, hi):
+        m = O.OracleModel(with_layers(cfg, L).as_dict(), seed, 0.02)
+        for b, c in enumerate(contexts):
+            m.fill_kv_random(int(c), seq=b)
+
+        def step():
+            if ds:
+                for b in range(B):
+                    m.step(toks[b], int(contexts[b]), seq=b)
+            else:
+                m.step_rows(list(range(B)), toks, [int(c) for c in contexts])
+        step()                                              # untimed: generates the routed experts
+        t = time.time()
+        for _ in range(reps):
+            step()
+        times[L] = (time.time() - t) / reps
+        m.close()
+    per_layer = (times[hi] - times[lo]) / (hi - lo)
+    head = max(times[lo] - lo * per_layer, 0.0)
+    ms = (head + cfg.L * per_layer) * 1e3
+    import platform
+    return {"value": round(ms, 3), "unit": "ms/step", "cores": O.num_threads(), "kind": "port",
+            "sample": f"CPU oracle (C, OpenMP): the batch's {B} rows at their contexts through {lo}- and {hi}-layer "
+                      f"slices + lm_head, {reps} timed steps each after an untimed one; ms/step = head + {cfg.L} x "
+                      f"per-layer time ({platform.processor() or platform.machine()})",
+            "ms_per_token": round(ms / B, 3), "tokens_per_s": round(B * 1e3 / ms, 3)}
 
 
 def trace_summary(t, cfg):
@@ -311,9 +397,15 @@ def main():
     ap.add_argument("--seed", type=int, default=20261201)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--unfused", action="store_true")
+    ap.add_argument("--graph", action="store_true",
+                    help="with --unfused: capture one step's per-phase launches in a HIP graph and time replays of it "
+                         "(each replay a whole step at the context the warmup ends on)")
     ap.add_argument("--workgroups", type=int, default=0)
     ap.add_argument("--trace", action="store_true", help="after timing, trace one fused step per phase (stderr)")
     ap.add_argument("--trace-out", default="", help="with --trace: also save the raw stamps (.npy)")
+    ap.add_argument("--calibrate", action="store_true",
+                    help="measure the grid barrier and the streaming read bandwidth (libetxmk_calib.so), print them "
+                         "as one JSON line and exit")
     ap.add_argument("--calib-copy", action="store_true",
                     help="profiling runs: first copy 1 GiB device to device, the known-size reference for HBM counters")
     ap.add_argument("--kv-fill", action="store_true",
@@ -337,6 +429,13 @@ def main():
         sys.exit(2)
     if a.model == "qwen3-8b" and a.batch > 1:
         raise SystemExit("the Qwen3-8B workload (BASELINE.json configs[1]) is batch 1")
+    if a.calibrate:
+        import torch
+        print(json.dumps(calibrate(torch.device("cuda:0"))), flush=True)
+        return
+    if a.graph and not a.unfused:
+        raise SystemExit("--graph replays the unfused step; the persistent kernel's barrier generations advance per "
+                         "launch and are not replayable")
     if a.batch > 1 or a.model == "deepseek-v2-lite":
         return main_batch(a)
 
@@ -412,18 +511,35 @@ def main():
     dec.sync()
     stream = torch.cuda.current_stream(dev)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    graph = None
+    if a.graph:
+        # the step at position pos (its per-phase launches, parameters by value) recorded once and replayed; a
+        # replay rewrites the same KV slot and next token with the same values, so every replay is the same step
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            dec.step(pos, write_next=True)
+        for _ in range(a.warmup):
+            graph.replay()
+        torch.cuda.synchronize()
+        log(f"[gpu] one step at position {pos} captured in a HIP graph "
+            f"({cfg.L * (6 if cfg.moe else 5) + 2} kernel nodes)")
     torch.cuda.synchronize()
     w0 = time.perf_counter()
     e0.record(stream)
     first_timed = pos
     for _ in range(a.steps):
-        dec.step(pos, write_next=True)
-        pos += 1
+        if graph is not None:
+            graph.replay()
+        else:
+            dec.step(pos, write_next=True)
+            pos += 1
     e1.record(stream)
     torch.cuda.synchronize()
     wall = (time.perf_counter() - w0) * 1e3
     dec.sync()
     ms = e0.elapsed_time(e1) / a.steps
+    if graph is not None:
+        pos += 1
     toks = dec.read_tokens(pos)
     ctx_mean = (first_timed + pos - 1) / 2.0
     b = bytes_per_token(cfg, int(round(ctx_mean)))
@@ -449,10 +565,11 @@ def main():
                 + " weights N(0,0.02); " + ("KV cache of seeded N(0,1) values"
                 if a.kv_fill else "prompt of seeded uniform token ids, prefilled " +
                 (f"{rows} positions per launch (bit-identical to token by token)" if rows else "token by token")),
-        "config": {"workload": f"{cfg.name} decode, batch 1, context {a.ctx} (+{a.warmup} warmup), greedy "
+        "config": {"workload": f"{a.model} decode, batch 1, context {a.ctx} (+{a.warmup} warmup), greedy "
                                f"(BASELINE.json configs[{1 if dense else 2}])",
                    "batch": 1, "context": a.ctx, "layers": cfg.L, "experts": cfg.E, "top_k": cfg.TOPK,
-                   "vocab": cfg.V, "mode": "unfused" if a.unfused else "fused megakernel",
+                   "vocab": cfg.V, "mode": ("unfused, HIP graph replay" if a.graph else "unfused")
+                   if a.unfused else "fused megakernel",
                    "workgroups": a.workgroups or "one per CU", "seed": a.seed},
         "tokens_per_s": round(1e3 / ms, 2), "host_wall_ms_per_token": round(wall / a.steps, 4),
         "bytes_per_token": b["total"], "achieved_GBps": round(gbps, 1),
@@ -469,6 +586,11 @@ def main():
         out["prefill"] = prefill
     if not a.unfused and not a.fp8 and a.ctx == 1024:      # the workloads the counter passes were taken on
         attach_traffic(out, f"etxmk_fused_{'qwen3-8b' if dense else 'qwen3-30b-a3b'}_b1_ctx1024_hbm_traffic.json")
+    del graph
+    dec.close()                                           # release the handle before the CPU leg and the exit
+    del dec
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
     if not a.no_cpu:
         try:
             out["cpu_baseline"] = cpu_baseline(cfg, a.ctx, a.seed)

@@ -1,4 +1,5 @@
-"""Builds libetxmk.so (the gfx950 decode megakernel and its C ABI) in-tree with hipcc.
+"""Builds libetxmk.so (the gfx950 decode megakernel and its C ABI) and libetxmk_calib.so (the grid-barrier and
+streaming-read calibration kernels, outside the decode ABI) in-tree with hipcc.
 
     python etx-megakernel_amd/build_lib.py
 """
@@ -13,6 +14,7 @@ PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 SRC = PKG / "csrc"
 LIB = PKG / "lib" / "libetxmk.so"
+CALIB = PKG / "lib" / "libetxmk_calib.so"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 FLAGS = [
@@ -26,6 +28,7 @@ FLAGS = [
 # translation units: the host side (C ABI, unfused and initialisation kernels) and one per persistent-kernel list
 UNITS = ["mk_api.hip", "mk_fused_bf16.hip", "mk_fused_fp8.hip", "mk_batch_bf16.hip", "mk_batch_fp8.hip",
          "mk_mla.hip"]
+CALIB_UNITS = ["mk_calib.hip"]
 
 
 def build(verbose: bool = False) -> Path:
@@ -35,7 +38,7 @@ def build(verbose: bool = False) -> Path:
     obj_dir.mkdir(parents=True, exist_ok=True)
     inc = [f"-I{ROOT / 'include'}", f"-I{SRC}"]
     procs = []
-    for u in UNITS:
+    for u in UNITS + CALIB_UNITS:
         obj = obj_dir / (Path(u).stem + ".o")
         procs.append((u, obj, subprocess.Popen([HIPCC, *FLAGS, *inc, "-c", "-o", str(obj), str(SRC / u)],
                                                stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)))
@@ -49,13 +52,15 @@ def build(verbose: bool = False) -> Path:
             sys.stderr.write(out)
     if failed:
         raise RuntimeError(f"hipcc failed building {', '.join(failed)}")
-    tmp = LIB.with_suffix(".so.tmp")
-    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(tmp), *[str(o) for _, o, _ in procs]]
-    r = subprocess.run(cmd, capture_output=True, text=True)
-    if r.returncode != 0:
-        sys.stderr.write(r.stdout + r.stderr)
-        raise RuntimeError(f"linking {LIB} failed ({r.returncode})")
-    os.replace(tmp, LIB)
+    for lib, units in ((LIB, UNITS), (CALIB, CALIB_UNITS)):
+        tmp = lib.with_suffix(".so.tmp")
+        objs = [str(o) for u, o, _ in procs if u in units]
+        cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(tmp), *objs]
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode != 0:
+            sys.stderr.write(r.stdout + r.stderr)
+            raise RuntimeError(f"linking {lib} failed ({r.returncode})")
+        os.replace(tmp, lib)
     return LIB
 
 

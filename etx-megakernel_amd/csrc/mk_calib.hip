@@ -1,0 +1,106 @@
+// Calibration kernels for gfx950, built as their own library (libetxmk_calib.so), outside the decode ABI:
+//  - the cost of one grid barrier of the persistent decode kernels: the same grid_arrive / grid_wait (hierarchical
+//    arrival over 8 group counters, 8 release flags, bounded wait) that etxmk_fused runs between phases, here back
+//    to back with no work between them, one 512-thread workgroup per CU, cooperative launch;
+//  - the HBM read bandwidth of the decode kernels' streaming pattern: non-temporal 16-byte loads, 1 KiB per wave
+//    per load (64 lanes x 16 bytes), INF such loads issued before any is used, at 1, 2, 4, 8 and 16 in flight.
+// The stream kernel sums every 32-bit word it reads into a per-thread sink (mod 2^32) so that the loads cannot be
+// dropped and the caller can check that every byte was read exactly once.
+#include "mk_device.h"
+
+namespace mk {
+namespace {
+
+struct CalibSmem {
+  int32_t phase;
+  int32_t abort;
+};
+
+__global__ __launch_bounds__(NT) void calib_barrier(Params p, int iters) {
+  __shared__ CalibSmem s;
+  if (threadIdx.x == 0) s.abort = 0;
+  __syncthreads();
+  int k = 0;
+  for (int i = 0; i < iters; ++i) {
+    grid_arrive(p, k, s);
+    if (!grid_wait(p, k, s)) return;
+  }
+}
+
+// wave w reads 1 KiB chunks w + W * (INF * t + j), j = 0 .. INF - 1, issuing the INF loads of a round together
+template <int INF>
+__global__ __launch_bounds__(NT) void calib_stream(const u32x4* src, size_t nchunk, uint32_t* sink) {
+  const size_t W = (size_t)gridDim.x * NWAVE;
+  const size_t w = (size_t)blockIdx.x * NWAVE + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  uint32_t acc = 0;
+  for (size_t c = w; c < nchunk; c += W * INF) {
+    u32x4 v[INF];
+#pragma unroll
+    for (int j = 0; j < INF; ++j) {
+      const size_t cj = c + (size_t)j * W;
+      v[j] = cj < nchunk ? ld_nt16(src + cj * 64 + lane) : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int j = 0; j < INF; ++j) acc += v[j].x + v[j].y + v[j].z + v[j].w;
+  }
+  sink[(size_t)blockIdx.x * NT + threadIdx.x] = acc;
+}
+
+int co_resident(const void* fn) {
+  int dev = 0, cus = 0, per_cu = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return -1;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return -1;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, NT, 0) != hipSuccess) return -1;
+  return cus * per_cu;
+}
+
+}  // namespace
+}  // namespace mk
+
+extern "C" {
+
+// iters grid barriers in one cooperative launch of nwg workgroups.  bar: 17 * 64 uint32, zero on entry (the
+// barrier's generations start at 1); abort_word: one int32, zero on entry, nonzero afterwards if a wait gave up
+// (2: its 2 s limit).  Returns 0, or the HIP error code (hipErrorInvalidValue for a grid that is not co-resident).
+int etxmk_calib_barrier(uint32_t* bar, int32_t* abort_word, int nwg, int iters, void* stream) {
+  using namespace mk;
+  if (!bar || !abort_word || nwg < 8 || iters < 0) return (int)hipErrorInvalidValue;
+  const int most = co_resident((const void*)calib_barrier);
+  if (most < 0) return (int)hipErrorInvalidDevice;
+  if (nwg > most) return (int)hipErrorInvalidValue;
+  Params p{};
+  p.bar = bar;
+  p.bar_base = 0;
+  p.abort_word = abort_word;
+  p.host_stop = nullptr;
+  p.trace = nullptr;
+  p.nwg = nwg;
+  p.spin_ticks = 200000000ull;          // 2 s at the 100 MHz real-time clock
+  p.poll_mask = 255;
+  void* args[] = {&p, &iters};
+  const hipError_t e = hipLaunchCooperativeKernel((const void*)calib_barrier, dim3(nwg), dim3(NT), args, 0,
+                                                  (hipStream_t)stream);
+  return e == hipSuccess ? (int)hipGetLastError() : (int)e;
+}
+
+// one streaming read of bytes (a multiple of 1024) at src with inflight (1, 2, 4, 8 or 16) 1 KiB loads per wave
+// in flight, nwg workgroups of 512 threads; sink: nwg * 512 uint32, each thread's sum of the words it read.
+int etxmk_calib_stream(const void* src, size_t bytes, int inflight, int nwg, uint32_t* sink, void* stream) {
+  using namespace mk;
+  if (!src || !sink || nwg < 1 || bytes % 1024 != 0 || ((uintptr_t)src & 15) != 0) return (int)hipErrorInvalidValue;
+  const size_t nchunk = bytes / 1024;
+  const u32x4* s = (const u32x4*)src;
+  hipStream_t st = (hipStream_t)stream;
+  switch (inflight) {
+    case 1: hipLaunchKernelGGL(calib_stream<1>, dim3(nwg), dim3(NT), 0, st, s, nchunk, sink); break;
+    case 2: hipLaunchKernelGGL(calib_stream<2>, dim3(nwg), dim3(NT), 0, st, s, nchunk, sink); break;
+    case 4: hipLaunchKernelGGL(calib_stream<4>, dim3(nwg), dim3(NT), 0, st, s, nchunk, sink); break;
+    case 8: hipLaunchKernelGGL(calib_stream<8>, dim3(nwg), dim3(NT), 0, st, s, nchunk, sink); break;
+    case 16: hipLaunchKernelGGL(calib_stream<16>, dim3(nwg), dim3(NT), 0, st, s, nchunk, sink); break;
+    default: return (int)hipErrorInvalidValue;
+  }
+  return (int)hipGetLastError();
+}
+
+}  // extern "C"

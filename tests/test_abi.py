@@ -17,6 +17,12 @@ def test_library_exports_every_declared_symbol():
     assert L.etxmk_abi_version() == N.ABI_VERSION == 3
 
 
+def test_calibration_library_exports():
+    from etx.runtime import calib
+    lib = calib.load()                                     # loads without a GPU; nothing is launched
+    assert hasattr(lib, "etxmk_calib_barrier") and hasattr(lib, "etxmk_calib_stream")
+
+
 def test_sizes_of_real_configurations():
     s = N.sizes(configs.QWEN3_30B_A3B)
     c = configs.QWEN3_30B_A3B
