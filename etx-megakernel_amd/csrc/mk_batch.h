@@ -239,7 +239,8 @@ __device__ __forceinline__ float* sink_of(const Params& p) {
 // gemv_run with B input rows per group: groups of NR rows dealt round-robin to the grid's waves.  D register buffers
 // form a ring: the next D - 1 groups' weights stream while one group is reduced, the first D - 1 issued before
 // `prologue` (which waits for the inputs).  Every issue is the same run of loads: a missing row (nullptr) reloads
-// the group's first row, and past the wave's last group the issues reload that group (cache hits); with epilogues of
+// the group's first row, and past the wave's last group the issues reload that group (non-temporal loads, so these
+// are fetched from HBM again, not served from the cache: the price of an exact wait count); with epilogues of
 // one store per lane (the sink for lanes with nothing to store) the compiler's wait before a buffer's dots counts
 // exactly the loads and stores issued after it, so it never waits for groups still streaming.  nvec(g) is the number
 // of input rows of group g, xvec(g, b) the LDS address of its b-th; epi(g, nv, v) consumes v[NR][B].
@@ -885,7 +886,8 @@ __device__ __forceinline__ void phase_expert_up_b(const Params& p, int layer, S&
 // batch in flight while the current one is reduced) and dots each with the h rows of that expert's pairs.  The
 // pairs' h rows are staged in LDS in passes of whole experts that fit; lane b carries sequence b's combine chain,
 // kept in LDS between batches and passes.  Every batch issue is the same run of loads (a batch short of D experts
-// reloads its last one; after a row's last batch the issue reloads it) and the outputs are stored after the last
+// reloads its last one; after a row's last batch the issue reloads it: HBM re-fetches, the rows being streamed
+// non-temporally) and the outputs are stored after the last
 // pass, so the wait before a batch's dots counts exactly the loads issued after it.
 template <class WR, int B, class S, class Wait>
 __device__ __forceinline__ void phase_expert_down_b(const Params& p, int layer, S& s, Wait wait) {

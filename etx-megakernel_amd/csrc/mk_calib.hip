@@ -1,9 +1,11 @@
-// Calibration kernels for gfx950, built as their own library (libetxmk_calib.so), outside the decode ABI:
+// Calibration and probe kernels for gfx950, built as their own library (libetxmk_calib.so), outside the decode ABI:
 //  - the cost of one grid barrier of the persistent decode kernels: the same grid_arrive / grid_wait (hierarchical
 //    arrival over 8 group counters, 8 release flags, bounded wait) that etxmk_fused runs between phases, here back
 //    to back with no work between them, one 512-thread workgroup per CU, cooperative launch;
 //  - the HBM read bandwidth of the decode kernels' streaming pattern: non-temporal 16-byte loads, 1 KiB per wave
-//    per load (64 lanes x 16 bytes), INF such loads issued before any is used, at 1, 2, 4, 8 and 16 in flight.
+//    per load (64 lanes x 16 bytes), INF such loads issued before any is used, at 1, 2, 4, 8 and 16 in flight;
+//  - the matrix-core probe: chained v_mfma_f32_16x16x32_bf16 on register contents the caller lays out, one wave
+//    per case, so that the instruction's accumulation can be compared with a CPU statement of it.
 // The stream kernel sums every 32-bit word it reads into a per-thread sink (mod 2^32) so that the loads cannot be
 // dropped and the caller can check that every byte was read exactly once.
 #include "mk_device.h"
@@ -45,6 +47,22 @@ __global__ __launch_bounds__(NT) void calib_stream(const u32x4* src, size_t nchu
     for (int j = 0; j < INF; ++j) acc += v[j].x + v[j].y + v[j].z + v[j].w;
   }
   sink[(size_t)blockIdx.x * NT + threadIdx.x] = acc;
+}
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// lane i of case blockIdx.x: a, b hold nsteps blocks of 8 bf16 per lane, c and d 4 floats per lane
+__global__ __launch_bounds__(64) void calib_mfma_bf16(const u32x4* a, const u32x4* b, const f32x4* c, f32x4* d,
+                                                      int nsteps) {
+  const size_t i = (size_t)blockIdx.x * 64 + threadIdx.x;
+  f32x4 acc = c[i];
+  for (int s = 0; s < nsteps; ++s) {
+    const bf16x8 av = __builtin_bit_cast(bf16x8, a[i * nsteps + s]);
+    const bf16x8 bv = __builtin_bit_cast(bf16x8, b[i * nsteps + s]);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, acc, 0, 0, 0);
+  }
+  d[i] = acc;
 }
 
 int co_resident(const void* fn) {
@@ -100,6 +118,18 @@ int etxmk_calib_stream(const void* src, size_t bytes, int inflight, int nwg, uin
     case 16: hipLaunchKernelGGL(calib_stream<16>, dim3(nwg), dim3(NT), 0, st, s, nchunk, sink); break;
     default: return (int)hipErrorInvalidValue;
   }
+  return (int)hipGetLastError();
+}
+
+// ncase waves, each nsteps chained v_mfma_f32_16x16x32_bf16 (D = C + A B, K = 32 per step) on per-lane register
+// contents: a, b [ncase][64][nsteps][8] bf16 bits, c, d [ncase][64][4] fp32 (16-byte aligned).
+int etxmk_calib_mfma_bf16(const uint16_t* a, const uint16_t* b, const float* c, float* d, int ncase, int nsteps,
+                          void* stream) {
+  using namespace mk;
+  if (!a || !b || !c || !d || ncase < 1 || nsteps < 1 || nsteps > 4096) return (int)hipErrorInvalidValue;
+  if ((((uintptr_t)a | (uintptr_t)b | (uintptr_t)c | (uintptr_t)d) & 15) != 0) return (int)hipErrorInvalidValue;
+  hipLaunchKernelGGL(calib_mfma_bf16, dim3(ncase), dim3(64), 0, (hipStream_t)stream, (const u32x4*)a, (const u32x4*)b,
+                     (const f32x4*)c, (f32x4*)d, nsteps);
   return (int)hipGetLastError();
 }
 

@@ -23,6 +23,8 @@ def load():
         lib.etxmk_calib_barrier.restype = C.c_int
         lib.etxmk_calib_stream.argtypes = [C.c_void_p, C.c_size_t, C.c_int, C.c_int, C.c_void_p, C.c_void_p]
         lib.etxmk_calib_stream.restype = C.c_int
+        lib.etxmk_calib_mfma_bf16.argtypes = [C.c_void_p] * 4 + [C.c_int, C.c_int, C.c_void_p]
+        lib.etxmk_calib_mfma_bf16.restype = C.c_int
         _lib = lib
     return _lib
 
@@ -80,3 +82,39 @@ def word_sum(t) -> int:
     for i in range(0, w.numel(), step):
         total += int((w[i:i + step].to(torch.int64) & 0xFFFFFFFF).sum().item())
     return total & 0xFFFFFFFF
+
+
+def mfma_bf16(a_bits, b_bits, c, device="cuda:0"):
+    """D = C + A B through chained v_mfma_f32_16x16x32_bf16, one wave per case: a_bits [n][16][32 s] and b_bits
+    [n][32 s][16] bf16 bit patterns (uint16), c [n][16][16] fp32; returns D [n][16][16] fp32.  Step i takes k in
+    [32 i, 32 i + 32); within a step, lane l holds A row l % 16 and B column l % 16 at k = 8 (l // 16) .. + 7, and
+    D rows 4 (l // 16) .. + 3 of column l % 16."""
+    import numpy as np
+    import torch
+    lib = load()
+    a_bits = np.asarray(a_bits, np.uint16); b_bits = np.asarray(b_bits, np.uint16); c = np.asarray(c, np.float32)
+    n, K = a_bits.shape[0], a_bits.shape[2]
+    if a_bits.shape != (n, 16, K) or b_bits.shape != (n, K, 16) or c.shape != (n, 16, 16) or K % 32:
+        raise ValueError("shapes: a [n][16][32 s], b [n][32 s][16], c [n][16][16]")
+    steps = K // 32
+    lane = np.arange(64)
+    row, quad = lane % 16, lane // 16
+    # k index of lane l, step s, element j: 32 s + 8 quad + j
+    k = (32 * np.arange(steps)[None, :, None] + 8 * quad[:, None, None] + np.arange(8)[None, None, :])   # [64][s][8]
+    a = a_bits[:, row[:, None, None], k]                     # [n][64][s][8]
+    b = np.transpose(b_bits, (0, 2, 1))[:, row[:, None, None], k]
+    cr = c[:, 4 * quad[:, None] + np.arange(4)[None, :], row[:, None]]       # [n][64][4]
+    dev = torch.device(device)
+    ta = torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).to(dev)
+    tb = torch.from_numpy(np.ascontiguousarray(b).view(np.int16)).to(dev)
+    tc = torch.from_numpy(np.ascontiguousarray(cr)).to(dev)
+    td = torch.empty_like(tc)
+    rc = lib.etxmk_calib_mfma_bf16(C.c_void_p(ta.data_ptr()), C.c_void_p(tb.data_ptr()), C.c_void_p(tc.data_ptr()),
+                                   C.c_void_p(td.data_ptr()), n, steps, _stream(torch, dev))
+    if rc != 0:
+        raise RuntimeError(f"etxmk_calib_mfma_bf16: HIP error {rc}")
+    torch.cuda.synchronize(dev)
+    dr = td.cpu().numpy()
+    D = np.zeros((n, 16, 16), np.float32)
+    D[:, 4 * quad[:, None] + np.arange(4)[None, :], row[:, None]] = dr
+    return D

@@ -117,3 +117,31 @@ def test_step_rows_equals_batched_single_steps(oracle_lib, name):
         assert np.array_equal(ka, kb) and np.array_equal(va, vb), f"layer {layer}: pool differs"
     a.close()
     b.close()
+
+
+@pytest.mark.parametrize("K", [64, 128, 512, 768, 2048, 4096])
+def test_vector_dot_equals_scalar_dot(oracle_lib, K):
+    """The rows form's AVX2 dot (orc_dot64f: fp32 weight images, 8 ymm accumulators, hadd tree) against the scalar
+    canonical dot (orc_dot64: bf16 weights, 64 accumulators, lanes_reduce) on the same values: equal bit for bit.
+    The inputs span 40 binades so that the lane tree's shape decides the rounding: a plain left-to-right sum of the
+    same 64 lane values differs from the tree on most rows, which the test also checks (it could not tell the two
+    orders apart otherwise)."""
+    L = O.lib()
+    rng = np.random.default_rng(K)
+    differs = 0
+    for trial in range(200):
+        w = O.f32_to_bf16_bits((rng.standard_normal(K) * np.exp2(rng.uniform(-20, 20, K))).astype(np.float32))
+        x = O.bf16_bits_to_f32(O.f32_to_bf16_bits((rng.standard_normal(K) * np.exp2(rng.uniform(-20, 20, K)))
+                                                  .astype(np.float32)))
+        wf = O.bf16_bits_to_f32(w)
+        got = L.orc_dot64f(np.ascontiguousarray(wf), np.ascontiguousarray(x), K)
+        want = L.orc_dot64(np.ascontiguousarray(w), np.ascontiguousarray(x), K)
+        assert np.float32(got).tobytes() == np.float32(want).tobytes(), f"trial {trial}: {got!r} vs {want!r}"
+        acc = np.zeros(64, np.float32)
+        for k in range(K):                                 # the per-lane fma chains, rounded per step
+            acc[k % 64] = np.float32(np.float64(acc[k % 64]) + np.float64(wf[k]) * np.float64(x[k]))
+        seq = np.float32(0)
+        for v in acc:
+            seq = np.float32(seq + v)
+        differs += seq != np.float32(want)
+    assert differs > 20, "the inputs do not separate the tree from a sequential lane sum"
