@@ -976,6 +976,9 @@ static int launch(etxmk_handle* h, const int32_t* posv, int pos, int write_next,
     p.qkv_lds_rows = ok ? S : 0;
   }
   p.B = nrows;
+  // batched MoE gate/up on the matrix cores: handles of batch capacity >= 8 with whole row blocks (the CPU oracle
+  // applies the same rule to the models of such handles)
+  p.mfma = !ds && c.batch >= 8 && c.moe && c.H % (c.wdtype == ETXMK_W_FP8 ? 1024 : 512) == 0 && (2 * c.MI) % 16 == 0;
   p.nbps = nbps_of(&c);
   p.tok_stride = c.max_ctx + 1;
   if (pf) {                                // every row reads the one sequence's block table and token rows

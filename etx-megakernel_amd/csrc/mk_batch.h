@@ -881,6 +881,134 @@ __device__ __forceinline__ void phase_expert_up_b(const Params& p, int layer, S&
       [&]() { return true; }, p.nwg, p.trace, s.phase);
 }
 
+// P5 on the matrix cores (handles of batch capacity >= 8, p.mfma): tiles of 16 consecutive gate/up rows of one
+// routed expert against the sequences routed to it (at most 16: one MFMA column each, the others zero), D = W X
+// through chained v_mfma_f32_16x16x32_bf16 from 0.  Lane l (row l % 16, quad q = l / 16) loads the 16-byte lane slot
+// 4s + q of its row in every block, so one block of the tile's 16 rows is 16 loads per lane (16 KB, bf16 512-element
+// blocks; an e4m3 row's 1024-element block is the same 16 loads, each slot's codes 0-7 paired with the input's even
+// 512-block and codes 8-15 with the odd one, decoded to bf16 exactly); the input operand is the same slot of the
+// sequence's normed row in LDS.  The sum's order is therefore: 512-element blocks ascending, 16 steps a block, step s
+// giving quad q the elements 4s + q + 64 j (j < 8), each step by the hardware's accumulation rule (the oracle's
+// mfma_bf16_k32).  Two register buffers alternate: the next block's loads are issued before this block's MFMAs; past
+// the wave's last block the issue reads the wave's sink line, so every issue is the same run of loads.  D's lane holds
+// rows 4q .. 4q + 3 of one sequence, two whole gate/up pairs: SiLU * up is formed in the lane.
+typedef __bf16 mk_bf16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float mk_f32x4 __attribute__((ext_vector_type(4)));
+
+// codes 8h .. 8h + 7 of a 16-code e4m3 slot as 8 bf16 (exact: every e4m3 value is a bf16 value)
+__device__ __forceinline__ mk_bf16x8 e4m3_half_bf16(const u32x4& c, int h) {
+  u32x4 o;
+#pragma unroll
+  for (int d = 0; d < 2; ++d) {
+    const uint32_t w = c[2 * h + d];
+    // codes 0, 1 and 2, 3 of the word as fp32, taken as bits whole (a bit cast of one element of the conversion's
+    // 2-vector compiled to a copy of element 0)
+    const u32x2 lo = __builtin_bit_cast(u32x2, __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false));
+    const u32x2 hi = __builtin_bit_cast(u32x2, __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true));
+    // the upper halves of two fp32 values (their exact bf16 bits) into one word: bytes 2, 3 of the first, then
+    // bytes 2, 3 of the second (v_perm_b32 selector 0x07060302 over {second, first})
+    o[2 * d] = __builtin_amdgcn_perm(lo[1], lo[0], 0x07060302u);
+    o[2 * d + 1] = __builtin_amdgcn_perm(hi[1], hi[0], 0x07060302u);
+  }
+  return __builtin_bit_cast(mk_bf16x8, o);
+}
+
+template <class WR, int B, int EC, class S, class Wait>
+__device__ __forceinline__ void phase_expert_up_mfma(const Params& p, int layer, S& s, Wait wait) {
+  constexpr int KK = WR::K;
+  constexpr bool F8 = WR::FP8;
+  constexpr int NBLK = F8 ? KK / 1024 : KK / 512;
+  static_assert(KK % (F8 ? 1024 : 512) == 0 && NBLK >= 1, "the tile path takes whole blocks");
+  const LayerW Lw = layer_w(p, layer);
+  const int MI = p.MI, KT = p.TOPK, nb = p.B;
+  const uint8_t* W = Lw.w13;
+  build_norm_xb<KK, B>(p, false, Lw.ln2, s);              // x is final since the O projection
+  if (!wait()) return;
+  route_all<B, EC>(p, s);
+  if (blockIdx.x == 0) {
+    for (int t = threadIdx.x; t < nb * KT; t += NT) {
+      const int b = t / KT, k = t - b * KT;
+      if (p.dump_ids) st_i(p.dump_ids + ((size_t)layer * nb + b) * KT + k, s.rids[b][k]);
+      if (p.dump_wts) st_f(p.dump_wts + ((size_t)layer * nb + b) * KT + k, s.rwts[b][k]);
+    }
+    if (p.dump_logits)
+      for (int t = threadIdx.x; t < nb * p.E; t += NT) st_f(p.dump_logits + (size_t)layer * nb * p.E + t, ld_ag(p.logits + t));
+  }
+  const int TPE = (2 * MI) / 16, ntile = s.nexp * TPE;
+  const int lane = lane_id(), r = lane & 15, q = lane >> 4;
+  const int gw = blockIdx.x * NWAVE + wave_u(), nw = p.nwg * NWAVE;
+  const int nitem = (gw < ntile ? (ntile - 1 - gw) / nw + 1 : 0) * NBLK;
+  if (nitem == 0) return;
+  const uint8_t* sinkp = (const uint8_t*)sink_of(p);
+  auto row_of = [&](int it) -> const uint8_t* {
+    const int t = gw + (it / NBLK) * nw, u = t / TPE, jt = t - u * TPE;
+    return mrow<WR>(W, (size_t)s.uexp[u] * 2 * MI + 16 * jt + r);
+  };
+  auto issue = [&](int it, u32x4(&R)[16], float& sc) {
+    const bool ok = it < nitem;
+    const uint8_t* row = ok ? row_of(it) : sinkp;
+    const uint8_t* base = ok ? row + 1024 * (it % NBLK) + 16 * q : sinkp + 16 * q;
+    const int step = ok ? 64 : 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) R[i] = ld_nt16(base + step * i);
+    if constexpr (F8) sc = ld_f((const float*)(ok ? row + KK : sinkp));
+  };
+  mk_f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  auto compute = [&](int it, const u32x4(&R)[16], float sc) {
+    const int blk = it % NBLK, t = gw + (it / NBLK) * nw, u = t / TPE, jt = t - u * TPE;
+    const int p0 = s.ustart[u], nv = s.ustart[u + 1] - p0;
+    if (blk == 0) acc = mk_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    const bool has = r < nv;                              // MFMA column r: the expert's r-th routed sequence
+    const uint16_t* xb = s.n.xs + (size_t)(has ? s.pseq[p0 + r] : 0) * KK + 8 * q;
+    auto xop = [&](int xblk, int i) -> mk_bf16x8 {
+      const u32x4 v = *(const u32x4*)(xb + 512 * xblk + 32 * i);
+      return __builtin_bit_cast(mk_bf16x8, has ? v : u32x4{0u, 0u, 0u, 0u});
+    };
+    if constexpr (!F8) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(mk_bf16x8, R[i]), xop(blk, i), acc, 0, 0, 0);
+    } else {
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(e4m3_half_bf16(R[i], h), xop(2 * blk + h, i), acc, 0, 0, 0);
+    }
+    if (blk == NBLK - 1) {
+      // the epilogue reads the chain's last MFMA result: the compiler's own wait before that read (s_nop 7, 8 wait
+      // states) let 4 of 32 768 values be read before the result was complete (each differing from the finished
+      // sum); 18 wait states, fenced against rescheduling, make the read follow the write
+      __builtin_amdgcn_sched_barrier(0);
+      asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 1" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);
+      float v[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = F8 ? acc[i] * __shfl(sc, 4 * q + i) : acc[i];   // row 4q + i's scale
+      const int j0 = 8 * jt + 2 * q;                      // rows 4q, 4q+1: pair j0; rows 4q+2, 4q+3: pair j0 + 1
+      const float h0 = bfr(bfr(silu(bfr(v[0]))) * bfr(v[1]));
+      const float h1 = bfr(bfr(silu(bfr(v[2]))) * bfr(v[3]));
+      uint16_t* hrow = p.h16 + (size_t)(p0 + r) * MI;
+      st_ag_u16(has ? hrow + perm_stored(j0, MI) : (uint16_t*)sink_of(p), f2bf(h0));
+      st_ag_u16(has ? hrow + perm_stored(j0 + 1, MI) : (uint16_t*)sink_of(p), f2bf(h1));
+    }
+  };
+  u32x4 R0[16], R1[16];
+  float sc0 = 1.0f, sc1 = 1.0f;
+  issue(0, R0, sc0);
+  if (p.trace && threadIdx.x == 0)
+    *(MK_G uint64_t*)(p.trace + ((size_t)s.phase * p.nwg + blockIdx.x) * 3 + 2) = __builtin_amdgcn_s_memrealtime();
+  for (int it = 0;;) {
+    issue(it + 1, R1, sc1);
+    compute(it, R0, sc0);
+    if (++it >= nitem) break;
+    issue(it + 1, R0, sc0);
+    compute(it, R1, sc1);
+    if (++it >= nitem) break;
+  }
+}
+
 // P6: expert down, routing weight, combine per sequence in ascending expert id, residual (ref_numpy.py:146-148).
 // Each wave owns output rows; for its row it streams the rows of every distinct expert (D at a time, the next
 // batch in flight while the current one is reduced) and dots each with the h rows of that expert's pairs.  The
@@ -1102,7 +1230,12 @@ __device__ __forceinline__ void fused_body_b(const Params& p) {
       phase_router_b<H, B>(p, layer, s, wait);
       if (s.abort) return;
       grid_arrive(p, k, s);
-      phase_expert_up_b<RowOf<FP8, H>, B, EC>(p, layer, s, wait);
+      if constexpr (B >= 8 && H % (FP8 ? 1024 : 512) == 0 && (2 * KM) % 16 == 0) {
+        if (p.mfma) phase_expert_up_mfma<RowOf<FP8, H>, B, EC>(p, layer, s, wait);
+        else phase_expert_up_b<RowOf<FP8, H>, B, EC>(p, layer, s, wait);
+      } else {
+        phase_expert_up_b<RowOf<FP8, H>, B, EC>(p, layer, s, wait);
+      }
       if (s.abort) return;
       grid_arrive(p, k, s);
       phase_expert_down_b<RowOf<FP8, KM>, B>(p, layer, s, wait);
