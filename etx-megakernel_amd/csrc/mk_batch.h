@@ -950,8 +950,11 @@ __device__ __forceinline__ void phase_expert_up_mfma(const Params& p, int layer,
     const uint8_t* row = ok ? row_of(it) : sinkp;
     const uint8_t* base = ok ? row + 1024 * (it % NBLK) + 16 * q : sinkp + 16 * q;
     const int step = ok ? 64 : 0;
+    // ordinary (cached) loads: a wave's load of one slot column reads 64 bytes of each of its 16 rows, and the next
+    // slot column the other half of the same 128-byte lines; non-temporal loads let those lines go between the two
+    // (2.3 GB more fetched per batch-16 fp8 step, 13.75 against 12.99 ms)
 #pragma unroll
-    for (int i = 0; i < 16; ++i) R[i] = ld_nt16(base + step * i);
+    for (int i = 0; i < 16; ++i) R[i] = ld16(base + step * i);
     if constexpr (F8) sc = ld_f((const float*)(ok ? row + KK : sinkp));
   };
   mk_f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
