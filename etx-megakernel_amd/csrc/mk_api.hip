@@ -976,9 +976,13 @@ static int launch(etxmk_handle* h, const int32_t* posv, int pos, int write_next,
     p.qkv_lds_rows = ok ? S : 0;
   }
   p.B = nrows;
-  // batched MoE gate/up on the matrix cores: handles of batch capacity >= 8 with whole row blocks (the CPU oracle
-  // applies the same rule to the models of such handles)
-  p.mfma = !ds && c.batch >= 8 && c.moe && c.H % (c.wdtype == ETXMK_W_FP8 ? 1024 : 512) == 0 && (2 * c.MI) % 16 == 0;
+  // batched QKV, O projection and MoE gate/up on the matrix cores: handles of batch capacity >= 8 with whole row
+  // blocks (the CPU oracle applies the same rule to the models of such handles)
+  {
+    const int tb = c.wdtype == ETXMK_W_FP8 ? 1024 : 512;
+    p.mfma = !ds && c.batch >= 8 && c.moe && c.H % tb == 0 && c.H / tb <= NWAVE && (c.NH * c.HD) % tb == 0 &&
+             (c.NH * c.HD) / tb <= NWAVE && (2 * c.MI) % 16 == 0;
+  }
   p.nbps = nbps_of(&c);
   p.tok_stride = c.max_ctx + 1;
   if (pf) {                                // every row reads the one sequence's block table and token rows
@@ -1014,7 +1018,9 @@ static int launch(etxmk_handle* h, const int32_t* posv, int pos, int write_next,
     p.ibase[b + 1] = p.ibase[b] + (ds ? ds_nhg(c) * nch : c.NKV * ((nch + ATTN_CPI_B - 1) / ATTN_CPI_B));
   }
   if (h->fused) {
-    const void* fn = ds ? ds_kernel(c) : batched ? batch_kernel(c, nrows) : fused_kernel(c);
+    // p.mfma launches take a kernel of capacity >= 8 whatever their row count (a short prefill included): the tile
+    // forms exist in those kernels only, and the rule is the handle's, not the launch's
+    const void* fn = ds ? ds_kernel(c) : batched ? batch_kernel(c, p.mfma && nrows < 8 ? 8 : nrows) : fused_kernel(c);
     if (!fn) return fail(ETXMK_EINVAL, "no persistent kernel for H %d, NH*HD %d, %s %d (use the unfused mode)", c.H,
                          c.NH * c.HD, c.moe ? "MI" : "I", c.moe ? c.MI : c.I);
     p.bar_base = h->bar_epoch;

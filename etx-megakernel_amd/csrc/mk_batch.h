@@ -271,8 +271,8 @@ __device__ __forceinline__ bool gemv_run_b(int ngroups, RowF rowf, NVF nvec, XF 
     Regs R[D][NR];
     const bool any = gw < ngroups;
     const int last = any ? gw + (ngroups - 1 - gw) / nw * nw : 0;
-    auto issue = [&](Regs(&Rb)[NR], int g) {
-      const int gc = g <= last ? g : last;
+    auto issue = [&](Regs(&Rb)[NR], int g) {             // the lane per issue and per compute, held by neither
+      const int gc = g <= last ? g : last, lane = lane_id();
       const uint8_t* r0 = rowf(gc, 0);
 #pragma unroll
       for (int i = 0; i < NR; ++i) {
@@ -281,7 +281,7 @@ __device__ __forceinline__ bool gemv_run_b(int ngroups, RowF rowf, NVF nvec, XF 
       }
     };
     auto compute = [&](const Regs(&Rb)[NR], int g) {
-      const int nv = nvec(g);
+      const int nv = nvec(g), lane = lane_id();
       float v[NR][B];
       dot_rows_any<WR, NR, B>(Rb, [&](int b) { return xvec(g, b); }, nv, lane, v);
       epi(g, nv, v);
@@ -474,9 +474,10 @@ __device__ __forceinline__ void phase_attn_b(const Params& p, int layer, S& s, W
         const int tb = t0 + wave * 8;                     // 8 positions per 16-byte load
         if (tb < t0 + len && tb < fp) {
           const uint16_t* vp = Lw.vc + ((size_t)kb.v[ci] * NKV + g) * HD * BS + tb % BS;
-          __builtin_amdgcn_global_load_lds((const MK_G void*)(vp + (size_t)lane * BS),
+          const int lo = lane_id() * BS;                  // dim lane, lane + 64 (recomputed per load)
+          __builtin_amdgcn_global_load_lds((const MK_G void*)(vp + lo),
                                            (__attribute__((address_space(3))) void*)&s.a.vt[buf][ci][wave][0][0], 16, 0, 0);
-          __builtin_amdgcn_global_load_lds((const MK_G void*)(vp + (size_t)(lane + 64) * BS),
+          __builtin_amdgcn_global_load_lds((const MK_G void*)(vp + lo + 64 * BS),
                                            (__attribute__((address_space(3))) void*)&s.a.vt[buf][ci][wave][1][0], 16, 0, 0);
         }
       }
@@ -914,40 +915,26 @@ __device__ __forceinline__ mk_bf16x8 e4m3_half_bf16(const u32x4& c, int h) {
   return __builtin_bit_cast(mk_bf16x8, o);
 }
 
-template <class WR, int B, int EC, class S, class Wait>
-__device__ __forceinline__ void phase_expert_up_mfma(const Params& p, int layer, S& s, Wait wait) {
+// The tile engine: tiles t = gw, gw + nw, ... of the calling wave; tile t's A rows are rowf(t) (the format row of
+// the lane's row, l % 16 of the tile), its B columns colf(t, has) (the LDS input row of the lane's column; has = false
+// makes the column zero, and the row returned must still be an LDS row of KK elements); epi(t, v) receives D rows 4q .. 4q + 3 of the lane's column (fp8: times each row's scale).  The first
+// block's loads are issued before prologue() (which may wait and synchronise the workgroup; every thread calls it
+// once); rowf must then not depend on what the prologue waits for.
+template <class WR, class RowF, class ColF, class EpiF, class Pro>
+__device__ __forceinline__ bool mfma_tiles(const Params& p, int ntile, RowF rowf, ColF colf, EpiF epi, Pro prologue,
+                                           int s_phase) {
   constexpr int KK = WR::K;
   constexpr bool F8 = WR::FP8;
   constexpr int NBLK = F8 ? KK / 1024 : KK / 512;
   static_assert(KK % (F8 ? 1024 : 512) == 0 && NBLK >= 1, "the tile path takes whole blocks");
-  const LayerW Lw = layer_w(p, layer);
-  const int MI = p.MI, KT = p.TOPK, nb = p.B;
-  const uint8_t* W = Lw.w13;
-  build_norm_xb<KK, B>(p, false, Lw.ln2, s);              // x is final since the O projection
-  if (!wait()) return;
-  route_all<B, EC>(p, s);
-  if (blockIdx.x == 0) {
-    for (int t = threadIdx.x; t < nb * KT; t += NT) {
-      const int b = t / KT, k = t - b * KT;
-      if (p.dump_ids) st_i(p.dump_ids + ((size_t)layer * nb + b) * KT + k, s.rids[b][k]);
-      if (p.dump_wts) st_f(p.dump_wts + ((size_t)layer * nb + b) * KT + k, s.rwts[b][k]);
-    }
-    if (p.dump_logits)
-      for (int t = threadIdx.x; t < nb * p.E; t += NT) st_f(p.dump_logits + (size_t)layer * nb * p.E + t, ld_ag(p.logits + t));
-  }
-  const int TPE = (2 * MI) / 16, ntile = s.nexp * TPE;
-  const int lane = lane_id(), r = lane & 15, q = lane >> 4;
   const int gw = blockIdx.x * NWAVE + wave_u(), nw = p.nwg * NWAVE;
   const int nitem = (gw < ntile ? (ntile - 1 - gw) / nw + 1 : 0) * NBLK;
-  if (nitem == 0) return;
   const uint8_t* sinkp = (const uint8_t*)sink_of(p);
-  auto row_of = [&](int it) -> const uint8_t* {
-    const int t = gw + (it / NBLK) * nw, u = t / TPE, jt = t - u * TPE;
-    return mrow<WR>(W, (size_t)s.uexp[u] * 2 * MI + 16 * jt + r);
-  };
+  // the lane's quad, recomputed at each use (lane_id: no lane-dependent address is held across phases)
   auto issue = [&](int it, u32x4(&R)[16], float& sc) {
+    const int q = lane_id() >> 4;
     const bool ok = it < nitem;
-    const uint8_t* row = ok ? row_of(it) : sinkp;
+    const uint8_t* row = ok ? rowf(gw + (it / NBLK) * nw) : sinkp;
     const uint8_t* base = ok ? row + 1024 * (it % NBLK) + 16 * q : sinkp + 16 * q;
     const int step = ok ? 64 : 0;
     // ordinary (cached) loads: a wave's load of one slot column reads 64 bytes of each of its 16 rows, and the next
@@ -959,11 +946,10 @@ __device__ __forceinline__ void phase_expert_up_mfma(const Params& p, int layer,
   };
   mk_f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
   auto compute = [&](int it, const u32x4(&R)[16], float sc) {
-    const int blk = it % NBLK, t = gw + (it / NBLK) * nw, u = t / TPE, jt = t - u * TPE;
-    const int p0 = s.ustart[u], nv = s.ustart[u + 1] - p0;
+    const int blk = it % NBLK, t = gw + (it / NBLK) * nw, q = lane_id() >> 4;
     if (blk == 0) acc = mk_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    const bool has = r < nv;                              // MFMA column r: the expert's r-th routed sequence
-    const uint16_t* xb = s.n.xs + (size_t)(has ? s.pseq[p0 + r] : 0) * KK + 8 * q;
+    bool has;
+    const uint16_t* xb = colf(t, has) + 8 * q;
     auto xop = [&](int xblk, int i) -> mk_bf16x8 {
       const u32x4 v = *(const u32x4*)(xb + 512 * xblk + 32 * i);
       return __builtin_bit_cast(mk_bf16x8, has ? v : u32x4{0u, 0u, 0u, 0u});
@@ -989,19 +975,16 @@ __device__ __forceinline__ void phase_expert_up_mfma(const Params& p, int layer,
       float v[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) v[i] = F8 ? acc[i] * __shfl(sc, 4 * q + i) : acc[i];   // row 4q + i's scale
-      const int j0 = 8 * jt + 2 * q;                      // rows 4q, 4q+1: pair j0; rows 4q+2, 4q+3: pair j0 + 1
-      const float h0 = bfr(bfr(silu(bfr(v[0]))) * bfr(v[1]));
-      const float h1 = bfr(bfr(silu(bfr(v[2]))) * bfr(v[3]));
-      uint16_t* hrow = p.h16 + (size_t)(p0 + r) * MI;
-      st_ag_u16(has ? hrow + perm_stored(j0, MI) : (uint16_t*)sink_of(p), f2bf(h0));
-      st_ag_u16(has ? hrow + perm_stored(j0 + 1, MI) : (uint16_t*)sink_of(p), f2bf(h1));
+      epi(t, v);
     }
   };
   u32x4 R0[16], R1[16];
   float sc0 = 1.0f, sc1 = 1.0f;
   issue(0, R0, sc0);
   if (p.trace && threadIdx.x == 0)
-    *(MK_G uint64_t*)(p.trace + ((size_t)s.phase * p.nwg + blockIdx.x) * 3 + 2) = __builtin_amdgcn_s_memrealtime();
+    *(MK_G uint64_t*)(p.trace + ((size_t)s_phase * p.nwg + blockIdx.x) * 3 + 2) = __builtin_amdgcn_s_memrealtime();
+  if (!prologue()) return false;
+  if (nitem == 0) return true;
   for (int it = 0;;) {
     issue(it + 1, R1, sc1);
     compute(it, R0, sc0);
@@ -1010,6 +993,220 @@ __device__ __forceinline__ void phase_expert_up_mfma(const Params& p, int layer,
     compute(it, R1, sc1);
     if (++it >= nitem) break;
   }
+  return true;
+}
+
+template <class WR, int B, int EC, class S, class Wait>
+__device__ __forceinline__ void phase_expert_up_mfma(const Params& p, int layer, S& s, Wait wait) {
+  constexpr int KK = WR::K;
+  const LayerW Lw = layer_w(p, layer);
+  const int MI = p.MI, KT = p.TOPK, nb = p.B;
+  const uint8_t* W = Lw.w13;
+  build_norm_xb<KK, B>(p, false, Lw.ln2, s);              // x is final since the O projection
+  if (!wait()) return;
+  route_all<B, EC>(p, s);
+  if (blockIdx.x == 0) {
+    for (int t = threadIdx.x; t < nb * KT; t += NT) {
+      const int b = t / KT, k = t - b * KT;
+      if (p.dump_ids) st_i(p.dump_ids + ((size_t)layer * nb + b) * KT + k, s.rids[b][k]);
+      if (p.dump_wts) st_f(p.dump_wts + ((size_t)layer * nb + b) * KT + k, s.rwts[b][k]);
+    }
+    if (p.dump_logits)
+      for (int t = threadIdx.x; t < nb * p.E; t += NT) st_f(p.dump_logits + (size_t)layer * nb * p.E + t, ld_ag(p.logits + t));
+  }
+  const int TPE = (2 * MI) / 16;
+  mfma_tiles<WR>(
+      p, s.nexp * TPE,
+      [&](int t) {
+        const int u = t / TPE, jt = t - u * TPE, r = lane_id() & 15;
+        return mrow<WR>(W, (size_t)s.uexp[u] * 2 * MI + 16 * jt + r);
+      },
+      [&](int t, bool& has) -> const uint16_t* {         // column r: the expert's r-th routed sequence
+        const int u = t / TPE, p0 = s.ustart[u], r = lane_id() & 15;
+        has = r < s.ustart[u + 1] - p0;
+        return s.n.xs + (size_t)(has ? s.pseq[p0 + r] : 0) * KK;
+      },
+      [&](int t, const float(&v)[4]) {                    // rows 4q, 4q+1: pair j0; rows 4q+2, 4q+3: pair j0 + 1
+        const int u = t / TPE, jt = t - u * TPE, p0 = s.ustart[u], r = lane_id() & 15, q = lane_id() >> 4;
+        const bool has = r < s.ustart[u + 1] - p0;
+        const int j0 = 8 * jt + 2 * q;
+        const float h0 = bfr(bfr(silu(bfr(v[0]))) * bfr(v[1]));
+        const float h1 = bfr(bfr(silu(bfr(v[2]))) * bfr(v[3]));
+        uint16_t* hrow = p.h16 + (size_t)(p0 + r) * MI;
+        st_ag_u16(has ? hrow + perm_stored(j0, MI) : (uint16_t*)sink_of(p), f2bf(h0));
+        st_ag_u16(has ? hrow + perm_stored(j0 + 1, MI) : (uint16_t*)sink_of(p), f2bf(h1));
+      },
+      [&]() { return true; }, s.phase);
+}
+
+// The split form for the dense projections, whose few tiles would leave most waves idle as whole-row chains: tile t
+// belongs to workgroup t % nwg as its local tile t / nwg; local item j (tile j / NBLK, block j % NBLK) goes to wave
+// j % NWAVE in round j / NWAVE.  Each item runs its block's MFMA chain from zero; the NBLK partial tiles meet in LDS
+// and the wave of block 0 adds them as a pairwise tree ((P0 + P1) + (P2 + P3)) ..., scales (fp8) and hands the
+// lane's four D rows to epi(t, v).  Round 0's loads are issued before prologue(), each later round's one round ahead.
+template <class WR, class S, class RowF, class ColF, class EpiF, class Pro>
+__device__ __forceinline__ bool mfma_tiles_split(const Params& p, S& s, int ntile, RowF rowf, ColF colf, EpiF epi,
+                                                 Pro prologue) {
+  constexpr int KK = WR::K;
+  constexpr bool F8 = WR::FP8;
+  constexpr int NBLK = F8 ? KK / 1024 : KK / 512;
+  static_assert(KK % (F8 ? 1024 : 512) == 0 && NBLK >= 1 && NWAVE % NBLK == 0, "a round holds whole tiles");
+  static_assert(sizeof(s.v.xres) + sizeof(s.v.acc) >= sizeof(float) * NWAVE * 256 &&
+                    offsetof(S, v.acc) == offsetof(S, v.xres) + sizeof(s.v.xres),
+                "the partial tiles live in the residual and combine slots");
+  float* part = &s.v.xres[0][0];                          // [wave][lane][4]
+  const int w = wave_u(), wg = blockIdx.x, nwg = p.nwg;
+  const int nit = (wg < ntile ? (ntile - 1 - wg) / nwg + 1 : 0) * NBLK;
+  const int nround = (nit + NWAVE - 1) / NWAVE;
+  auto tile_of = [&](int j) { return wg + (j / NBLK) * nwg; };
+  auto issue = [&](int j, u32x4(&R)[16], float& sc) {    // j < nit
+    const int q = lane_id() >> 4;
+    const uint8_t* row = rowf(tile_of(j));
+    const uint8_t* base = row + 1024 * (j % NBLK) + 16 * q;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) R[i] = ld16(base + 64 * i);
+    if constexpr (F8) sc = ld_f((const float*)(row + KK));
+  };
+  auto round = [&](int r, const u32x4(&Rc)[16], float scc, u32x4(&Rn)[16], float& scn) {
+    const int j = r * NWAVE + w, lane = lane_id(), q = lane >> 4;
+    if (j + NWAVE < nit) issue(j + NWAVE, Rn, scn);
+    if (j < nit) {
+      const int blk = j % NBLK;
+      bool has;
+      const uint16_t* xb = colf(tile_of(j), has) + 8 * q;
+      auto xop = [&](int xblk, int i) -> mk_bf16x8 {
+        const u32x4 v = *(const u32x4*)(xb + 512 * xblk + 32 * i);
+        return __builtin_bit_cast(mk_bf16x8, has ? v : u32x4{0u, 0u, 0u, 0u});
+      };
+      mk_f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+      if constexpr (!F8) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(mk_bf16x8, Rc[i]), xop(blk, i), acc, 0, 0, 0);
+      } else {
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int i = 0; i < 16; ++i)
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(e4m3_half_bf16(Rc[i], h), xop(2 * blk + h, i), acc, 0, 0, 0);
+      }
+      // the chain's last result is read by VALU next: the wait states the compiler's own s_nop 7 leaves were found
+      // too few for the gate/up tiles (4 of 32 768 values read early); 18, fenced against rescheduling
+      __builtin_amdgcn_sched_barrier(0);
+      asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 1" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);
+      *(mk_f32x4*)(part + 4 * (w * 64 + lane)) = acc;
+    }
+    __syncthreads();
+    if (j < nit && j % NBLK == 0) {
+      float t[NBLK][4];
+#pragma unroll
+      for (int k = 0; k < NBLK; ++k) {
+        const mk_f32x4 v = *(const mk_f32x4*)(part + 4 * ((w + k) * 64 + lane));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) t[k][i] = v[i];
+      }
+#pragma unroll
+      for (int width = 1; width < NBLK; width *= 2)
+#pragma unroll
+        for (int k = 0; k + width < NBLK; k += 2 * width)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) t[k][i] = t[k][i] + t[k + width][i];
+      float v[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = F8 ? t[0][i] * __shfl(scc, 4 * q + i) : t[0][i];   // row 4q + i's scale
+      epi(tile_of(j), v);
+    }
+    __syncthreads();                                      // the partial slots are the next round's
+  };
+  u32x4 R0[16], R1[16];
+  float sc0 = 1.0f, sc1 = 1.0f;
+  if (w < nit) issue(w, R0, sc0);
+  if (p.trace && threadIdx.x == 0)
+    *(MK_G uint64_t*)(p.trace + ((size_t)s.phase * p.nwg + blockIdx.x) * 3 + 2) = __builtin_amdgcn_s_memrealtime();
+  if (!prologue()) return false;
+  for (int r = 0; r < nround;) {
+    round(r, R0, sc0, R1, sc1);
+    if (++r >= nround) break;
+    round(r, R1, sc1, R0, sc0);
+    ++r;
+  }
+  return true;
+}
+
+// P1 on the matrix cores (p.mfma): tiles of 16 QKV rows against every sequence's normed row (the columns), split by
+// block; the first blocks issued before the wait
+template <class WR, int B, class S, class Wait>
+__device__ __forceinline__ void phase_qkv_mfma(const Params& p, int layer, S& s, Wait wait) {
+  constexpr int KK = WR::K;
+  const LayerW Lw = layer_w(p, layer);
+  const bool first = layer == p.l0 && p.do_embed;
+  const int rows = p.nqkv, nb = p.B;
+  const uint8_t* W = Lw.wqkv;
+  mfma_tiles_split<WR>(
+      p, s, rows / 16, [&](int t) { return mrow<WR>(W, (size_t)16 * t + (lane_id() & 15)); },
+      [&](int, bool& has) -> const uint16_t* {
+        const int r = lane_id() & 15;
+        has = r < nb;
+        return s.n.xs + (size_t)(has ? r : 0) * KK;
+      },
+      [&](int t, const float(&v)[4]) {
+        const int r = lane_id() & 15, q = lane_id() >> 4;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int row = 16 * t + 4 * q + i;
+          st_ag(r < nb ? p.qkv + (size_t)r * rows + row : sink_of(p), bfr(v[i]));
+        }
+      },
+      [&]() {
+        if (!wait()) return false;
+        build_norm_xb<KK, B>(p, first, Lw.ln1, s);
+        if (blockIdx.x == 0) {
+          if (p.dump_x && layer > p.l0)
+            for (int i = threadIdx.x; i < nb * KK; i += NT)
+              st_f(p.dump_x + (size_t)(layer - 1) * nb * KK + i, bf2f(s.n.xr[i]));
+          if (layer == p.l0 && p.do_head && (int)threadIdx.x < nb)
+            __hip_atomic_store(p.amax + 32 * threadIdx.x, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        return true;
+      });
+}
+
+// P3 on the matrix cores (p.mfma): tiles of 16 output rows of the O projection against every sequence's attention
+// output (copied into LDS after the wait), split by block, plus the residual read per (row, sequence)
+template <class WR, int B, class S, class Wait>
+__device__ __forceinline__ void phase_oproj_mfma(const Params& p, int layer, S& s, Wait wait) {
+  constexpr int KK = WR::K;
+  static_assert(B * KK <= S::XCAP, "attention rows exceed the LDS budget");
+  const LayerW Lw = layer_w(p, layer);
+  const int H = p.H, nb = p.B;
+  const bool first = layer == p.l0 && p.do_embed;
+  const uint8_t* W = Lw.wo;
+  mfma_tiles_split<WR>(
+      p, s, H / 16, [&](int t) { return mrow<WR>(W, (size_t)16 * t + (lane_id() & 15)); },
+      [&](int, bool& has) -> const uint16_t* {
+        const int r = lane_id() & 15;
+        has = r < nb;
+        return s.v.xs + (size_t)(has ? r : 0) * KK;
+      },
+      [&](int t, const float(&v)[4]) {
+        const int r = lane_id() & 15, q = lane_id() >> 4;
+        const int b = r < nb ? r : 0;
+        const int tok = first ? token_of_b(p, b) : 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int g = 16 * t + 4 * q + i;
+          const float xres = first ? bf2f(ld_u16(p.embed + (size_t)tok * H + g)) : bf2f(ld_ag_u16(p.x16 + (size_t)b * H + g));
+          st_ag_u16(r < nb ? p.x16 + (size_t)b * H + g : (uint16_t*)sink_of(p), f2bf(xres + bfr(v[i])));
+        }
+      },
+      [&]() {
+        if (!wait()) return false;
+        copy_rows_lds(p.o16, nb * KK, s.v.xs);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        return true;
+      });
 }
 
 // P6: expert down, routing weight, combine per sequence in ascending expert id, residual (ref_numpy.py:146-148).
@@ -1216,8 +1413,18 @@ __device__ __forceinline__ void fused_body_b(const Params& p) {
   auto wait = [&]() { return grid_wait(p, k, s); };
   if (p.trace && threadIdx.x == 0) *(MK_G uint64_t*)(p.trace + (size_t)blockIdx.x * 3) = __builtin_amdgcn_s_memrealtime();
   s.phase = 0;
+  // the matrix-core forms (p.mfma, set by the host for MoE handles of batch capacity >= 8 whose shapes take whole
+  // tiles): the dense projections and the expert gate/up rows in 16-row tiles against up to 16 sequence columns
+  constexpr int TB = FP8 ? 1024 : 512;
+  constexpr bool TILES = MOE && B >= 8 && H % TB == 0 && KA % TB == 0 && H / TB <= NWAVE && KA / TB <= NWAVE &&
+                        (2 * KM) % 16 == 0;
   for (int layer = p.l0; layer < p.l1; ++layer) {
-    phase_qkv_b<RowOf<FP8, H>, B>(p, layer, s, wait);
+    if constexpr (TILES) {
+      if (p.mfma) phase_qkv_mfma<RowOf<FP8, H>, B>(p, layer, s, wait);
+      else phase_qkv_b<RowOf<FP8, H>, B>(p, layer, s, wait);
+    } else {
+      phase_qkv_b<RowOf<FP8, H>, B>(p, layer, s, wait);
+    }
     if (s.abort) return;
     grid_arrive(p, k, s);
     phase_attn_b<B>(p, layer, s, wait);
@@ -1226,14 +1433,19 @@ __device__ __forceinline__ void fused_body_b(const Params& p) {
     phase_attn_merge_b<B>(p, s, wait);
     if (s.abort) return;
     grid_arrive(p, k, s);
-    phase_oproj_b<RowOf<FP8, KA>, B>(p, layer, s, wait);
+    if constexpr (TILES) {
+      if (p.mfma) phase_oproj_mfma<RowOf<FP8, KA>, B>(p, layer, s, wait);
+      else phase_oproj_b<RowOf<FP8, KA>, B>(p, layer, s, wait);
+    } else {
+      phase_oproj_b<RowOf<FP8, KA>, B>(p, layer, s, wait);
+    }
     if (s.abort) return;
     grid_arrive(p, k, s);
     if constexpr (MOE) {
       phase_router_b<H, B>(p, layer, s, wait);
       if (s.abort) return;
       grid_arrive(p, k, s);
-      if constexpr (B >= 8 && H % (FP8 ? 1024 : 512) == 0 && (2 * KM) % 16 == 0) {
+      if constexpr (TILES) {
         if (p.mfma) phase_expert_up_mfma<RowOf<FP8, H>, B, EC>(p, layer, s, wait);
         else phase_expert_up_b<RowOf<FP8, H>, B, EC>(p, layer, s, wait);
       } else {

@@ -1,4 +1,5 @@
 // The batched persistent kernels with bf16 weights (one translation unit per list, compiled in parallel).
+#define MK_LANE_OPAQUE 1   // lane_id() kept local to each phase (mk_device.h)
 #include "mk_batch.h"
 
 namespace mk {

@@ -141,7 +141,19 @@ struct Smem {
   int32_t phase;                        // arrivals so far (the current phase index), for trace stamps
 };
 
-__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+// The lane.  Translation units that define MK_LANE_OPAQUE (the batched kernels) put it behind an empty volatile asm
+// so that what is computed from it stays where it is computed: the compiler cannot hoist the asm, so no
+// lane-dependent offset or address is lifted out of the layer loop to hold registers through every phase.  With
+// plain threadIdx.x & 63 such hoisted values pushed the batch-16 kernels to 256 VGPRs with 31 to 78 spilled, and a
+// spill reloaded inside a pipelined loop waits for every load still in flight (vmcnt counts in order): +8 us per layer
+// in the batch-16 attention phase.  The single-sequence kernels fit without it and run 2% faster with the hoisting.
+__device__ __forceinline__ int lane_id() {
+  int l = threadIdx.x & 63;
+#ifdef MK_LANE_OPAQUE
+  asm volatile("" : "+v"(l));
+#endif
+  return l;
+}
 // one layer's pointer table, read through the constant address space (scalar loads)
 __device__ __forceinline__ LayerW layer_w(const Params& p, int layer) {
   static_assert(sizeof(LayerW) % 8 == 0, "pointer table");

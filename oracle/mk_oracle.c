@@ -440,7 +440,8 @@ typedef struct {
   float *rcos, *rsin;             /* DeepSeek-V2: fp32 yarn tables [max_ctx][qk_rope / 2] */
   float scale;
   float attn_scale;
-  int mfma;                       /* expert gate/up rows in the matrix-core order (batched kernels of capacity >= 8) */
+  int mfma;                       /* QKV, O and expert gate/up rows in the matrix-core order (batched kernels of
+                                     capacity >= 8) */
 } orc_model;
 
 static uint16_t* gen_tensor(uint64_t seed, uint64_t stream, size_t n, float scale) {
@@ -479,9 +480,12 @@ EXPORT void* orc_model_create(const orc_config* cfg, uint64_t seed, float wscale
   m->embed = gen_tensor(seed, sid(S_EMBED, -1, 0), (size_t)c->V * c->H, wscale);
   m->lm_head = gen_tensor(seed, sid(S_LMHEAD, -1, 0), (size_t)c->V * c->H, wscale);
   m->batch = c->batch > 1 ? c->batch : 1;
-  /* the library's rule for its matrix-core gate/up tiles (etxmk_config: batch capacity >= 8, MoE, whole blocks) */
-  m->mfma = c->batch >= 8 && c->moe && c->wdtype != 2 && c->H % (c->wdtype == 1 ? 1024 : 512) == 0 &&
-            (2 * c->MI) % 16 == 0;
+  /* the library's rule for its matrix-core tiles (etxmk_config: batch capacity >= 8, MoE, whole blocks) */
+  {
+    const int tb = c->wdtype == 1 ? 1024 : 512;
+    m->mfma = c->batch >= 8 && c->moe && c->wdtype != 2 && c->H % tb == 0 && c->H / tb <= 8 &&
+              (c->NH * c->HD) % tb == 0 && (c->NH * c->HD) / tb <= 8 && (2 * c->MI) % 16 == 0;
+  }
   m->nbps = (c->max_ctx + c->block_size - 1) / c->block_size;
   m->nblocks = m->batch * m->nbps;               /* one paged pool shared by the sequences of the batch */
   m->btab = (int32_t*)malloc(sizeof(int32_t) * (size_t)m->nblocks);
@@ -581,6 +585,13 @@ static void gemv_bf(const uint16_t* W, int R, int K, const float* x, float* out)
 /* one decoder layer at position pos on residual x (in place) of the sequence whose block table is bt;
  * dump_ids / dump_wts / dump_logits optional */
 static float gateup_dot(const orc_model* m, const orc_mat* W, int wdtype, size_t r, const float* x, int K);
+static void gemv_rows_tiles(const orc_mat* W, int wdtype, int R, int K, const float* X, int ldx, int n, float* out,
+                            int ldo);
+/* a dense projection of one vector: the matrix-core tile order for models whose batched kernel uses it */
+static void proj_mat(const orc_model* m, const orc_mat* W, int wdtype, int R, int K, const float* x, float* out) {
+  if (m->mfma) gemv_rows_tiles(W, wdtype, R, K, x, K, 1, out, R);
+  else gemv_mat(W, wdtype, R, K, x, out);
+}
 static void layer_step(orc_model* m, int l, float* x, int pos, const int32_t* bt, int32_t* ids_out, float* wts_out,
                        float* logits_out) {
   const orc_config* c = &m->c;
@@ -592,7 +603,7 @@ static void layer_step(orc_model* m, int l, float* x, int pos, const int32_t* bt
   float* o = (float*)malloc(sizeof(float) * (size_t)NH * HD);
   rmsnorm(x, NULL, H, c->eps, xs);                                 /* input_layernorm (weight 1.0) */
   const int wt = c->wdtype;
-  gemv_mat(&y->wqkv, wt, NQKV, H, xs, qkv);                         /* :112-115 */
+  proj_mat(m, &y->wqkv, wt, NQKV, H, xs, qkv);                     /* :112-115 */
   const float* cs = m->rcos + (size_t)pos * (HD / 2);
   const float* sn = m->rsin + (size_t)pos * (HD / 2);
   float tmp[512];
@@ -611,7 +622,7 @@ static void layer_step(orc_model* m, int l, float* x, int pos, const int32_t* bt
   for (int hh = 0; hh < NH; ++hh)                                   /* :122-129 */
     attention_head(qkv + (size_t)hh * HD, y->kc, y->vc, bt, pos + 1, hh / G, NKV, HD, BS, o + (size_t)hh * HD);
   float* t = (float*)malloc(sizeof(float) * (size_t)(H > c->I ? H : c->I) * 2 + 64);
-  gemv_mat(&y->wo, wt, H, NH * HD, o, t);                           /* :130 */
+  proj_mat(m, &y->wo, wt, H, NH * HD, o, t);                       /* :130 */
   for (int i = 0; i < H; ++i) x[i] = bfr(x[i] + t[i]);
   rmsnorm(x, NULL, H, c->eps, xs);                                 /* :131 post_attention_layernorm */
   if (c->moe) {
@@ -914,6 +925,52 @@ static void gemv_rows_multi(const orc_mat* W, int wdtype, int R, int K, const fl
   }
 }
 
+/* a dense projection row's value before scaling in the split order (decomposed operands in the tile order, blocks of
+ * TBK, a power-of-two count up to 8): each block's chain from zero, then the pairwise tree of the partials */
+static float proj_split_dot(const int16_t* am, const int16_t* ae, const int16_t* bm, const int16_t* be, int K, int TBK) {
+  const int nb = K / TBK;
+  float t[8];
+  for (int k = 0; k < nb; ++k) t[k] = mfma_dot_split(am + k * TBK, ae + k * TBK, bm + k * TBK, be + k * TBK, TBK);
+  for (int width = 1; width < nb; width *= 2)
+    for (int k = 0; k + width < nb; k += 2 * width) t[k] = t[k] + t[k + width];
+  return t[0];
+}
+EXPORT float orc_mfma_proj_dot(const float* w, const float* x, int K, int TBK) {
+  if (TBK <= 0 || K % TBK || K / TBK > 8 || ((K / TBK) & (K / TBK - 1))) return NAN;
+  int16_t* buf = (int16_t*)malloc(sizeof(int16_t) * 4 * (size_t)K);
+  mfma_split_row(w, K, buf, buf + K);
+  mfma_split_row(x, K, buf + 2 * K, buf + 3 * K);
+  const float r = proj_split_dot(buf, buf + K, buf + 2 * K, buf + 3 * K, K, TBK);
+  free(buf);
+  return r;
+}
+/* gemv_rows_multi in the batched kernels' split tile order for the dense projections: the row's blocks (512
+ * elements, 1024 for e4m3 rows) each run the tile chain from zero, and the partials are added as a pairwise tree
+ * ((P0 + P1) + (P2 + P3)) ... (a block count of 1, 2, 4 or 8), then scaled; each vector decomposed once, each row
+ * once per thread */
+static void gemv_rows_tiles(const orc_mat* W, int wdtype, int R, int K, const float* X, int ldx, int n, float* out,
+                            int ldo) {
+  const int TBK = wdtype == 1 ? 1024 : 512;
+  int16_t* xsp = (int16_t*)malloc(sizeof(int16_t) * 2 * (size_t)n * K);
+  for (int b = 0; b < n; ++b) mfma_split_row(X + (size_t)b * ldx, K, xsp + 2 * (size_t)b * K, xsp + (2 * (size_t)b + 1) * K);
+#pragma omp parallel
+  {
+    float* wf = (float*)malloc(sizeof(float) * (size_t)K);
+    int16_t* wsp = (int16_t*)malloc(sizeof(int16_t) * 2 * (size_t)K);
+#pragma omp for schedule(dynamic, 8)
+    for (int r = 0; r < R; ++r) {
+      const float sc = row_f32(W, wdtype, (size_t)r, K, wf);
+      mfma_split_row(wf, K, wsp, wsp + K);
+      for (int b = 0; b < n; ++b) {
+        const int16_t* xm = xsp + 2 * (size_t)b * K;
+        out[(size_t)b * ldo + r] = bfr(proj_split_dot(wsp, wsp + K, xm, xm + K, K, TBK) * sc);
+      }
+    }
+    free(wf); free(wsp);
+  }
+  free(xsp);
+}
+
 /* attention_head for every row's q heads (row r's at qkv + r * ldq).  Rows of one sequence share one gathered copy of
  * that sequence's cache, fp32 K^T [h][d][t] and V [h][t][d] over positions 0 .. (largest position of its rows): the
  * scores of eight positions are computed at a time (each one's fma chain over d ascending, as in attention_head),
@@ -1016,7 +1073,8 @@ static void layer_rows(orc_model* m, int l, float* X, int n, const orc_row* rows
   float* o = (float*)malloc(sizeof(float) * (size_t)n * NH * HD);
   float* t = (float*)malloc(sizeof(float) * (size_t)n * H);
   for (int b = 0; b < n; ++b) rmsnorm(X + (size_t)b * H, NULL, H, c->eps, xs + (size_t)b * H);
-  gemv_rows_multi(&y->wqkv, wt, NQKV, H, xs, H, n, qkv, NQKV);                /* :112-115 */
+  if (m->mfma) gemv_rows_tiles(&y->wqkv, wt, NQKV, H, xs, H, n, qkv, NQKV);   /* :112-115 */
+  else gemv_rows_multi(&y->wqkv, wt, NQKV, H, xs, H, n, qkv, NQKV);
 #pragma omp parallel for schedule(static)
   for (int b = 0; b < n; ++b) {                                                 /* :116-121 */
     float* q = qkv + (size_t)b * NQKV;
@@ -1037,7 +1095,8 @@ static void layer_rows(orc_model* m, int l, float* X, int n, const orc_row* rows
       }
   }
   attention_rows(y->kc, y->vc, rows, n, qkv, NQKV, NH, NKV, HD, BS, o);         /* :122-129 */
-  gemv_rows_multi(&y->wo, wt, H, NH * HD, o, NH * HD, n, t, H);                /* :130 */
+  if (m->mfma) gemv_rows_tiles(&y->wo, wt, H, NH * HD, o, NH * HD, n, t, H);  /* :130 */
+  else gemv_rows_multi(&y->wo, wt, H, NH * HD, o, NH * HD, n, t, H);
   for (size_t i = 0; i < (size_t)n * H; ++i) X[i] = bfr(X[i] + t[i]);
   for (int b = 0; b < n; ++b) rmsnorm(X + (size_t)b * H, NULL, H, c->eps, xs + (size_t)b * H);  /* :131 */
   if (c->moe) {

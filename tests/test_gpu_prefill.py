@@ -85,18 +85,21 @@ def test_tiny_prefill_fp8(gpu):
     run_prefill(cfg, 40, n_new=4, rows=16)
 
 
-def test_tiny_batched_handle_prefill_per_sequence(gpu):
-    """A batch-4 handle: each prompt prefilled on its own (4 positions per launch, other sequences untouched), then
-    batched decode from the end of each prompt; against the oracle's token-by-token decode of every prompt."""
-    cfg = configs.with_layers(configs.TINY_MOE, configs.TINY_MOE.L, batch=4)
-    say(f"[gpu] prefill per sequence, batch-4 handle {cfg.name}")
+@pytest.mark.parametrize("B", [4, 16], ids=["b4", "b16"])
+def test_tiny_batched_handle_prefill_per_sequence(gpu, B):
+    """A batch-B handle: each prompt prefilled on its own (B positions per launch, other sequences untouched), then
+    batched decode from the end of each prompt; against the oracle's token-by-token decode of every prompt.  At
+    batch 16 the handle's projections run on the matrix cores, the ragged last launches of fewer than 8 positions
+    included, and the oracle (a model of the same batch capacity) follows the tile order."""
+    cfg = configs.with_layers(configs.TINY_MOE, configs.TINY_MOE.L, batch=B)
+    say(f"[gpu] prefill per sequence, batch-{B} handle {cfg.name}")
     dec = N.Decoder(cfg)
     dec.init_weights(SEED, 0.02)
-    assert dec.prefill_rows == 4
-    prompts = [O.gen_tokens(SEED + b, 5 + 9 * b, cfg.V) for b in range(4)]
+    assert dec.prefill_rows == B
+    prompts = [O.gen_tokens(SEED + b, 5 + (9 if B == 4 else 7) * b, cfg.V) for b in range(B)]
     got = dec.generate_batch(prompts, 5, prefill=True)
     for b, p in enumerate(prompts):
-        o = O.OracleModel(configs.TINY_MOE.as_dict(), SEED, 0.02)
+        o = O.OracleModel(cfg.as_dict(), SEED, 0.02)
         toks = list(p)
         for q in range(len(p) + 4):
             t = o.step(toks[q], q)

@@ -93,3 +93,36 @@ def test_tile_dot_is_the_step_chain_in_tile_order(K, fp8):
         want = L.orc_mfma_bf16_chain(0.0, H.bf16_bits(w[order]), H.bf16_bits(x[order]), K // 32)
         got = L.orc_mfma_tile_dot(np.ascontiguousarray(w), np.ascontiguousarray(x), K)
         assert np.float32(got).tobytes() == np.float32(want).tobytes()
+
+
+@pytest.mark.parametrize("K,fp8", [(512, False), (2048, False), (4096, False), (2048, True), (4096, True)])
+def test_projection_dot_is_the_block_chains_summed_as_a_tree(K, fp8):
+    """orc_mfma_proj_dot (the dense projections' split order: each 512-block, 1024 for e4m3 rows, chained from zero
+    on its own, the partials added pairwise ((P0 + P1) + (P2 + P3)) ...) against the chains of the permuted operands
+    added in float32 here; and the split differs from the whole-row chain on some rows, so a projection stated with
+    the gate/up order would fail the GPU parity tests."""
+    L = O.lib()
+    order = tile_order(K)
+    tbk = 1024 if fp8 else 512
+    nb = K // tbk
+    rng = np.random.default_rng(K + 7 * fp8)
+    differs = 0
+    for _ in range(20):
+        if fp8:
+            codes = rng.integers(0, 256, K).astype(np.uint8)
+            codes[(codes & 0x7F) == 0x7F] = 0
+            w = np.array([L.orc_e4m3_to_f32(int(c)) for c in codes], np.float32)
+        else:
+            w = O.bf16_bits_to_f32(H.bf16_bits(rng.standard_normal(K) * 0.02))
+        x = O.bf16_bits_to_f32(H.bf16_bits(rng.standard_normal(K)))
+        a, b = H.bf16_bits(w[order]), H.bf16_bits(x[order])
+        parts = [np.float32(L.orc_mfma_bf16_chain(0.0, np.ascontiguousarray(a[k * tbk:(k + 1) * tbk]),
+                                                  np.ascontiguousarray(b[k * tbk:(k + 1) * tbk]), tbk // 32))
+                 for k in range(nb)]
+        while len(parts) > 1:
+            parts = [np.float32(parts[i] + parts[i + 1]) for i in range(0, len(parts), 2)]
+        got = L.orc_mfma_proj_dot(np.ascontiguousarray(w), np.ascontiguousarray(x), K, tbk)
+        assert np.float32(got).tobytes() == parts[0].tobytes()
+        differs += np.float32(got) != np.float32(L.orc_mfma_tile_dot(np.ascontiguousarray(w), np.ascontiguousarray(x), K))
+    assert nb == 1 or differs > 0
+    assert np.isnan(L.orc_mfma_proj_dot(np.zeros(1536, np.float32), np.zeros(1536, np.float32), 1536, 512))
