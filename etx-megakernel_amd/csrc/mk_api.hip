@@ -212,15 +212,24 @@ const char* kernel_symbol(const etxmk_config& c, int* cap) {
   return best;
 }
 
+// The matrix-core rule: MoE Qwen3 handles of batch capacity >= 8 whose shapes take whole tiles run their batched
+// QKV, O projection, expert gate/up and expert down on the matrix cores (the down outputs combined in a phase of their
+// own).  The CPU oracle applies the same rule to the models of such handles.
+bool mfma_rule(const etxmk_config& c) {
+  const int tb = c.wdtype == ETXMK_W_FP8 ? 1024 : 512, ka = c.NH * c.HD;
+  return c.arch == ETXMK_ARCH_QWEN3 && c.batch >= 8 && c.moe && c.H % tb == 0 && c.H / tb <= NWAVE && ka % tb == 0 &&
+         ka / tb <= NWAVE && c.MI % 256 == 0 && c.MI <= 4096;
+}
+
 // grid barriers of a launch over layers [l0, l1) (plus the head), one per phase; `batched`: the batched kernel
-// (Qwen3: the attention merge is a phase of its own)
+// (Qwen3: the attention merge is a phase of its own; with the matrix-core rule, the expert combine too)
 int barriers_of(const etxmk_config& c, int l0, int l1, int head, bool batched) {
   if (c.arch == ETXMK_ARCH_DSV2) {                         // 5 attention phases, then 2 dense or 3 MoE phases
     int n = 0;
     for (int l = l0; l < l1; ++l) n += l < c.first_dense ? 7 : 8;
     return n + (head ? 1 : 0);
   }
-  return ((c.moe ? 6 : 5) + (batched ? 1 : 0)) * (l1 - l0) + (head ? 1 : 0);
+  return ((c.moe ? 6 : 5) + (batched ? 1 : 0) + (batched && mfma_rule(c) ? 1 : 0)) * (l1 - l0) + (head ? 1 : 0);
 }
 
 int check_config(const etxmk_config* c) {
@@ -337,7 +346,7 @@ uint64_t kv_layer_elems(const etxmk_config* c) {
 int kv_pools(const etxmk_config* c) { return c->arch == ETXMK_ARCH_DSV2 ? 1 : 2; }
 
 struct WsLayout {
-  uint64_t x, x16, qkv, o, o16, logits, hbuf, h16, apart, acnt, amax, bar, abort_w, tokens, out_tokens, btab, rcos, rsin,
+  uint64_t x, x16, qkv, o, o16, logits, hbuf, h16, ys, apart, acnt, amax, bar, abort_w, tokens, out_tokens, btab, rcos, rsin,
       layers, h16d, qc, h16s, sink, total;
 };
 
@@ -357,6 +366,7 @@ WsLayout ws_layout(const etxmk_config* c) {
   const int hb = c->moe ? c->TOPK * c->MI : c->I;
   w.hbuf = take(4ull * (hb > 0 ? hb : 1) * B);
   w.h16 = take(2ull * (hb > 0 ? hb : 1) * B);
+  w.ys = take(2ull * (c->moe ? c->TOPK : 1) * c->H * B);   // matrix-core expert down: weighted outputs per pair
   w.apart = take(4ull * c->NH * MAX_CHUNKS * (ds ? MLA_PART : PART) * B);
   w.acnt = take(4ull * 64 * 2 * (ds ? ds_nhg(*c) : c->NKV) * B); // one 256-byte line per (sequence, kv head / head group, half)
   w.amax = take(256ull * B);             // one 256-byte line per sequence
@@ -976,13 +986,7 @@ static int launch(etxmk_handle* h, const int32_t* posv, int pos, int write_next,
     p.qkv_lds_rows = ok ? S : 0;
   }
   p.B = nrows;
-  // batched QKV, O projection and MoE gate/up on the matrix cores: handles of batch capacity >= 8 with whole row
-  // blocks (the CPU oracle applies the same rule to the models of such handles)
-  {
-    const int tb = c.wdtype == ETXMK_W_FP8 ? 1024 : 512;
-    p.mfma = !ds && c.batch >= 8 && c.moe && c.H % tb == 0 && c.H / tb <= NWAVE && (c.NH * c.HD) % tb == 0 &&
-             (c.NH * c.HD) / tb <= NWAVE && (2 * c.MI) % 16 == 0;
-  }
+  p.mfma = mfma_rule(c);
   p.nbps = nbps_of(&c);
   p.tok_stride = c.max_ctx + 1;
   if (pf) {                                // every row reads the one sequence's block table and token rows
@@ -996,6 +1000,7 @@ static int launch(etxmk_handle* h, const int32_t* posv, int pos, int write_next,
   p.x16 = h->wsptr<uint16_t>(h->ws.x16);
   p.o16 = h->wsptr<uint16_t>(h->ws.o16);
   p.h16 = h->wsptr<uint16_t>(h->ws.h16);
+  p.ys = h->wsptr<uint16_t>(h->ws.ys);
   p.nqkv = nqkv_of(c);
   p.Ip = ds ? ds_ip(c) : c.I;
   p.h16d = h->wsptr<uint16_t>(h->ws.h16d);

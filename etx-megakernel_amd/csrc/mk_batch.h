@@ -62,6 +62,7 @@ struct SmemB {
   int32_t uexp[MAX_PAIRS];              // distinct experts ascending; expert u owns pairs [ustart[u], ustart[u + 1])
   int32_t ustart[MAX_PAIRS + 1];
   int32_t nexp;
+  int32_t bpair[B][MAX_TOPK];           // sequence b's pairs (indices into pexp..) in ascending expert order
   uint32_t kbits[KEY_WORDS];            // routing: bitmap of the pairs' keys, then their prefix popcounts
   uint32_t kpre[KEY_WORDS];
   int32_t abort, last, phase;
@@ -821,6 +822,9 @@ __device__ __forceinline__ void route_all(const Params& p, S& s) {
     s.pexp[rank] = s.rids[b][k];
     s.pseq[rank] = b;
     s.pw[rank] = s.rwts[b][k];
+    int j = 0;                                            // the pair's place among its sequence's experts
+    for (int k2 = 0; k2 < K; ++k2) j += s.rids[b][k2] < s.rids[b][k];
+    s.bpair[b][j] = rank;
   }
   __syncthreads();
   if (wave == 0) {                                         // first pair of each expert -> ustart
@@ -1032,9 +1036,13 @@ __device__ __forceinline__ void phase_expert_up_mfma(const Params& p, int layer,
         const int j0 = 8 * jt + 2 * q;
         const float h0 = bfr(bfr(silu(bfr(v[0]))) * bfr(v[1]));
         const float h1 = bfr(bfr(silu(bfr(v[2]))) * bfr(v[3]));
+        // h in the stored order of the down rows it meets (fp8 rows: blocks of 1024), the order the matrix-core
+        // down tiles chain over
         uint16_t* hrow = p.h16 + (size_t)(p0 + r) * MI;
-        st_ag_u16(has ? hrow + perm_stored(j0, MI) : (uint16_t*)sink_of(p), f2bf(h0));
-        st_ag_u16(has ? hrow + perm_stored(j0 + 1, MI) : (uint16_t*)sink_of(p), f2bf(h1));
+        const int s0 = WR::FP8 ? perm_stored8(j0, MI) : perm_stored(j0, MI);
+        const int s1 = WR::FP8 ? perm_stored8(j0 + 1, MI) : perm_stored(j0 + 1, MI);
+        st_ag_u16(has ? hrow + s0 : (uint16_t*)sink_of(p), f2bf(h0));
+        st_ag_u16(has ? hrow + s1 : (uint16_t*)sink_of(p), f2bf(h1));
       },
       [&]() { return true; }, s.phase);
 }
@@ -1299,6 +1307,147 @@ __device__ __forceinline__ void phase_expert_down_b(const Params& p, int layer, 
     }
 }
 
+// 8 e4m3 codes (two words) as 8 bf16 values, exactly (e4m3_half_bf16 on the low half of a 4-word vector)
+__device__ __forceinline__ mk_bf16x8 e4m3_8_bf16(const u32x2& c) { return e4m3_half_bf16(u32x4{c[0], c[1], 0u, 0u}, 0); }
+__device__ __forceinline__ u32x2 ld8(const void* p) { return *(const MK_G u32x2*)p; }
+
+// P6 on the matrix cores (p.mfma): tiles of 16 down rows of one expert against its routed pairs' h rows (the
+// columns), chained from zero over the rows' stored order in 32-element steps: per lane and step 16 bytes of a bf16
+// row or 8 bytes of an fp8 row (whose pairs' h rows the gate/up tiles store in the fp8 order).  Every (pair, row)
+// value y = bfr(bfr(d) * weight) goes to p.ys; the combine phase adds them per sequence in ascending expert order.
+// The U * H/16 tiles, expert-major, are cut into nwg contiguous ranges, one per workgroup: the workgroup stages the
+// h rows of its range's experts in LDS (as many experts at a time as fit) and its waves take the range's tiles
+// round-robin, each tile in chunks of 8 steps (256 elements) streamed through a ring of three (two in flight while
+// one is chained).  The first chunks are issued before the wait.
+template <class WR, int B, class S, class Wait>
+__device__ __forceinline__ void phase_expert_down_mfma(const Params& p, int layer, S& s, Wait wait) {
+  constexpr int KK = WR::K;
+  constexpr bool F8 = WR::FP8;
+  constexpr int NC = KK / 256;
+  static_assert(KK % 256 == 0, "down rows are whole chunks of 256");
+  static_assert(B * KK <= S::XCAP, "one expert's h rows must fit the LDS rows");
+  using Chunk = typename std::conditional<F8, u32x2, u32x4>::type;
+  const LayerW Lw = layer_w(p, layer);
+  const int H = p.H, HT = H / 16, U = s.nexp, w = wave_u(), wg = blockIdx.x, nwg = p.nwg;
+  const int T = U * HT;
+  const int ta = (int)((int64_t)T * wg / nwg), tb = (int)((int64_t)T * (wg + 1) / nwg);
+  const uint8_t* W = Lw.w2;
+  // a group: experts [u, ue] of the range whose pairs fit the LDS rows together (at least one expert)
+  auto group_end = [&](int u, int ulast) {
+    int ue = u;
+    while (ue < ulast && (s.ustart[ue + 2] - s.ustart[u]) * KK <= S::XCAP) ++ue;
+    return ue;
+  };
+  int u = ta < tb ? ta / HT : 0;
+  const int ulast = ta < tb ? (tb - 1) / HT : -1;
+  int ue = u <= ulast ? group_end(u, ulast) : -1;
+  int g0 = 0, nit = 0;
+  auto set_group = [&]() {
+    g0 = ta > u * HT ? ta : u * HT;
+    const int g1 = tb < (ue + 1) * HT ? tb : (ue + 1) * HT;
+    nit = (g0 + w < g1 ? (g1 - 1 - g0 - w) / NWAVE + 1 : 0) * NC;
+  };
+  auto tile_of = [&](int it) { return g0 + w + (it / NC) * NWAVE; };
+  auto issue = [&](int it, Chunk(&R)[8], float& sc) {    // item it < nit: chunk it % NC of tile tile_of(it)
+    const int t = tile_of(it), c = it % NC, ut = t / HT, lane = lane_id(), q = lane >> 4;
+    const uint8_t* row = mrow<WR>(W, (size_t)s.uexp[ut] * H + 16 * (t - ut * HT) + (lane & 15));
+    if constexpr (F8) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) R[i] = ld8(row + 256 * c + 32 * i + 8 * q);
+      sc = ld_f((const float*)(row + KK));
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) R[i] = ld16(row + 2 * (256 * c + 32 * i + 8 * q));
+    }
+  };
+  mk_f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  auto compute = [&](int it, const Chunk(&R)[8], float sc) {
+    const int t = tile_of(it), c = it % NC, ut = t / HT, lane = lane_id(), q = lane >> 4, r = lane & 15;
+    const int p0 = s.ustart[ut], np = s.ustart[ut + 1] - p0;
+    const bool has = r < np;                              // column r: the expert's r-th pair
+    const uint16_t* xb = s.v.xs + (size_t)(has ? p0 - s.ustart[u] + r : 0) * KK + 256 * c + 8 * q;
+    if (c == 0) acc = mk_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const u32x4 xv = *(const u32x4*)(xb + 32 * i);
+      const mk_bf16x8 bv = __builtin_bit_cast(mk_bf16x8, has ? xv : u32x4{0u, 0u, 0u, 0u});
+      mk_bf16x8 av;
+      if constexpr (F8) av = e4m3_8_bf16(R[i]);
+      else av = __builtin_bit_cast(mk_bf16x8, R[i]);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, acc, 0, 0, 0);
+    }
+    if (c == NC - 1) {
+      // the chain's last result read by VALU: 18 wait states, fenced (the compiler's s_nop 7 was found too few)
+      __builtin_amdgcn_sched_barrier(0);
+      asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 1" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);
+      const float pw = has ? s.pw[p0 + r] : 0.0f;
+      const int rt = t - ut * HT;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float v = F8 ? acc[i] * __shfl(sc, 4 * q + i) : acc[i];   // row 4q + i's scale
+        st_ag_u16(has ? p.ys + (size_t)(p0 + r) * H + 16 * rt + 4 * q + i : (uint16_t*)sink_of(p), f2bf(bfr(bfr(v) * pw)));
+      }
+    }
+  };
+  Chunk R0[8], R1[8], R2[8];
+  float c0 = 1.0f, c1 = 1.0f, c2 = 1.0f;
+  if (u <= ulast) {
+    set_group();
+    if (nit > 0) issue(0, R0, c0);
+    if (nit > 1) issue(1, R1, c1);
+  }
+  if (p.trace && threadIdx.x == 0)
+    *(MK_G uint64_t*)(p.trace + ((size_t)s.phase * p.nwg + blockIdx.x) * 3 + 2) = __builtin_amdgcn_s_memrealtime();
+  if (!wait()) return;
+  for (bool first = true; u <= ulast; first = false) {
+    if (!first) {
+      set_group();
+      if (nit > 0) issue(0, R0, c0);
+      if (nit > 1) issue(1, R1, c1);
+    }
+    const int pb = s.ustart[u];
+    __syncthreads();                                      // the previous group is done with the LDS rows
+    copy_rows_lds(p.h16 + (size_t)pb * KK, (s.ustart[ue + 1] - pb) * KK, s.v.xs);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    for (int it = 0; it < nit; it += 3) {
+      if (it + 2 < nit) issue(it + 2, R2, c2);
+      compute(it, R0, c0);
+      if (it + 1 >= nit) break;
+      if (it + 3 < nit) issue(it + 3, R0, c0);
+      compute(it + 1, R1, c1);
+      if (it + 2 >= nit) break;
+      if (it + 4 < nit) issue(it + 4, R1, c1);
+      compute(it + 2, R2, c2);
+    }
+    u = ue + 1;
+    if (u <= ulast) ue = group_end(u, ulast);
+  }
+}
+
+// P7 (p.mfma): per (sequence, row) the weighted expert outputs of P6 added in ascending expert order, then the
+// residual (ref_numpy.py:146-148); workgroup j takes rows [H j / nwg, H (j + 1) / nwg) of every sequence, each
+// thread one (sequence, row) with its TOPK values loaded together
+template <int B, class S, class Wait>
+__device__ __forceinline__ void phase_combine_mfma(const Params& p, S& s, Wait wait) {
+  const int H = p.H, nb = p.B, K = p.TOPK, wg = blockIdx.x, nwg = p.nwg;
+  const int g0 = (int)((int64_t)H * wg / nwg), R = (int)((int64_t)H * (wg + 1) / nwg) - g0;
+  if (!wait()) return;
+  for (int t = threadIdx.x; t < nb * R; t += NT) {
+    const int b = t / R, g = g0 + (t - b * R);
+    float y[MAX_TOPK];
+#pragma unroll
+    for (int j = 0; j < MAX_TOPK; ++j) y[j] = j < K ? bf2f(ld_ag_u16(p.ys + (size_t)s.bpair[b][j] * H + g)) : 0.0f;
+    const float xr = bf2f(ld_ag_u16(p.x16 + (size_t)b * H + g));
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < MAX_TOPK; ++j)
+      if (j < K) acc = bfr(acc + y[j]);
+    st_ag_u16(p.x16 + (size_t)b * H + g, f2bf(xr + acc));
+  }
+}
+
 // dense MLP (ref_numpy.py:149-152): gate/up + SiLU*up per sequence into h16, then down + residual
 template <class WR, int B, class S, class Wait>
 __device__ __forceinline__ void phase_gateup_b(const Params& p, int layer, S& s, Wait wait) {
@@ -1417,7 +1566,7 @@ __device__ __forceinline__ void fused_body_b(const Params& p) {
   // tiles): the dense projections and the expert gate/up rows in 16-row tiles against up to 16 sequence columns
   constexpr int TB = FP8 ? 1024 : 512;
   constexpr bool TILES = MOE && B >= 8 && H % TB == 0 && KA % TB == 0 && H / TB <= NWAVE && KA / TB <= NWAVE &&
-                        (2 * KM) % 16 == 0;
+                        KM % 256 == 0 && KM <= 4096;
   for (int layer = p.l0; layer < p.l1; ++layer) {
     if constexpr (TILES) {
       if (p.mfma) phase_qkv_mfma<RowOf<FP8, H>, B>(p, layer, s, wait);
@@ -1453,7 +1602,18 @@ __device__ __forceinline__ void fused_body_b(const Params& p) {
       }
       if (s.abort) return;
       grid_arrive(p, k, s);
-      phase_expert_down_b<RowOf<FP8, KM>, B>(p, layer, s, wait);
+      if constexpr (TILES) {
+        if (p.mfma) {
+          phase_expert_down_mfma<RowOf<FP8, KM>, B>(p, layer, s, wait);
+          if (s.abort) return;
+          grid_arrive(p, k, s);
+          phase_combine_mfma<B>(p, s, wait);
+        } else {
+          phase_expert_down_b<RowOf<FP8, KM>, B>(p, layer, s, wait);
+        }
+      } else {
+        phase_expert_down_b<RowOf<FP8, KM>, B>(p, layer, s, wait);
+      }
       if (s.abort) return;
       grid_arrive(p, k, s);
     } else {

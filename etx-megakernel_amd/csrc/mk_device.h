@@ -92,7 +92,9 @@ struct Params {
   int B, nbps, tok_stride;
   int pf;                               // prefill: rows b are positions posb[0] + b of one sequence (btab and
                                         // tokens point at its rows, nbps = tok_stride = 0)
-  int mfma;                             // batched MoE gate/up on the matrix cores (handles of batch capacity >= 8)
+  int mfma;                             // batched projections and experts on the matrix cores (handles of batch
+                                        // capacity >= 8 whose shapes take whole tiles)
+  uint16_t* ys;                         // matrix-core expert down: [pairs][H] weighted outputs, bf16, for the combine
   uint16_t* x16;                        // [B][H] residual, bf16
   uint16_t* o16;                        // [B][NH*HD] attention output, bf16 lane-permuted
   uint16_t* h16;                        // MoE [pairs][MI] / dense [B][I] MLP activations, bf16 lane-permuted

@@ -106,14 +106,6 @@ __device__ __forceinline__ uint8_t f32_to_e4m3(float f) {
   if (e > 8 || (e == 8 && qm > 6)) return (uint8_t)(sign | 0x7E);
   return (uint8_t)(sign | (uint8_t)((e + 7) << 3) | (uint8_t)qm);
 }
-// logical element k of an fp8 row -> its stored byte (blocks of 1024; lane l holds l, l+64, ...)
-__host__ __device__ __forceinline__ int perm_stored8(int k, int K) {
-  const int base = k & ~1023;
-  const int S = (K - base) < 1024 ? (K - base) : 1024;
-  const int m = S >> 6;
-  const int q = k - base;
-  return base + (q & 63) * m + (q >> 6);
-}
 
 // fp8 rows (Fp8Row format: K codes, the fp32 scale, 12 zero bytes) of n_t consecutive tensors of rows x cols, one
 // wave per row: s = amax / 448, q = e4m3(w / s).  The bf16 values come from src (natural rows, one tensor) or, when

@@ -72,6 +72,7 @@ struct SmemD {
   int32_t uexp[MAX_PAIRS];
   int32_t ustart[MAX_PAIRS + 1];
   int32_t nexp;
+  int32_t bpair[B][MAX_TOPK];           // route_all's per-sequence pair lists (unused by these kernels)
   uint32_t kbits[KEY_WORDS];
   uint32_t kpre[KEY_WORDS];
   int32_t abort, last, phase;

@@ -136,6 +136,14 @@ __host__ __device__ __forceinline__ int perm_stored(int k, int K) {    // logica
   const int q = k - base;
   return base + (q & 63) * m + (q >> 6);
 }
+// logical element k of an fp8 row -> its stored byte (blocks of 1024; lane l holds l, l+64, ...)
+__host__ __device__ __forceinline__ int perm_stored8(int k, int K) {
+  const int base = k & ~1023;
+  const int S = (K - base) < 1024 ? (K - base) : 1024;
+  const int m = S >> 6;
+  const int q = k - base;
+  return base + (q & 63) * m + (q >> 6);
+}
 
 // Lane reduction of a wave64 in the fixed order the CPU oracle restates: partner l^1, then l^2 (DPP quad
 // permutes), then the mirror inside 8 lanes and inside 16 lanes (DPP row_half_mirror, row_mirror); each 16-lane row

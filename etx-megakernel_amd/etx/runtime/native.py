@@ -230,6 +230,10 @@ def phase_names(cfg: ModelConfig) -> list[list[str]]:
     else:                                   # batched kernels merge the attention partials in a phase of its own
         att = ["qkv", "attn"] + (["attn_merge"] if cfg.batch > 1 else []) + ["oproj"]
         mlp = ["router", "expert_up", "expert_down"] if cfg.moe else ["gateup", "down"]
+        # handles whose experts run on the matrix cores combine the expert outputs in one more phase (the library's
+        # barrier count says which)
+        if cfg.moe and plan_info(cfg)["barriers_per_step"] == (len(att) + len(mlp) + 1) * cfg.L + 1:
+            mlp = mlp + ["combine"]
         layers = [att + mlp for _ in range(cfg.L)]
     return layers + [["head"]]
 

@@ -440,8 +440,8 @@ typedef struct {
   float *rcos, *rsin;             /* DeepSeek-V2: fp32 yarn tables [max_ctx][qk_rope / 2] */
   float scale;
   float attn_scale;
-  int mfma;                       /* QKV, O and expert gate/up rows in the matrix-core order (batched kernels of
-                                     capacity >= 8) */
+  int mfma;                       /* QKV, O, expert gate/up and down rows in the matrix-core orders (batched kernels
+                                     of capacity >= 8) */
 } orc_model;
 
 static uint16_t* gen_tensor(uint64_t seed, uint64_t stream, size_t n, float scale) {
@@ -484,7 +484,7 @@ EXPORT void* orc_model_create(const orc_config* cfg, uint64_t seed, float wscale
   {
     const int tb = c->wdtype == 1 ? 1024 : 512;
     m->mfma = c->batch >= 8 && c->moe && c->wdtype != 2 && c->H % tb == 0 && c->H / tb <= 8 &&
-              (c->NH * c->HD) % tb == 0 && (c->NH * c->HD) / tb <= 8 && (2 * c->MI) % 16 == 0;
+              (c->NH * c->HD) % tb == 0 && (c->NH * c->HD) / tb <= 8 && c->MI % 256 == 0 && c->MI <= 4096;
   }
   m->nbps = (c->max_ctx + c->block_size - 1) / c->block_size;
   m->nblocks = m->batch * m->nbps;               /* one paged pool shared by the sequences of the batch */
@@ -585,6 +585,8 @@ static void gemv_bf(const uint16_t* W, int R, int K, const float* x, float* out)
 /* one decoder layer at position pos on residual x (in place) of the sequence whose block table is bt;
  * dump_ids / dump_wts / dump_logits optional */
 static float gateup_dot(const orc_model* m, const orc_mat* W, int wdtype, size_t r, const float* x, int K);
+static void down_rows(const orc_model* m, const orc_mat* W2, int wdtype, int H, int MI, const float* h, float w,
+                      float* out);
 static void gemv_rows_tiles(const orc_mat* W, int wdtype, int R, int K, const float* X, int ldx, int n, float* out,
                             int ldo);
 /* a dense projection of one vector: the matrix-core tile order for models whose batched kernel uses it */
@@ -650,9 +652,7 @@ static void layer_step(orc_model* m, int l, float* x, int pos, const int32_t* bt
         const float u = bfr(gateup_dot(m, W13, wt, (size_t)(2 * j + 1), xs, H));
         hk[j] = bfr(bfr(silu(g)) * u);
       }
-      const orc_mat* W2 = &y->w2[ids[k]];
-#pragma omp parallel for schedule(static)
-      for (int i = 0; i < H; ++i) ys[(size_t)k * H + i] = bfr(bfr(mat_dot(W2, wt, (size_t)i, hk, MI)) * wts[k]);
+      down_rows(m, &y->w2[ids[k]], wt, H, MI, hk, wts[k], ys + (size_t)k * H);
     }
     for (int i = 0; i < H; ++i) {                                    /* :146-148 */
       float acc = 0.0f;
@@ -899,6 +899,57 @@ EXPORT float orc_mfma_tile_dot(const float* w, const float* x, int K) {
   free(buf);
   return r;
 }
+/* logical element k of a stored row of K -> its stored position: blocks of blk (512 for bf16 rows, 1024 for e4m3
+ * rows; a last block of 64m gives each lane m), lane l of a block holding l, l + 64, ... (the library's
+ * perm_stored / perm_stored8) */
+static int stored_pos(int k, int K, int blk) {
+  const int base = k & ~(blk - 1), S = K - base < blk ? K - base : blk, m = S >> 6, q = k - base;
+  return base + (q & 63) * m + (q >> 6);
+}
+/* The order of the batched kernels' matrix-core expert down tiles over a row of K (a multiple of 256): the down row's
+ * stored positions ascending, step s giving lane quad q positions 32s + 8q .. + 7 (the pairs' h rows are stored in
+ * the same order).  mfma_split_stored decomposes a row of fp32 values holding bf16 (or e4m3) values into it. */
+static void mfma_split_stored(const float* v, int K, int blk, int16_t* m, int16_t* e) {
+  for (int k = 0; k < K; ++k) {
+    const int o = stored_pos(k, K, blk);
+    bf_split(f2bf(v[k]), m + o, e + o);
+  }
+}
+/* out[i] = bfr(bfr(down row i . h) * w) for rows [0, H): the matrix-core stored order for models whose batched kernel
+ * uses it (m->mfma), else mat_dot */
+static void down_rows(const orc_model* m, const orc_mat* W2, int wdtype, int H, int MI, const float* h, float w,
+                      float* out) {
+  if (!m->mfma) {
+#pragma omp parallel for schedule(static)
+    for (int i = 0; i < H; ++i) out[i] = bfr(bfr(mat_dot(W2, wdtype, (size_t)i, h, MI)) * w);
+    return;
+  }
+  const int blk = wdtype == 1 ? 1024 : 512;
+  int16_t* hsp = (int16_t*)malloc(sizeof(int16_t) * 2 * (size_t)MI);
+  mfma_split_stored(h, MI, blk, hsp, hsp + MI);
+#pragma omp parallel
+  {
+    float* wf = (float*)malloc(sizeof(float) * (size_t)MI);
+    int16_t* wsp = (int16_t*)malloc(sizeof(int16_t) * 2 * (size_t)MI);
+#pragma omp for schedule(static)
+    for (int i = 0; i < H; ++i) {
+      const float sc = row_f32(W2, wdtype, (size_t)i, MI, wf);
+      mfma_split_stored(wf, MI, blk, wsp, wsp + MI);
+      out[i] = bfr(bfr(mfma_dot_split(wsp, wsp + MI, hsp, hsp + MI, MI) * sc) * w);
+    }
+    free(wf); free(wsp);
+  }
+  free(hsp);
+}
+EXPORT float orc_mfma_down_dot(const float* w, const float* h, int K, int blk) {
+  if (K % 256 || (blk != 512 && blk != 1024)) return NAN;
+  int16_t* buf = (int16_t*)malloc(sizeof(int16_t) * 4 * (size_t)K);
+  mfma_split_stored(w, K, blk, buf, buf + K);
+  mfma_split_stored(h, K, blk, buf + 2 * K, buf + 3 * K);
+  const float r = mfma_dot_split(buf, buf + K, buf + 2 * K, buf + 3 * K, K);
+  free(buf);
+  return r;
+}
 /* value of row r for vector x: mat_dot's result, from the row's fp32 image */
 static inline float row_dot(const float* wf, float sc, int wdtype, const float* x, int K) {
   const float d = dot64f(wf, x, K);
@@ -1130,6 +1181,7 @@ static void layer_rows(orc_model* m, int l, float* X, int n, const orc_row* rows
 #pragma omp parallel for schedule(static)
       for (int i = 0; i < n; ++i) mfma_split_row(xs + (size_t)i * H, H, xsp + 2 * (size_t)i * H, xsp + (2 * (size_t)i + 1) * H);
     }
+    int16_t* hsp = m->mfma ? (int16_t*)malloc(sizeof(int16_t) * 2 * (size_t)n * K * MI) : NULL;
 #pragma omp parallel
     {
       float* wg = (float*)malloc(sizeof(float) * (size_t)(H > MI ? H : MI) * 2);
@@ -1161,15 +1213,26 @@ static void layer_rows(orc_model* m, int l, float* X, int n, const orc_row* rows
         }
       }
       free(wsp);
+      if (hsp) {                       /* matrix-core order: each pair's h decomposed once, in the down rows' order */
+#pragma omp for schedule(static)
+        for (int i = 0; i < n * K; ++i)
+          mfma_split_stored(hb + (size_t)i * MI, MI, wt == 1 ? 1024 : 512, hsp + 2 * (size_t)i * MI,
+                            hsp + (2 * (size_t)i + 1) * MI);
+      }
+      int16_t* dsp = hsp ? (int16_t*)malloc(sizeof(int16_t) * 2 * (size_t)MI) : NULL;
 #pragma omp for schedule(dynamic, 16)
       for (int u = 0; u < nu * H; ++u) {                                        /* :146 */
         const int e = used[u / H], r = u % H;
         const float sd = row_f32(&y->w2[e], wt, (size_t)r, MI, wg);
+        if (dsp) mfma_split_stored(wg, MI, wt == 1 ? 1024 : 512, dsp, dsp + MI);
         for (int q = pe[e]; q < pe[e + 1]; ++q) {
           const int i = pr[q];
-          ys[(size_t)i * H + r] = bfr(bfr(row_dot(wg, sd, wt, hb + (size_t)i * MI, MI)) * wts[i]);
+          const float d = dsp ? mfma_dot_split(dsp, dsp + MI, hsp + 2 * (size_t)i * MI, hsp + (2 * (size_t)i + 1) * MI, MI) * sd
+                              : row_dot(wg, sd, wt, hb + (size_t)i * MI, MI);
+          ys[(size_t)i * H + r] = bfr(bfr(d) * wts[i]);
         }
       }
+      free(dsp);
       free(wg);
     }
     for (int b = 0; b < n; ++b) {                                               /* :146-148 ascending expert id */
@@ -1185,7 +1248,7 @@ static void layer_rows(orc_model* m, int l, float* X, int n, const orc_row* rows
         x[i] = bfr(x[i] + acc);
       }
     }
-    free(logits); free(ids); free(wts); free(pe); free(pr); free(fill); free(used); free(xsp); free(hb); free(ys);
+    free(logits); free(ids); free(wts); free(pe); free(pr); free(fill); free(used); free(xsp); free(hsp); free(hb); free(ys);
   } else {                                                                      /* :149-152 */
     const int I = c->I;
     float* hb = (float*)malloc(sizeof(float) * (size_t)n * I);

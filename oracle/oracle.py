@@ -72,6 +72,7 @@ def lib():
             "orc_mfma_bf16_chain": (C.c_float, [C.c_float, u16p, u16p, C.c_int]),
             "orc_mfma_tile_dot": (C.c_float, [f32p, f32p, C.c_int]),
             "orc_mfma_proj_dot": (C.c_float, [f32p, f32p, C.c_int, C.c_int]),
+            "orc_mfma_down_dot": (C.c_float, [f32p, f32p, C.c_int, C.c_int]),
             "orc_e4m3_to_f32": (C.c_float, [C.c_uint8]),
             "orc_f32_to_e4m3": (C.c_uint8, [C.c_float]),
             "orc_quantize_rows": (None, [u16p, C.c_int64, C.c_int, u8p, f32p]),

@@ -126,3 +126,40 @@ def test_projection_dot_is_the_block_chains_summed_as_a_tree(K, fp8):
         differs += np.float32(got) != np.float32(L.orc_mfma_tile_dot(np.ascontiguousarray(w), np.ascontiguousarray(x), K))
     assert nb == 1 or differs > 0
     assert np.isnan(L.orc_mfma_proj_dot(np.zeros(1536, np.float32), np.zeros(1536, np.float32), 1536, 512))
+
+
+def stored_order(K, blk):
+    """logical element at each stored position of a row of K: blocks of blk (512 bf16, 1024 e4m3), a last block of
+    64m giving each lane m, lane l of a block holding l, l + 64, ..."""
+    out = []
+    for base in range(0, K, blk):
+        m = min(blk, K - base) // 64
+        out += [base + l + 64 * j for l in range(64) for j in range(m)]
+    return np.array(out)
+
+
+@pytest.mark.parametrize("K,blk", [(256, 512), (768, 512), (768, 1024), (1536, 1024)])
+def test_down_dot_is_the_chain_over_the_stored_order(K, blk):
+    """orc_mfma_down_dot (the expert down tiles: the row's stored positions in 32-element steps from zero) against
+    the step chain over both operands permuted into the stored order here; the stored order is a permutation, and
+    the chain over the natural order gives other values on some rows."""
+    L = O.lib()
+    order = stored_order(K, blk)
+    assert sorted(order.tolist()) == list(range(K))
+    rng = np.random.default_rng(K + blk)
+    differs = 0
+    for _ in range(20):
+        if blk == 1024:
+            codes = rng.integers(0, 256, K).astype(np.uint8)
+            codes[(codes & 0x7F) == 0x7F] = 0
+            w = np.array([L.orc_e4m3_to_f32(int(c)) for c in codes], np.float32)
+        else:
+            w = O.bf16_bits_to_f32(H.bf16_bits(rng.standard_normal(K) * 0.02))
+        h = O.bf16_bits_to_f32(H.bf16_bits(rng.standard_normal(K)))
+        want = L.orc_mfma_bf16_chain(0.0, H.bf16_bits(w[order]), H.bf16_bits(h[order]), K // 32)
+        got = L.orc_mfma_down_dot(np.ascontiguousarray(w), np.ascontiguousarray(h), K, blk)
+        assert np.float32(got).tobytes() == np.float32(want).tobytes()
+        natural = L.orc_mfma_bf16_chain(0.0, H.bf16_bits(w), H.bf16_bits(h), K // 32)
+        differs += np.float32(got) != np.float32(natural)
+    assert differs > 0
+    assert np.isnan(L.orc_mfma_down_dot(np.zeros(320, np.float32), np.zeros(320, np.float32), 320, 512))
