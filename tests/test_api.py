@@ -87,8 +87,11 @@ def test_plan_records_kernel_grid_and_phases():
     assert ds["barriers_per_step"] == 7 + 8 * 26 + 1 == sum(len(x) for x in ds["phases"])
     assert ds["phases"][0][-2:] == ["gateup", "down"] and ds["phases"][1][-3:] == ["router_shared", "expert_up", "expert_down"]
     b16 = _plan(_wl(configs.QWEN3_30B_A3B), batch=16).report.to_dict()     # a binding overrides the batch
-    assert b16["barriers_per_step"] == 7 * 48 + 1 == sum(len(x) for x in b16["phases"])   # the merge phase
-    assert b16["phases"][0][:4] == ["qkv", "attn", "attn_merge", "oproj"]
+    # the attention merge and (matrix-core experts at batch 16) the expert combine are phases of their own
+    assert b16["barriers_per_step"] == 8 * 48 + 1 == sum(len(x) for x in b16["phases"])
+    assert b16["phases"][0] == ["qkv", "attn", "attn_merge", "oproj", "router", "expert_up", "expert_down", "combine"]
+    b4 = _plan(_wl(configs.QWEN3_30B_A3B), batch=4).report.to_dict()
+    assert b4["barriers_per_step"] == 7 * 48 + 1 and b4["phases"][0][-1] == "expert_down"
     f8 = _plan(_wl(configs.with_layers(configs.QWEN3_30B_A3B, 48, batch=16, wdtype=1)))
     assert f8.report["kernel"] == "etxmk_fused_fp8_b16_h2048_a4096_moe768_e128" and any("fp8" in d for d in f8.decisions)
     un = _plan(_wl(configs.TINY_MOE, fused=False)).report.to_dict()
