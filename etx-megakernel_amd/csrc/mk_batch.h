@@ -117,15 +117,35 @@ __device__ __forceinline__ void build_norm_xb(const Params& p, bool first, const
     if (lane == 0) s.rs[b] = 1.0f / __builtin_sqrtf(acc / (float)H + p.eps);
   }
   __syncthreads();
-  for (int b = b0; b < nb; b += RSTEP) {
-    const float r = s.rs[b];
-    const u32x4 xv = *(const u32x4*)(s.n.xr + b * H + 8 * c);
-    uint16_t* dst = s.n.xs + b * H;
+  if constexpr (H % 512 == 0) {
+    // thread t writes whole 16-byte slots of the lane-permuted rows: slot (b, block, lane l) holds the logical
+    // elements 512 block + l + 64 j, j < 8, read from the natural rows (consecutive lanes read consecutive elements,
+    // write consecutive slots: no LDS bank conflicts; scattered 2-byte writes put 16 lanes on each bank)
+    constexpr int NS = H / 8;                             // slots per row
+    for (int t = threadIdx.x; t < nb * NS; t += NT) {
+      const int b = t / NS, sl = t - b * NS, base = 512 * (sl >> 6), l = sl & 63;
+      const float r = s.rs[b];
+      uint32_t o[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int k = 8 * c + 2 * e;
-      dst[perm_stored(k, H)] = f2bf(bfr(bf_lo(wv[e]) * bfr(bf_lo(xv[e]) * r)));
-      dst[perm_stored(k + 1, H)] = f2bf(bfr(bf_hi(wv[e]) * bfr(bf_hi(xv[e]) * r)));
+      for (int e = 0; e < 4; ++e) {
+        const int k0 = base + l + 64 * (2 * e), k1 = k0 + 64;
+        const float y0 = bfr(bf2f(ld_u16(w + k0)) * bfr(bf2f(s.n.xr[b * H + k0]) * r));
+        const float y1 = bfr(bf2f(ld_u16(w + k1)) * bfr(bf2f(s.n.xr[b * H + k1]) * r));
+        o[e] = (uint32_t)f2bf(y0) | ((uint32_t)f2bf(y1) << 16);
+      }
+      *(u32x4*)(s.n.xs + b * H + 8 * sl) = u32x4{o[0], o[1], o[2], o[3]};
+    }
+  } else {
+    for (int b = b0; b < nb; b += RSTEP) {
+      const float r = s.rs[b];
+      const u32x4 xv = *(const u32x4*)(s.n.xr + b * H + 8 * c);
+      uint16_t* dst = s.n.xs + b * H;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int k = 8 * c + 2 * e;
+        dst[perm_stored(k, H)] = f2bf(bfr(bf_lo(wv[e]) * bfr(bf_lo(xv[e]) * r)));
+        dst[perm_stored(k + 1, H)] = f2bf(bfr(bf_hi(wv[e]) * bfr(bf_hi(xv[e]) * r)));
+      }
     }
   }
   __syncthreads();
@@ -1006,7 +1026,7 @@ __device__ __forceinline__ void phase_expert_up_mfma(const Params& p, int layer,
   const LayerW Lw = layer_w(p, layer);
   const int MI = p.MI, KT = p.TOPK, nb = p.B;
   const uint8_t* W = Lw.w13;
-  build_norm_xb<KK, B>(p, false, Lw.ln2, s);              // x is final since the O projection
+  // the normed rows: left in LDS by the router phase (every workgroup normed them there; nothing since wrote s.n)
   if (!wait()) return;
   route_all<B, EC>(p, s);
   if (blockIdx.x == 0) {
@@ -1213,6 +1233,34 @@ __device__ __forceinline__ void phase_oproj_mfma(const Params& p, int layer, S& 
         copy_rows_lds(p.o16, nb * KK, s.v.xs);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
+        return true;
+      });
+}
+
+// P4 on the matrix cores (p.mfma): tiles of 16 experts' router rows (bf16) against every sequence's post-attention
+// normed row, split by block as the dense projections (E/16 tiles: a few workgroups).  Every workgroup norms the rows
+// in its prologue and keeps them in LDS for the gate/up phase.
+template <int KK, int B, int EC, class S, class Wait>
+__device__ __forceinline__ void phase_router_mfma(const Params& p, int layer, S& s, Wait wait) {
+  using WR = Bf16Row<KK>;                                 // the router stays bf16 in every weight type
+  static_assert(EC % 16 == 0, "whole router tiles");
+  const LayerW Lw = layer_w(p, layer);
+  const int nb = p.B;
+  mfma_tiles_split<WR>(
+      p, s, EC / 16, [&](int t) { return mrow<WR>(Lw.wr, (size_t)16 * t + (lane_id() & 15)); },
+      [&](int, bool& has) -> const uint16_t* {
+        const int r = lane_id() & 15;
+        has = r < nb;
+        return s.n.xs + (size_t)(has ? r : 0) * KK;
+      },
+      [&](int t, const float(&v)[4]) {
+        const int r = lane_id() & 15, q = lane_id() >> 4;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) st_ag(r < nb ? p.logits + (size_t)r * EC + 16 * t + 4 * q + i : sink_of(p), bfr(v[i]));
+      },
+      [&]() {
+        if (!wait()) return false;
+        build_norm_xb<KK, B>(p, false, Lw.ln2, s);
         return true;
       });
 }
@@ -1563,10 +1611,10 @@ __device__ __forceinline__ void fused_body_b(const Params& p) {
   if (p.trace && threadIdx.x == 0) *(MK_G uint64_t*)(p.trace + (size_t)blockIdx.x * 3) = __builtin_amdgcn_s_memrealtime();
   s.phase = 0;
   // the matrix-core forms (p.mfma, set by the host for MoE handles of batch capacity >= 8 whose shapes take whole
-  // tiles): the dense projections and the expert gate/up rows in 16-row tiles against up to 16 sequence columns
+  // tiles): the dense projections, the router and the expert rows in 16-row tiles against up to 16 sequence columns
   constexpr int TB = FP8 ? 1024 : 512;
   constexpr bool TILES = MOE && B >= 8 && H % TB == 0 && KA % TB == 0 && H / TB <= NWAVE && KA / TB <= NWAVE &&
-                        KM % 256 == 0 && KM <= 4096;
+                        H / 512 <= NWAVE && EC % 16 == 0 && KM % 256 == 0 && KM <= 4096;
   for (int layer = p.l0; layer < p.l1; ++layer) {
     if constexpr (TILES) {
       if (p.mfma) phase_qkv_mfma<RowOf<FP8, H>, B>(p, layer, s, wait);
@@ -1591,7 +1639,12 @@ __device__ __forceinline__ void fused_body_b(const Params& p) {
     if (s.abort) return;
     grid_arrive(p, k, s);
     if constexpr (MOE) {
-      phase_router_b<H, B>(p, layer, s, wait);
+      if constexpr (TILES) {
+        if (p.mfma) phase_router_mfma<H, B, EC>(p, layer, s, wait);
+        else phase_router_b<H, B>(p, layer, s, wait);
+      } else {
+        phase_router_b<H, B>(p, layer, s, wait);
+      }
       if (s.abort) return;
       grid_arrive(p, k, s);
       if constexpr (TILES) {

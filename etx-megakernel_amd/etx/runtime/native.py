@@ -52,7 +52,7 @@ class EtxmkConfig(C.Structure):
 
 class EtxmkPlanInfo(C.Structure):
     _fields_ = [("kernel", C.c_char * 96), ("barriers_per_step", C.c_int32), ("threads", C.c_int32),
-                ("batch_capacity", C.c_int32), ("reserved", C.c_int32), ("weight_bytes", C.c_uint64),
+                ("batch_capacity", C.c_int32), ("matrix_cores", C.c_int32), ("weight_bytes", C.c_uint64),
                 ("kv_bytes", C.c_uint64), ("workspace_bytes", C.c_uint64)]
 
 
@@ -216,7 +216,8 @@ def plan_info(cfg: ModelConfig, fused: bool = True) -> dict:
     out = EtxmkPlanInfo()
     _check(L, L.etxmk_plan(C.byref(c), int(fused), C.byref(out)))
     return {"kernel": out.kernel.decode(), "barriers_per_step": int(out.barriers_per_step), "threads": int(out.threads),
-            "batch_capacity": int(out.batch_capacity), "weight_bytes": int(out.weight_bytes),
+            "batch_capacity": int(out.batch_capacity), "matrix_cores": bool(out.matrix_cores),
+            "weight_bytes": int(out.weight_bytes),
             "kv_bytes": int(out.kv_bytes), "workspace_bytes": int(out.workspace_bytes)}
 
 
@@ -230,9 +231,9 @@ def phase_names(cfg: ModelConfig) -> list[list[str]]:
     else:                                   # batched kernels merge the attention partials in a phase of its own
         att = ["qkv", "attn"] + (["attn_merge"] if cfg.batch > 1 else []) + ["oproj"]
         mlp = ["router", "expert_up", "expert_down"] if cfg.moe else ["gateup", "down"]
-        # handles whose experts run on the matrix cores combine the expert outputs in one more phase (the library's
-        # barrier count says which)
-        if cfg.moe and plan_info(cfg)["barriers_per_step"] == (len(att) + len(mlp) + 1) * cfg.L + 1:
+        # handles on the matrix cores combine the expert outputs in a phase of their own (the library's plan says
+        # which)
+        if cfg.moe and plan_info(cfg)["matrix_cores"]:
             mlp = mlp + ["combine"]
         layers = [att + mlp for _ in range(cfg.L)]
     return layers + [["head"]]

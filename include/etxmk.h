@@ -242,7 +242,8 @@ typedef struct etxmk_plan_info {
   int32_t barriers_per_step;
   int32_t threads;
   int32_t batch_capacity;
-  int32_t reserved;
+  int32_t matrix_cores;  // 1: the batched projections and experts run on the matrix cores (phases per layer: qkv,
+                         // attn, attn_merge, oproj, router, expert_up, expert_down, combine)
   uint64_t weight_bytes, kv_bytes, workspace_bytes;
 } etxmk_plan_info;
 int etxmk_plan(const etxmk_config* cfg, int32_t fused, etxmk_plan_info* out);

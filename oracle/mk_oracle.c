@@ -440,8 +440,8 @@ typedef struct {
   float *rcos, *rsin;             /* DeepSeek-V2: fp32 yarn tables [max_ctx][qk_rope / 2] */
   float scale;
   float attn_scale;
-  int mfma;                       /* QKV, O, expert gate/up and down rows in the matrix-core orders (batched kernels
-                                     of capacity >= 8) */
+  int mfma;                       /* QKV, O, router, expert gate/up and down rows in the matrix-core orders (batched
+                                     kernels of capacity >= 8) */
 } orc_model;
 
 static uint16_t* gen_tensor(uint64_t seed, uint64_t stream, size_t n, float scale) {
@@ -484,7 +484,8 @@ EXPORT void* orc_model_create(const orc_config* cfg, uint64_t seed, float wscale
   {
     const int tb = c->wdtype == 1 ? 1024 : 512;
     m->mfma = c->batch >= 8 && c->moe && c->wdtype != 2 && c->H % tb == 0 && c->H / tb <= 8 &&
-              (c->NH * c->HD) % tb == 0 && (c->NH * c->HD) / tb <= 8 && c->MI % 256 == 0 && c->MI <= 4096;
+              (c->NH * c->HD) % tb == 0 && (c->NH * c->HD) / tb <= 8 && c->H / 512 <= 8 && c->E % 16 == 0 &&
+              c->MI % 256 == 0 && c->MI <= 4096;
   }
   m->nbps = (c->max_ctx + c->block_size - 1) / c->block_size;
   m->nblocks = m->batch * m->nbps;               /* one paged pool shared by the sequences of the batch */
@@ -630,7 +631,12 @@ static void layer_step(orc_model* m, int l, float* x, int pos, const int32_t* bt
   if (c->moe) {
     const int E = c->E, K = c->TOPK, MI = c->MI;
     float logits[1024];
-    gemv_bf(y->wr, E, H, xs, logits);                                /* :134 */
+    if (m->mfma) {                                                   /* :134 */
+      const orc_mat wr = {y->wr, NULL, NULL};
+      gemv_rows_tiles(&wr, 0, E, H, xs, H, 1, logits, E);
+    } else {
+      gemv_bf(y->wr, E, H, xs, logits);
+    }
     if (logits_out) memcpy(logits_out, logits, sizeof(float) * (size_t)E);
     int32_t ids[64]; float wts[64];
     route(logits, E, K, c->norm_topk, ids, wts);                     /* :135-140 */
@@ -1154,7 +1160,8 @@ static void layer_rows(orc_model* m, int l, float* X, int n, const orc_row* rows
     const int E = c->E, K = c->TOPK, MI = c->MI;
     float* logits = (float*)malloc(sizeof(float) * (size_t)n * E);
     const orc_mat wr = {y->wr, NULL, NULL};
-    gemv_rows_multi(&wr, 0, E, H, xs, H, n, logits, E);                          /* :134 */
+    if (m->mfma) gemv_rows_tiles(&wr, 0, E, H, xs, H, n, logits, E);            /* :134 */
+    else gemv_rows_multi(&wr, 0, E, H, xs, H, n, logits, E);
     int32_t* ids = (int32_t*)malloc(sizeof(int32_t) * (size_t)n * K);
     float* wts = (float*)malloc(sizeof(float) * (size_t)n * K);
     for (int b = 0; b < n; ++b) {
