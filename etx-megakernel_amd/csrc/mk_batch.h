@@ -26,11 +26,19 @@ constexpr int MAX_PAIRS = MAX_B * MAX_TOPK;
 constexpr int KEY_WORDS = MAX_E * MAX_B / 32;  // routed-pair keys expert * MAX_B + sequence, one bit each
 constexpr int ATTN_CPI_B = 2;           // chunks per attention item in batched kernels
 
+typedef __bf16 mk_bf16x8 __attribute__((ext_vector_type(8)));   // MFMA operands, accumulators
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float mk_f32x4 __attribute__((ext_vector_type(4)));
+
 // LDS of the batched attention phase: two buffers of ATTN_CPI_B chunk tile pairs (the next item's K and V stream in
 // while this item computes); the merge phase's per-wave chunk weights and sums
 struct AttnTilesB {
   u32x4 kt[2][ATTN_CPI_B][HDIM / 8][CHUNK];         // [buffer][chunk][8-dim group][position]
   u32x4 vt[2][ATTN_CPI_B][CHUNK / 8][2][CHUNK];     // [buffer][chunk][8-position group][dim half][dim in half]
+  // wave j's roped q (dims in order) and its chunks' probabilities (positions in order), read back by the whole wave
+  // at one address (an LDS broadcast) as the wave-uniform operands of the score and P.V chains
+  alignas(16) float qb[NWAVE][HDIM];
+  alignas(16) float pb[NWAVE][ATTN_CPI_B][CHUNK];
 };
 struct AttnMergeB {
   float p[NWAVE][2 * MAX_CHUNKS];
@@ -508,7 +516,6 @@ __device__ __forceinline__ void phase_attn_b(const Params& p, int layer, S& s, W
   const float kn0 = bf2f(ld_u16(Lw.kn + lane)), kn1 = bf2f(ld_u16(Lw.kn + lane + 64));
   if ((int)blockIdx.x < nitems) load_kv(blockIdx.x, 0, kv_blocks(blockIdx.x));
   if (!wait()) return;
-  auto bcast = [](float v, int l) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l)); };
   int k = 0;
   for (int item = blockIdx.x; item < nitems; item += p.nwg, ++k) {
     const int buf = k & 1;
@@ -582,25 +589,31 @@ __device__ __forceinline__ void phase_attn_b(const Params& p, int layer, S& s, W
     __syncthreads();
     if (more) load_kv(item + p.nwg, buf ^ 1, nkb);
     if (j < G) {
-      // scores (:126), lane = position: both chunks' chains over ascending d, each broadcast q value feeding both;
-      // the K reads run a block of GB dim groups ahead.  With one chunk the second chain reads stale LDS, unused.
+      // scores (:126), lane = position: both chunks' chains over ascending d, each q value (an LDS broadcast read)
+      // feeding both; the K and q reads run a block of GB dim groups ahead.  With one chunk the second chain reads
+      // stale LDS, unused.
       constexpr int GB = 2, NB = HDIM / 8 / GB;
+      float* qw = s.a.qb[j];
+      qw[lane] = q0;
+      qw[lane + 64] = q1;
       float acc0 = 0.0f, acc1 = 0.0f;
       u32x4 kA[2][GB], kB[2][GB];
-      auto ldk = [&](u32x4(&kk)[2][GB], int blk) {
+      mk_f32x4 qA[GB][2], qB[GB][2];
+      auto ldk = [&](u32x4(&kk)[2][GB], mk_f32x4(&qq)[GB][2], int blk) {
 #pragma unroll
         for (int u = 0; u < GB; ++u) {
           kk[0][u] = s.a.kt[buf][0][blk * GB + u][lane];
           kk[1][u] = s.a.kt[buf][1][blk * GB + u][lane];
+          qq[u][0] = *(const mk_f32x4*)(qw + 8 * (blk * GB + u));
+          qq[u][1] = *(const mk_f32x4*)(qw + 8 * (blk * GB + u) + 4);
         }
       };
-      auto fmk = [&](const u32x4(&kk)[2][GB], int blk) {
+      auto fmk = [&](const u32x4(&kk)[2][GB], const mk_f32x4(&qq)[GB][2]) {
 #pragma unroll
         for (int u = 0; u < GB; ++u) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const int d = 8 * (blk * GB + u) + 2 * e;
-            const float qa = bcast(d < 64 ? q0 : q1, d & 63), qb = bcast(d + 1 < 64 ? q0 : q1, (d + 1) & 63);
+            const float qa = qq[u][e >> 1][2 * (e & 1)], qb = qq[u][e >> 1][2 * (e & 1) + 1];   // dims d, d + 1
             acc0 = __builtin_fmaf(qa, bf_lo(kk[0][u][e]), acc0);
             acc1 = __builtin_fmaf(qa, bf_lo(kk[1][u][e]), acc1);
             acc0 = __builtin_fmaf(qb, bf_hi(kk[0][u][e]), acc0);
@@ -608,13 +621,13 @@ __device__ __forceinline__ void phase_attn_b(const Params& p, int layer, S& s, W
           }
         }
       };
-      ldk(kA, 0);
+      ldk(kA, qA, 0);
 #pragma unroll
       for (int blk = 0; blk < NB; blk += 2) {
-        ldk(kB, blk + 1);
-        fmk(kA, blk);
-        if (blk + 2 < NB) ldk(kA, blk + 2);
-        fmk(kB, blk + 1);
+        ldk(kB, qB, blk + 1);
+        fmk(kA, qA);
+        if (blk + 2 < NB) ldk(kA, qA, blk + 2);
+        fmk(kB, qB);
       }
       const int len0 = min(CHUNK, n - c0 * CHUNK), len1 = nc > 1 ? min(CHUNK, n - (c0 + 1) * CHUNK) : 0;
       const float sc0 = lane < len0 ? acc0 * p.attn_scale : -__builtin_huge_valf();
@@ -622,21 +635,30 @@ __device__ __forceinline__ void phase_attn_b(const Params& p, int layer, S& s, W
       const float m0 = wave_max(sc0), m1 = wave_max(sc1);
       const float pr0 = lane < len0 ? expf_mk(sc0 - m0) : 0.0f;
       const float pr1 = lane < len1 ? expf_mk(sc1 - m1) : 0.0f;
+      float* pw0 = s.a.pb[j][0];
+      float* pw1 = s.a.pb[j][1];
+      pw0[lane] = pr0;                                    // read back as LDS broadcasts by the P.V chains
+      pw1[lane] = pr1;
       // V (:127-128), lanes = dims (lane, lane + 64): a = sum_t p_t v_t[d] and l = sum_t p_t over ascending t
       float a[2][2] = {{0.0f, 0.0f}, {0.0f, 0.0f}}, l[2] = {0.0f, 0.0f};
       auto vat = [](const u32x4& w, int e) { return (e & 1) ? bf_hi(w[e >> 1]) : bf_lo(w[e >> 1]); };
       if (len1 == CHUNK) {                                // two full chunks: both chains together, reads ahead
         u32x4 vA[4], vB[4];
-        auto ldv = [&](u32x4(&v)[4], int hb) {
+        mk_f32x4 pA[4], pB[4];                               // positions 8 hb .. + 7 of chunk 0 (0, 1), chunk 1 (2, 3)
+        auto ldv = [&](u32x4(&v)[4], mk_f32x4(&pp)[4], int hb) {
           v[0] = s.a.vt[buf][0][hb][0][lane];
           v[1] = s.a.vt[buf][0][hb][1][lane];
           v[2] = s.a.vt[buf][1][hb][0][lane];
           v[3] = s.a.vt[buf][1][hb][1][lane];
+          pp[0] = *(const mk_f32x4*)(pw0 + 8 * hb);
+          pp[1] = *(const mk_f32x4*)(pw0 + 8 * hb + 4);
+          pp[2] = *(const mk_f32x4*)(pw1 + 8 * hb);
+          pp[3] = *(const mk_f32x4*)(pw1 + 8 * hb + 4);
         };
-        auto fmv = [&](const u32x4(&v)[4], int hb) {
+        auto fmv = [&](const u32x4(&v)[4], const mk_f32x4(&pp)[4]) {
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
-            const float p0 = bcast(pr0, hb * 8 + e), p1 = bcast(pr1, hb * 8 + e);
+            const float p0 = pp[e >> 2][e & 3], p1 = pp[2 + (e >> 2)][e & 3];
             a[0][0] = __builtin_fmaf(p0, vat(v[0], e), a[0][0]);
             a[0][1] = __builtin_fmaf(p0, vat(v[1], e), a[0][1]);
             l[0] = l[0] + p0;
@@ -645,25 +667,26 @@ __device__ __forceinline__ void phase_attn_b(const Params& p, int layer, S& s, W
             l[1] = l[1] + p1;
           }
         };
-        ldv(vA, 0);
+        ldv(vA, pA, 0);
 #pragma unroll
         for (int hb = 0; hb < CHUNK / 8; hb += 2) {
-          ldv(vB, hb + 1);
-          fmv(vA, hb);
-          if (hb + 2 < CHUNK / 8) ldv(vA, hb + 2);
-          fmv(vB, hb + 1);
+          ldv(vB, pB, hb + 1);
+          fmv(vA, pA);
+          if (hb + 2 < CHUNK / 8) ldv(vA, pA, hb + 2);
+          fmv(vB, pB);
         }
       } else {                                            // a partial last chunk: one chunk at a time
 #pragma unroll
         for (int ci = 0; ci < CPI; ++ci) {
           const int len = ci == 0 ? len0 : len1;
-          const float pr = ci == 0 ? pr0 : pr1;
+          const float* pwc = ci == 0 ? pw0 : pw1;
           for (int hb = 0; hb < CHUNK / 8 && hb * 8 < len; ++hb) {
             const u32x4 w0 = s.a.vt[buf][ci][hb][0][lane], w1 = s.a.vt[buf][ci][hb][1][lane];
+            const mk_f32x4 pl = *(const mk_f32x4*)(pwc + 8 * hb), ph = *(const mk_f32x4*)(pwc + 8 * hb + 4);
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
               if (hb * 8 + e < len) {
-                const float pt = bcast(pr, hb * 8 + e);
+                const float pt = e < 4 ? pl[e] : ph[e - 4];
                 a[ci][0] = __builtin_fmaf(pt, vat(w0, e), a[ci][0]);
                 a[ci][1] = __builtin_fmaf(pt, vat(w1, e), a[ci][1]);
                 l[ci] = l[ci] + pt;
@@ -917,9 +940,6 @@ __device__ __forceinline__ void phase_expert_up_b(const Params& p, int layer, S&
 // mfma_bf16_k32).  Two register buffers alternate: the next block's loads are issued before this block's MFMAs; past
 // the wave's last block the issue reads the wave's sink line, so every issue is the same run of loads.  D's lane holds
 // rows 4q .. 4q + 3 of one sequence, two whole gate/up pairs: SiLU * up is formed in the lane.
-typedef __bf16 mk_bf16x8 __attribute__((ext_vector_type(8)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-typedef float mk_f32x4 __attribute__((ext_vector_type(4)));
 
 // codes 8h .. 8h + 7 of a 16-code e4m3 slot as 8 bf16 (exact: every e4m3 value is a bf16 value)
 __device__ __forceinline__ mk_bf16x8 e4m3_half_bf16(const u32x4& c, int h) {
