@@ -213,12 +213,12 @@ const char* kernel_symbol(const etxmk_config& c, int* cap) {
 }
 
 // The matrix-core rule: MoE Qwen3 handles of batch capacity >= 8 whose shapes take whole tiles run their batched
-// QKV, O projection, router, expert gate/up and expert down on the matrix cores (the down outputs combined in a phase
-// of their own).  The CPU oracle applies the same rule to the models of such handles.
+// QKV, O projection, router, expert gate/up, expert down and lm_head on the matrix cores (the down outputs combined
+// in a phase of their own).  The CPU oracle applies the same rule to the models of such handles.
 bool mfma_rule(const etxmk_config& c) {
   const int tb = c.wdtype == ETXMK_W_FP8 ? 1024 : 512, ka = c.NH * c.HD;
   return c.arch == ETXMK_ARCH_QWEN3 && c.batch >= 8 && c.moe && c.H % tb == 0 && c.H / tb <= NWAVE && ka % tb == 0 &&
-         ka / tb <= NWAVE && c.H / 512 <= NWAVE && c.E % 16 == 0 && c.MI % 256 == 0 && c.MI <= 4096;
+         ka / tb <= NWAVE && c.H / 512 <= NWAVE && c.E % 16 == 0 && c.MI % 256 == 0 && c.MI <= 4096 && c.V % 16 == 0;
 }
 
 // grid barriers of a launch over layers [l0, l1) (plus the head), one per phase; `batched`: the batched kernel

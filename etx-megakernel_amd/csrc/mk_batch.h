@@ -1603,6 +1603,52 @@ __device__ __forceinline__ void phase_head_b(const Params& p, S& s, Wait wait) {
     __hip_atomic_fetch_max(p.amax + 32 * lane_id(), best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// P7 on the matrix cores (p.mfma): 16-row tiles of the lm_head (bf16) against every sequence's final normed row,
+// each tile's 4 blocks chained as the expert gate/up tiles; lane l keeps the best key of its sequence l % 16 over
+// its rows, the four quads of a column are folded, and one atomic per (wave, sequence) publishes it
+template <int KK, int B, class S, class Wait>
+__device__ __forceinline__ void phase_head_mfma(const Params& p, S& s, Wait wait) {
+  using WR = Bf16Row<KK>;                                 // lm_head stays bf16 in every weight type
+  const int nb = p.B;
+  const uint8_t* W = (const uint8_t*)p.lm_head;
+  uint64_t best = 0;
+  const bool ran = mfma_tiles<WR>(
+      p, p.V / 16, [&](int t) { return mrow<WR>(W, (size_t)16 * t + (lane_id() & 15)); },
+      [&](int, bool& has) -> const uint16_t* {
+        const int r = lane_id() & 15;
+        has = r < nb;
+        return s.n.xs + (size_t)(has ? r : 0) * KK;
+      },
+      [&](int t, const float(&v)[4]) {
+        const int r = lane_id() & 15, q = lane_id() >> 4;
+        if (r < nb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const uint64_t key = argmax_key(bfr(v[i]), 16 * t + 4 * q + i);
+            best = key > best ? key : best;
+          }
+      },
+      [&]() {
+        if (!wait()) return false;
+        build_norm_xb<KK, B>(p, false, p.final_norm, s);
+        if (blockIdx.x == 0 && p.dump_x)
+          for (int i = threadIdx.x; i < nb * KK; i += NT)
+            st_f(p.dump_x + (size_t)(p.l1 - 1) * nb * KK + i, bf2f(s.n.xr[i]));
+        return true;
+      },
+      s.phase);
+  if (!ran) return;
+#pragma unroll
+  for (int m = 16; m < 64; m <<= 1) {                     // fold the quads: lanes r, r + 16, r + 32, r + 48
+    const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)best, m, 64);
+    const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(best >> 32), m, 64);
+    const uint64_t o = ((uint64_t)hi << 32) | lo;
+    best = o > best ? o : best;
+  }
+  if (lane_id() < nb && best)
+    __hip_atomic_fetch_max(p.amax + 32 * lane_id(), best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 template <class Wait>
 __device__ __forceinline__ void phase_token_b(const Params& p, Wait wait) {
   if (!wait()) return;
@@ -1631,7 +1677,8 @@ __device__ __forceinline__ void fused_body_b(const Params& p) {
   if (p.trace && threadIdx.x == 0) *(MK_G uint64_t*)(p.trace + (size_t)blockIdx.x * 3) = __builtin_amdgcn_s_memrealtime();
   s.phase = 0;
   // the matrix-core forms (p.mfma, set by the host for MoE handles of batch capacity >= 8 whose shapes take whole
-  // tiles): the dense projections, the router and the expert rows in 16-row tiles against up to 16 sequence columns
+  // tiles): the dense projections, the router, the expert rows and the lm_head in 16-row tiles against up to 16
+  // sequence columns
   constexpr int TB = FP8 ? 1024 : 512;
   constexpr bool TILES = MOE && B >= 8 && H % TB == 0 && KA % TB == 0 && H / TB <= NWAVE && KA / TB <= NWAVE &&
                         H / 512 <= NWAVE && EC % 16 == 0 && KM % 256 == 0 && KM <= 4096;
@@ -1699,7 +1746,12 @@ __device__ __forceinline__ void fused_body_b(const Params& p) {
     }
   }
   if (p.do_head) {
-    phase_head_b<H, B>(p, s, wait);
+    if constexpr (TILES) {
+      if (p.mfma) phase_head_mfma<H, B>(p, s, wait);
+      else phase_head_b<H, B>(p, s, wait);
+    } else {
+      phase_head_b<H, B>(p, s, wait);
+    }
     if (s.abort) return;
     grid_arrive(p, k, s);
     phase_token_b(p, wait);

@@ -440,8 +440,8 @@ typedef struct {
   float *rcos, *rsin;             /* DeepSeek-V2: fp32 yarn tables [max_ctx][qk_rope / 2] */
   float scale;
   float attn_scale;
-  int mfma;                       /* QKV, O, router, expert gate/up and down rows in the matrix-core orders (batched
-                                     kernels of capacity >= 8) */
+  int mfma;                       /* QKV, O, router, expert gate/up and down and lm_head rows in the matrix-core
+                                     orders (batched kernels of capacity >= 8) */
 } orc_model;
 
 static uint16_t* gen_tensor(uint64_t seed, uint64_t stream, size_t n, float scale) {
@@ -485,7 +485,7 @@ EXPORT void* orc_model_create(const orc_config* cfg, uint64_t seed, float wscale
     const int tb = c->wdtype == 1 ? 1024 : 512;
     m->mfma = c->batch >= 8 && c->moe && c->wdtype != 2 && c->H % tb == 0 && c->H / tb <= 8 &&
               (c->NH * c->HD) % tb == 0 && (c->NH * c->HD) / tb <= 8 && c->H / 512 <= 8 && c->E % 16 == 0 &&
-              c->MI % 256 == 0 && c->MI <= 4096;
+              c->MI % 256 == 0 && c->MI <= 4096 && c->V % 16 == 0;
   }
   m->nbps = (c->max_ctx + c->block_size - 1) / c->block_size;
   m->nblocks = m->batch * m->nbps;               /* one paged pool shared by the sequences of the batch */
@@ -1352,24 +1352,36 @@ EXPORT int orc_step_rows(void* h, int n, const int32_t* seqs, const int32_t* tok
   const int nt = omp_get_max_threads();
   float* bv = (float*)malloc(sizeof(float) * (size_t)nt * n);
   int* bi = (int*)malloc(sizeof(int) * (size_t)nt * n);
+  int16_t* xsp = NULL;                             /* matrix-core order: the rows' vectors decomposed once */
+  if (m->mfma) {
+    xsp = (int16_t*)malloc(sizeof(int16_t) * 2 * (size_t)n * H);
+    for (int b = 0; b < n; ++b) mfma_split_row(xs + (size_t)b * H, H, xsp + 2 * (size_t)b * H, xsp + (2 * (size_t)b + 1) * H);
+  }
 #pragma omp parallel
   {
     const int tid = omp_get_thread_num(), nth = omp_get_num_threads();
     float* wf = (float*)malloc(sizeof(float) * (size_t)H * ORC_TR);
+    int16_t* wsp = xsp ? (int16_t*)malloc(sizeof(int16_t) * 2 * (size_t)H * ORC_TR) : NULL;
     for (int b = 0; b < n; ++b) { bv[(size_t)tid * n + b] = -INFINITY; bi[(size_t)tid * n + b] = -1; }
     const int r0 = (int)((int64_t)V * tid / nth), r1 = (int)((int64_t)V * (tid + 1) / nth);
     const orc_mat lm = {m->lm_head, NULL, NULL};
     for (int rt = r0; rt < r1; rt += ORC_TR) {                                  /* :157-158 */
       const int nr = r1 - rt < ORC_TR ? r1 - rt : ORC_TR;
-      for (int i = 0; i < nr; ++i) row_f32(&lm, 0, (size_t)(rt + i), H, wf + (size_t)i * H);
+      for (int i = 0; i < nr; ++i) {
+        row_f32(&lm, 0, (size_t)(rt + i), H, wf + (size_t)i * H);
+        if (wsp) mfma_split_row(wf + (size_t)i * H, H, wsp + 2 * (size_t)i * H, wsp + (2 * (size_t)i + 1) * H);
+      }
       for (int b = 0; b < n; ++b)
         for (int i = 0; i < nr; ++i) {                /* rows ascending within the thread's range */
-          const float v = bfr(dot64f(wf + (size_t)i * H, xs + (size_t)b * H, H));
+          const float v = wsp ? bfr(mfma_dot_split(wsp + 2 * (size_t)i * H, wsp + (2 * (size_t)i + 1) * H,
+                                                   xsp + 2 * (size_t)b * H, xsp + (2 * (size_t)b + 1) * H, H))
+                              : bfr(dot64f(wf + (size_t)i * H, xs + (size_t)b * H, H));
           if (bi[(size_t)tid * n + b] < 0 || v > bv[(size_t)tid * n + b]) { bv[(size_t)tid * n + b] = v; bi[(size_t)tid * n + b] = rt + i; }
         }
     }
-    free(wf);
+    free(wf); free(wsp);
   }
+  free(xsp);
   for (int b = 0; b < n; ++b) {                    /* threads hold ascending row ranges: the first maximum wins */
     int best = -1; float v = -INFINITY;
     for (int t = 0; t < nt; ++t) {
@@ -1415,7 +1427,13 @@ EXPORT int32_t orc_step_seq(void* h, int seq, int32_t tok, int pos, float* dump_
   rmsnorm(x, NULL, H, c->eps, xs);                                  /* :155 final norm (weight 1.0) */
   const int V = c->V;
   float* lg = (float*)malloc(sizeof(float) * (size_t)V);
-  gemv_bf(m->lm_head, V, H, xs, lg);                                 /* :157 */
+  if (m->mfma) {                                                     /* :157 */
+    const orc_mat lm = {m->lm_head, NULL, NULL};
+#pragma omp parallel for schedule(static)
+    for (int v = 0; v < V; ++v) lg[v] = bfr(gateup_dot(m, &lm, 0, (size_t)v, xs, H));
+  } else {
+    gemv_bf(m->lm_head, V, H, xs, lg);
+  }
   int best = 0;
   for (int v = 1; v < V; ++v) if (lg[v] > lg[best]) best = v;        /* :158 first maximum */
   free(x); free(xs); free(lg);
