@@ -268,10 +268,18 @@ def calibrate(dev) -> dict:
     got = calib.word_sum(sink)
     if got != want:
         raise RuntimeError(f"stream calibration read {got:#x}, words sum to {want:#x}")
+    # the matrix-core tiles' pattern over the same words: 16 rows of 2064 bytes (an fp8 row of 2048 codes and its
+    # scale), two 1 KiB blocks of each row, 64 bytes of each of 16 rows per load
+    tiles = []
+    for inflight in (1, 2):
+        calib.stream_tiles(src, 2064, 2, inflight, cus)
+        t, used, _ = min((calib.stream_tiles(src, 2064, 2, inflight, cus) for _ in range(3)), key=lambda r: r[0])
+        tiles.append({"blocks_in_flight_per_wave": inflight, "GBps": round(used / t / 1e9, 1)})
+        log(f"[gpu] tile stream, {inflight} x 16 KiB per wave in flight: {tiles[-1]['GBps']} GB/s")
     del src, sink
     return {"calibration": "gfx950 grid barrier and streaming read", "cus": cus,
             "barrier_us": round(best, 3), "barriers_per_launch": iters, "stream_bytes": nbytes,
-            "stream": rows, "stream_checksum_ok": True,
+            "stream": rows, "stream_checksum_ok": True, "tile_stream": tiles,
             "kernels": "etx-megakernel_amd/csrc/mk_calib.hip (grid_arrive/grid_wait of mk_device.h)"}
 
 

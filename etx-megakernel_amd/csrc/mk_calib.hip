@@ -49,6 +49,36 @@ __global__ __launch_bounds__(NT) void calib_stream(const u32x4* src, size_t nchu
   sink[(size_t)blockIdx.x * NT + threadIdx.x] = acc;
 }
 
+// the matrix-core tiles' load pattern: wave w reads tiles of 16 consecutive rows (row_bytes apart), a tile's rows
+// in blocks of 1024 bytes; one block is 16 loads per lane, lane (r = l % 16, q = l / 16) taking row r's bytes
+// 16 q + 64 i of the block, i < 16 (64 bytes of every row per load, the other 64 of each 128-byte line in the next);
+// INF blocks in flight
+template <int INF>
+__global__ __launch_bounds__(NT) void calib_stream_tiles(const uint8_t* src, int ntile, int nblk, int row_bytes,
+                                                         uint32_t* sink) {
+  const int W = gridDim.x * NWAVE, w = blockIdx.x * NWAVE + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, r = lane & 15, q = lane >> 4;
+  const int nitem = (w < ntile ? (ntile - 1 - w) / W + 1 : 0) * nblk;
+  uint32_t acc = 0;
+  for (int it0 = 0; it0 < nitem; it0 += INF) {
+    u32x4 v[INF][16];
+#pragma unroll
+    for (int j = 0; j < INF; ++j) {
+      const int it = it0 + j;
+      const bool ok = it < nitem;
+      const int t = w + (it / nblk) * W, blk = it % nblk;
+      const uint8_t* base = src + ((size_t)16 * t + r) * row_bytes + 1024 * blk + 16 * q;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) v[j][i] = ok ? *(const u32x4*)(base + 64 * i) : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int j = 0; j < INF; ++j)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc += v[j][i].x + v[j][i].y + v[j][i].z + v[j][i].w;
+  }
+  sink[(size_t)blockIdx.x * NT + threadIdx.x] = acc;
+}
+
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
@@ -116,6 +146,24 @@ int etxmk_calib_stream(const void* src, size_t bytes, int inflight, int nwg, uin
     case 4: hipLaunchKernelGGL(calib_stream<4>, dim3(nwg), dim3(NT), 0, st, s, nchunk, sink); break;
     case 8: hipLaunchKernelGGL(calib_stream<8>, dim3(nwg), dim3(NT), 0, st, s, nchunk, sink); break;
     case 16: hipLaunchKernelGGL(calib_stream<16>, dim3(nwg), dim3(NT), 0, st, s, nchunk, sink); break;
+    default: return (int)hipErrorInvalidValue;
+  }
+  return (int)hipGetLastError();
+}
+
+// one read of ntile tiles of 16 rows (row_bytes apart, nblk blocks of 1024 bytes each) with the matrix-core tiles'
+// load pattern, inflight (1 or 2) blocks of 16 KB per wave in flight, nwg workgroups of 512 threads; sink as above
+int etxmk_calib_stream_tiles(const void* src, int ntile, int nblk, int row_bytes, int inflight, int nwg, uint32_t* sink,
+                             void* stream) {
+  using namespace mk;
+  if (!src || !sink || nwg < 1 || ntile < 1 || nblk < 1 || row_bytes < 1024 * nblk || row_bytes % 16 ||
+      ((uintptr_t)src & 15) != 0)
+    return (int)hipErrorInvalidValue;
+  const uint8_t* s = (const uint8_t*)src;
+  hipStream_t st = (hipStream_t)stream;
+  switch (inflight) {
+    case 1: hipLaunchKernelGGL(calib_stream_tiles<1>, dim3(nwg), dim3(NT), 0, st, s, ntile, nblk, row_bytes, sink); break;
+    case 2: hipLaunchKernelGGL(calib_stream_tiles<2>, dim3(nwg), dim3(NT), 0, st, s, ntile, nblk, row_bytes, sink); break;
     default: return (int)hipErrorInvalidValue;
   }
   return (int)hipGetLastError();

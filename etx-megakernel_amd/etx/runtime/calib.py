@@ -25,6 +25,8 @@ def load():
         lib.etxmk_calib_stream.restype = C.c_int
         lib.etxmk_calib_mfma_bf16.argtypes = [C.c_void_p] * 4 + [C.c_int, C.c_int, C.c_void_p]
         lib.etxmk_calib_mfma_bf16.restype = C.c_int
+        lib.etxmk_calib_stream_tiles.argtypes = [C.c_void_p] + [C.c_int] * 5 + [C.c_void_p, C.c_void_p]
+        lib.etxmk_calib_stream_tiles.restype = C.c_int
         _lib = lib
     return _lib
 
@@ -71,6 +73,28 @@ def stream(src, inflight: int, nwg: int):
     e1.record(st)
     e1.synchronize()
     return e0.elapsed_time(e1) * 1e-3, sink
+
+
+def stream_tiles(src, row_bytes: int, nblk: int, inflight: int, nwg: int):
+    """One read of the device tensor `src` as tiles of 16 rows of `row_bytes` (nblk blocks of 1024 bytes each) with
+    the matrix-core tiles' load pattern (a load: 64 bytes of each of 16 rows), 1 or 2 blocks of 16 KB per wave in
+    flight.  Returns (seconds, the bytes of the blocks read, the per-thread sums of the words read)."""
+    import torch
+    lib = load()
+    dev = src.device
+    nbytes = src.numel() * src.element_size()
+    ntile = nbytes // (16 * row_bytes)
+    sink = torch.empty(nwg * 512, dtype=torch.int32, device=dev)
+    st = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    rc = lib.etxmk_calib_stream_tiles(C.c_void_p(src.data_ptr()), int(ntile), int(nblk), int(row_bytes), int(inflight),
+                                      int(nwg), C.c_void_p(sink.data_ptr()), _stream(torch, dev))
+    if rc != 0:
+        raise RuntimeError(f"etxmk_calib_stream_tiles: HIP error {rc}")
+    e1.record(st)
+    e1.synchronize()
+    return e0.elapsed_time(e1) * 1e-3, ntile * 16 * nblk * 1024, sink
 
 
 def word_sum(t) -> int:

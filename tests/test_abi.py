@@ -21,6 +21,7 @@ def test_calibration_library_exports():
     from etx.runtime import calib
     lib = calib.load()                                     # loads without a GPU; nothing is launched
     assert hasattr(lib, "etxmk_calib_barrier") and hasattr(lib, "etxmk_calib_stream")
+    assert hasattr(lib, "etxmk_calib_stream_tiles") and hasattr(lib, "etxmk_calib_mfma_bf16")
 
 
 def test_sizes_of_real_configurations():

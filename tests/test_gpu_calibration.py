@@ -49,3 +49,22 @@ def test_stream_reads_every_word_once(gpu, inflight):
     assert secs > 0
     with pytest.raises(RuntimeError, match="HIP error"):
         calib.stream(src, 3, cus)                          # not one of the built depths
+
+
+@pytest.mark.parametrize("inflight", [1, 2])
+def test_tile_stream_reads_every_block_word_once(gpu, inflight):
+    """The tiles' pattern reads the 16 rows' first nblk KiB each exactly once: the sinks add up to the sum of those
+    words (a tile count that is not a multiple of the waves leaves some waves with fewer tiles)."""
+    import torch
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    row_bytes, nblk, ntile = 2064, 2, 3 * cus * 8 + 5
+    g = torch.Generator(device="cuda:0").manual_seed(10 + inflight)
+    src = torch.randint(-2**31, 2**31 - 1, (ntile * 16 * row_bytes // 4,), dtype=torch.int32, device="cuda:0",
+                        generator=g)
+    say(f"[gpu] calibration tile stream: {ntile} tiles, {inflight} in flight")
+    secs, used, sink = calib.stream_tiles(src, row_bytes, nblk, inflight, cus)
+    assert used == ntile * 16 * nblk * 1024 and secs > 0
+    blocks = src.view(ntile * 16, row_bytes // 4)[:, : nblk * 256]
+    assert calib.word_sum(sink) == calib.word_sum(blocks.contiguous())
+    with pytest.raises(RuntimeError, match="HIP error"):
+        calib.stream_tiles(src, row_bytes, nblk, 3, cus)   # not one of the built depths
