@@ -3,7 +3,11 @@
 // paged-KV block table and token row.  The phases are those of the single-sequence kernel (mk_device.h); every
 // weight row streams from HBM once per step and is dotted with the input vectors of every sequence that needs it.
 // Per (row, sequence) the arithmetic is the single-sequence dot in the same order, so a batched step equals B
-// single-sequence steps bit for bit.
+// single-sequence steps bit for bit.  Handles of batch capacity >= 8 whose shapes take whole tiles (Params.mfma, the
+// host's matrix-core rule) run the dense projections, the router, the experts and the lm_head instead as tiles of 16
+// weight rows against up to 16 sequence columns on v_mfma_f32_16x16x32_bf16: each (row, sequence) value is then the
+// matrix-core chain in a fixed order (per form below), the same for every column, so a batched step still equals B
+// single steps of the CPU oracle stated with the same rule.
 //
 // Reference path: examples/vllm_llm/host.hip:126-1159 and examples/vllm_llm/vl_tiles.hip:1-95 (per-request
 // parameters, block tables, slot mapping, greedy argmax), with examples/llm/ref_numpy.py:105-158 per sequence.
@@ -14,7 +18,10 @@
 //   o16     [B][NH*HD] bf16   attention output, lane-permuted: the O projection copies rows straight into LDS
 //   logits  [B][E] fp32       router logits
 //   h16     MoE [pairs][MI] / dense [B][I] bf16, lane-permuted; MoE rows are the routed (sequence, slot) pairs in
-//           pair order (ascending expert, then sequence)
+//           pair order (ascending expert, then sequence); with the matrix cores and fp8 weights, in the fp8 rows'
+//           stored order (blocks of 1024) that the down tiles chain over
+//   ys      [pairs][H] bf16   matrix-core expert down: each pair's weighted outputs, added per sequence by the
+//           combine phase
 // Cross-workgroup values are written with agent-scope stores and read with agent-scope loads (sc1), as in the
 // single-sequence kernel.
 #include "mk_device.h"
