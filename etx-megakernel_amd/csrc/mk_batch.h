@@ -950,18 +950,15 @@ __device__ __forceinline__ void phase_expert_up_b(const Params& p, int layer, S&
 
 // codes 8h .. 8h + 7 of a 16-code e4m3 slot as 8 bf16 (exact: every e4m3 value is a bf16 value)
 __device__ __forceinline__ mk_bf16x8 e4m3_half_bf16(const u32x4& c, int h) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
   u32x4 o;
 #pragma unroll
   for (int d = 0; d < 2; ++d) {
     const uint32_t w = c[2 * h + d];
-    // codes 0, 1 and 2, 3 of the word as fp32, taken as bits whole (a bit cast of one element of the conversion's
-    // 2-vector compiled to a copy of element 0)
-    const u32x2 lo = __builtin_bit_cast(u32x2, __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false));
-    const u32x2 hi = __builtin_bit_cast(u32x2, __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true));
-    // the upper halves of two fp32 values (their exact bf16 bits) into one word: bytes 2, 3 of the first, then
-    // bytes 2, 3 of the second (v_perm_b32 selector 0x07060302 over {second, first})
-    o[2 * d] = __builtin_amdgcn_perm(lo[1], lo[0], 0x07060302u);
-    o[2 * d + 1] = __builtin_amdgcn_perm(hi[1], hi[0], 0x07060302u);
+    // gfx950's v_cvt_scalef32_pk_bf16_fp8 at scale 1: codes 0, 1 (then 2, 3) of the word to a bf16 pair, low half
+    // first; every e4m3 value is a bf16 value, so the conversion is exact
+    o[2 * d] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)w, 1.0f, false));
+    o[2 * d + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)w, 1.0f, true));
   }
   return __builtin_bit_cast(mk_bf16x8, o);
 }
