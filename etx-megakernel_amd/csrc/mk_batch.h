@@ -54,6 +54,7 @@ struct AttnMergeB {
 template <int B>
 struct SmemB {
   static constexpr int NCAP = B * MAX_H > 32768 ? 32768 : B * MAX_H;    // B * H of the norm phases
+  static constexpr bool NORM_HOIST = true;              // build_norm_xb loads a thread's weights once
   static constexpr int XCAP = B * MAX_K > 65536 ? 65536 : B * MAX_K;    // input rows of the other GEMVs
   union {
     struct {
@@ -111,6 +112,17 @@ __device__ __forceinline__ void build_norm_xb(const Params& p, bool first, const
   const int nb = p.B, lane = lane_id(), wave = wave_u();
   const int c = (int)threadIdx.x % C8, b0 = (int)threadIdx.x / C8;
   const u32x4 wv = ld16(w + 8 * c);
+  constexpr int NS = H / 8;
+  // slot form (H a multiple of 512) with whole rows of slots per workgroup: thread t writes slot t % NS of every
+  // row, so its 8 weights are loaded once, with the row copy, instead of once per row after it (8 more live VGPRs
+  // across the copy: layouts whose kernels are short of registers set NORM_HOIST false and keep the per-row loads)
+  constexpr bool FIXED = S::NORM_HOIST && H % 512 == 0 && NT % NS == 0;
+  uint16_t wk[8];
+  if constexpr (FIXED) {
+    const int sl = (int)threadIdx.x % NS, base = 512 * (sl >> 6), l = sl & 63;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) wk[j] = ld_u16(w + base + l + 64 * j);
+  }
   if (first) {
     for (int q = threadIdx.x; q < nb * C8; q += NT) {
       const int b = q / C8, qq = q - b * C8;
@@ -136,16 +148,16 @@ __device__ __forceinline__ void build_norm_xb(const Params& p, bool first, const
     // thread t writes whole 16-byte slots of the lane-permuted rows: slot (b, block, lane l) holds the logical
     // elements 512 block + l + 64 j, j < 8, read from the natural rows (consecutive lanes read consecutive elements,
     // write consecutive slots: no LDS bank conflicts; scattered 2-byte writes put 16 lanes on each bank)
-    constexpr int NS = H / 8;                             // slots per row
-    for (int t = threadIdx.x; t < nb * NS; t += NT) {
+    for (int t = threadIdx.x; t < nb * NS; t += NT) {    // NS slots per row
       const int b = t / NS, sl = t - b * NS, base = 512 * (sl >> 6), l = sl & 63;
       const float r = s.rs[b];
       uint32_t o[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int k0 = base + l + 64 * (2 * e), k1 = k0 + 64;
-        const float y0 = bfr(bf2f(ld_u16(w + k0)) * bfr(bf2f(s.n.xr[b * H + k0]) * r));
-        const float y1 = bfr(bf2f(ld_u16(w + k1)) * bfr(bf2f(s.n.xr[b * H + k1]) * r));
+        const float w0 = bf2f(FIXED ? wk[2 * e] : ld_u16(w + k0)), w1 = bf2f(FIXED ? wk[2 * e + 1] : ld_u16(w + k1));
+        const float y0 = bfr(w0 * bfr(bf2f(s.n.xr[b * H + k0]) * r));
+        const float y1 = bfr(w1 * bfr(bf2f(s.n.xr[b * H + k1]) * r));
         o[e] = (uint32_t)f2bf(y0) | ((uint32_t)f2bf(y1) << 16);
       }
       *(u32x4*)(s.n.xs + b * H + 8 * sl) = u32x4{o[0], o[1], o[2], o[3]};

@@ -49,6 +49,7 @@ struct MlaTiles {
 template <int B, int XC>
 struct SmemD {
   static constexpr int NCAP = B * MAX_H > 32768 ? 32768 : B * MAX_H;
+  static constexpr bool NORM_HOIST = false;             // per-row weight loads in build_norm_xb (registers)
   static constexpr int XCAP = XC;
   union {
     struct {
