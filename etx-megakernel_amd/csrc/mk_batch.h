@@ -1266,7 +1266,8 @@ __device__ __forceinline__ void phase_oproj_mfma(const Params& p, int layer, S& 
       },
       [&]() {
         if (!wait()) return false;
-        copy_rows_lds(p.o16, nb * KK, s.v.xs);
+        // tile t is workgroup t % nwg's: with H / 16 tiles on more workgroups, the rest have none and copy nothing
+        if ((int)blockIdx.x < H / 16) copy_rows_lds(p.o16, nb * KK, s.v.xs);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
         return true;
